@@ -1,0 +1,227 @@
+// Row-wise epilogues around the routed MoE output: gated shared-expert
+// combine, combine + residual + RMSNorm (direct and inverse-row), residual
+// add + RMSNorm, and the bf16 SwiGLU of the shared expert input.
+//
+// One workgroup (256 threads) per row; 4 contiguous bf16 per thread access
+// (8-byte loads).  Rounding points follow the reference kernels exactly; the
+// single-rounding bf16 FMA is evaluated as an exact fp64 fma followed by one
+// round-to-nearest-even to bf16.
+#include <math.h>
+
+#include "common.h"
+#include "status.h"
+
+namespace d3 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxPerThread = 32;  // width <= 8192
+
+__device__ __forceinline__ void load4(const uint16_t* p, float v[4]) {
+  const uint2 raw = *reinterpret_cast<const uint2*>(p);
+  v[0] = __uint_as_float(raw.x << 16);
+  v[1] = __uint_as_float(raw.x & 0xffff0000u);
+  v[2] = __uint_as_float(raw.y << 16);
+  v[3] = __uint_as_float(raw.y & 0xffff0000u);
+}
+
+__device__ __forceinline__ void store4(uint16_t* p, const float v[4]) {
+  const uint32_t lo = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+  const uint32_t hi = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+  *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// bf16(sigmoid(fp32 gate)) (kernels.py:434-438).
+__device__ __forceinline__ float gate_bf16(const uint16_t* gate, int64_t stride, int row) {
+  const float g = bf16_to_f32(gate[static_cast<int64_t>(row) * stride]);
+  return round_bf16(1.0f / (1.0f + expf(-g)));
+}
+
+// Single rounding of a*b + c to bf16 for bf16 operands: the fp64 fma is exact
+// unless the operands differ by more than ~2^37 in magnitude.
+__device__ __forceinline__ float fma_bf16(float a, float b, float c) {
+  const double exact = fma(static_cast<double>(a), static_cast<double>(b), static_cast<double>(c));
+  const uint64_t bits = static_cast<uint64_t>(__double_as_longlong(exact));
+  const uint64_t mag = bits & 0x7fffffffffffffffull;
+  if (mag == 0) return static_cast<float>(exact);
+  uint64_t kept = mag >> 45;
+  const uint64_t rest = mag & ((1ull << 45) - 1);
+  const uint64_t half = 1ull << 44;
+  kept += (rest > half) || (rest == half && (kept & 1));
+  const int64_t exponent = static_cast<int64_t>(kept >> 7) - 1023 + 127;
+  if (exponent <= 0 || exponent >= 255) return round_bf16(static_cast<float>(exact));
+  const uint32_t out = (static_cast<uint32_t>(bits >> 63) << 31) |
+                       (static_cast<uint32_t>(exponent) << 23) |
+                       (static_cast<uint32_t>(kept & 0x7f) << 16);
+  return __uint_as_float(out);
+}
+
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  v = segment_sum<kWave>(v);
+  const int wave = threadIdx.x / kWave;
+  if (lane_id() == 0) scratch[wave] = v;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kThreads / kWave; ++w) total += scratch[w];
+  return total;
+}
+
+__global__ __launch_bounds__(kThreads) void combine_experts_kernel(
+    const uint16_t* __restrict__ routed, const uint16_t* __restrict__ shared,
+    const uint16_t* __restrict__ gate, int64_t gate_stride, int width,
+    uint16_t* __restrict__ out) {
+  const int row = blockIdx.x;
+  const float g = gate_bf16(gate, gate_stride, row);
+  const int64_t base = static_cast<int64_t>(row) * width;
+  for (int column = threadIdx.x * 4; column < width; column += kThreads * 4) {
+    float r[4], s[4], v[4];
+    load4(routed + base + column, r);
+    load4(shared + base + column, s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = r[i] + round_bf16(s[i] * g);
+    store4(out + base + column, v);
+  }
+}
+
+// kMode 0: add_norm(x, residual); 1: combine_experts_add_norm(_inverse).
+template <int kMode>
+__global__ __launch_bounds__(kThreads) void add_norm_kernel(
+    const uint16_t* __restrict__ routed, const uint16_t* __restrict__ shared,
+    const uint16_t* __restrict__ gate, int64_t gate_stride, const int64_t* __restrict__ inverse,
+    uint16_t* __restrict__ residual, const uint16_t* __restrict__ weight, float eps, int width,
+    uint16_t* __restrict__ out) {
+  __shared__ float scratch[kThreads / kWave];
+  const int row = blockIdx.x;
+  const int source = inverse != nullptr ? static_cast<int>(inverse[row]) : row;
+  const int64_t src = static_cast<int64_t>(source) * width;
+  const int64_t dst = static_cast<int64_t>(row) * width;
+  float g = 0.0f;
+  if constexpr (kMode == 1) g = gate_bf16(gate, gate_stride, source);
+  float values[kMaxPerThread];
+  float squares = 0.0f;
+  int count = 0;
+  for (int column = threadIdx.x * 4; column < width; column += kThreads * 4, count += 4) {
+    float r[4], res[4], v[4];
+    load4(routed + src + column, r);
+    load4(residual + dst + column, res);
+    if constexpr (kMode == 1) {
+      float s[4];
+      load4(shared + src + column, s);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = round_bf16(fma_bf16(s[i], g, r[i]) + res[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = round_bf16(r[i] + res[i]);
+    }
+    store4(residual + dst + column, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      values[count + i] = v[i];
+      squares += v[i] * v[i];
+    }
+  }
+  const float total = block_sum(squares, scratch);
+  const float inv = 1.0f / sqrtf(total / static_cast<float>(width) + eps);
+  count = 0;
+  for (int column = threadIdx.x * 4; column < width; column += kThreads * 4, count += 4) {
+    float w[4], v[4];
+    load4(weight + column, w);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = values[count + i] * inv * (1.0f + w[i]);
+    store4(out + dst + column, v);
+  }
+}
+
+// silu_mul (kernels.py:386-395): bf16(bf16(g * sigmoid(g)) * u).
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ x,
+                                                            int64_t stride, int width,
+                                                            uint16_t* __restrict__ out) {
+  const int row = blockIdx.x;
+  const uint16_t* in = x + static_cast<int64_t>(row) * stride;
+  for (int column = threadIdx.x * 4; column < width; column += kThreads * 4) {
+    float g[4], u[4], v[4];
+    load4(in + column, g);
+    load4(in + width + column, u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = round_bf16(g[i] * (1.0f / (1.0f + expf(-g[i])))) * u[i];
+    store4(out + static_cast<int64_t>(row) * width + column, v);
+  }
+}
+
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+}  // namespace
+}  // namespace d3
+
+using namespace d3;
+
+extern "C" int d3_combine_experts(const uint16_t* routed, const uint16_t* shared,
+                                  const uint16_t* gate, int64_t gate_stride, int32_t rows,
+                                  int32_t width, uint16_t* out, void* stream) {
+  D3_REQUIRE(routed && shared && gate && out, "combine_experts: null pointer");
+  D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0, "combine_experts: width %% 4 != 0");
+  D3_REQUIRE(aligned8(routed) && aligned8(shared) && aligned8(out), "combine_experts: alignment");
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  hipLaunchKernelGGL(combine_experts_kernel, dim3(rows), dim3(kThreads), 0, as_stream(stream),
+                     routed, shared, gate, gate_stride, width, out);
+  D3_LAUNCHED("combine_experts");
+}
+
+extern "C" int d3_combine_experts_add_norm(const uint16_t* routed, const uint16_t* shared,
+                                           const uint16_t* gate, int64_t gate_stride,
+                                           const int64_t* inverse, uint16_t* residual,
+                                           const uint16_t* weight, float eps, int32_t rows,
+                                           int32_t width, uint16_t* out, void* stream) {
+  D3_REQUIRE(routed && shared && gate && residual && weight && out,
+             "combine_experts_add_norm: null pointer");
+  D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0 && width <= kThreads * kMaxPerThread,
+             "combine_experts_add_norm: width %d must be a multiple of 4 and <= 8192", width);
+  D3_REQUIRE(aligned8(routed) && aligned8(shared) && aligned8(residual) && aligned8(out) &&
+                 aligned8(weight),
+             "combine_experts_add_norm: alignment");
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  hipLaunchKernelGGL(add_norm_kernel<1>, dim3(rows), dim3(kThreads), 0, as_stream(stream), routed,
+                     shared, gate, gate_stride, inverse, residual, weight, eps, width, out);
+  D3_LAUNCHED("combine_experts_add_norm");
+}
+
+extern "C" int d3_add_norm(const uint16_t* x, uint16_t* residual, const uint16_t* weight, float eps,
+                           int32_t rows, int32_t width, uint16_t* out, void* stream) {
+  D3_REQUIRE(x && residual && weight && out, "add_norm: null pointer");
+  D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0 && width <= kThreads * kMaxPerThread,
+             "add_norm: width %d must be a multiple of 4 and <= 8192", width);
+  D3_REQUIRE(aligned8(x) && aligned8(residual) && aligned8(out) && aligned8(weight),
+             "add_norm: alignment");
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  hipLaunchKernelGGL(add_norm_kernel<0>, dim3(rows), dim3(kThreads), 0, as_stream(stream), x,
+                     nullptr, nullptr, 0, nullptr, residual, weight, eps, width, out);
+  D3_LAUNCHED("add_norm");
+}
+
+extern "C" int d3_silu_mul(const uint16_t* projected, int64_t row_stride, int32_t rows,
+                           int32_t width, uint16_t* out, void* stream) {
+  D3_REQUIRE(projected && out, "silu_mul: null pointer");
+  D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0 && row_stride >= 2 * width &&
+                 row_stride % 4 == 0,
+             "silu_mul: bad shape");
+  D3_REQUIRE(aligned8(projected) && aligned8(out), "silu_mul: alignment");
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(rows), dim3(kThreads), 0, as_stream(stream), projected,
+                     row_stride, width, out);
+  D3_LAUNCHED("silu_mul");
+}

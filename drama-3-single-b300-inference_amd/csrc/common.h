@@ -1,0 +1,126 @@
+// Device helpers shared by the MoE kernels (gfx950, wave64).
+//
+// Numeric conventions follow the reference (src/drama3/kernels.py,
+// moe_input.py): bf16 activations, OCP FP8 e4m3fn ("fn": no infinities,
+// max finite 448) weights and quantised activations, fp32 block scales.
+// Conversions are exact bit manipulations so that quantised bytes match a
+// CPU restatement bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace d3 {
+
+constexpr int kWave = 64;
+constexpr int kGroup = 128;  // FP8 block size along every contracted dimension
+
+// ---------------------------------------------------------------------------
+// bf16
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((b >> 16) | 0x40u);
+  return static_cast<uint16_t>((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+// ---------------------------------------------------------------------------
+// OCP e4m3fn
+// ---------------------------------------------------------------------------
+// float -> e4m3fn code, round to nearest even.  Magnitudes >= 464 and NaN
+// give the NaN code 0x7f (torch's float8_e4m3fn conversion); the MoE path
+// clamps to +-448 first so it never produces NaN.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  const uint32_t b = __float_as_uint(f);
+  const uint32_t sign = (b >> 24) & 0x80u;
+  const uint32_t mag = b & 0x7fffffffu;
+  uint32_t code;
+  if (mag >= 0x43e80000u) {
+    code = 0x7fu;
+  } else if (mag < 0x3c800000u) {
+    // Below the smallest normal 2^-6: value = m * 2^-9, m in [0, 8].
+    // Scaling by 512 is exact; rint rounds half to even.
+    code = static_cast<uint32_t>(__builtin_rintf(__uint_as_float(mag) * 512.0f));
+  } else {
+    uint32_t shifted = (((mag >> 23) - 120u) << 3) | ((mag >> 20) & 7u);
+    const uint32_t rest = mag & 0xfffffu;
+    shifted += (rest > 0x80000u) || (rest == 0x80000u && (shifted & 1u));
+    code = shifted;
+  }
+  return code | sign;
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t code) {
+  const uint32_t sign = (code & 0x80u) << 24;
+  const uint32_t exponent = (code >> 3) & 0xfu;
+  const uint32_t mantissa = code & 7u;
+  float mag;
+  if (exponent == 0) {
+    mag = static_cast<float>(mantissa) * (1.0f / 512.0f);
+  } else if (exponent == 15 && mantissa == 7) {
+    mag = __uint_as_float(0x7fc00000u);
+  } else {
+    mag = __uint_as_float(((exponent + 120u) << 23) | (mantissa << 20));
+  }
+  return __uint_as_float(__float_as_uint(mag) | sign);
+}
+
+// Per-128 group quantisation rule of the reference (moe_input.py:24-27):
+// scale = max(amax, 1e-10) / 448 and q = e4m3(clamp(x / scale, -448, 448)),
+// with IEEE fp32 division.
+__device__ __forceinline__ float group_scale(float amax) {
+  return fmaxf(amax, 1e-10f) / 448.0f;
+}
+
+__device__ __forceinline__ uint32_t quantize_one(float x, float scale) {
+  const float v = fminf(fmaxf(x / scale, -448.0f), 448.0f);
+  return f32_to_e4m3(v);
+}
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------
+template <int WIDTH>
+__device__ __forceinline__ float segment_max(float v) {
+#pragma unroll
+  for (int offset = WIDTH / 2; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset));
+  return v;
+}
+
+template <int WIDTH>
+__device__ __forceinline__ float segment_sum(float v) {
+#pragma unroll
+  for (int offset = WIDTH / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    const uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), offset));
+    v = v > other ? v : other;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int lane = lane_id();
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Row count visible to graph-captured kernels: a device scalar when given,
+// otherwise the host capacity.
+__device__ __forceinline__ int live_rows(const int32_t* count, int capacity) {
+  if (count == nullptr) return capacity;
+  const int n = *count;
+  return n < capacity ? (n < 0 ? 0 : n) : capacity;
+}
+
+}  // namespace d3

@@ -1,0 +1,312 @@
+// Front end of the MoE step: active-slot compaction, top-k routing and
+// per-128 FP8 activation quantisation.
+//
+// All three are row-parallel integer / byte work: one wavefront per row (or
+// one workgroup for the compaction), coalesced 16-byte loads, wave64 ballots
+// and shuffles instead of LDS round trips.
+#include <math.h>
+
+#include "common.h"
+#include "status.h"
+
+namespace d3 {
+namespace {
+
+constexpr int kFrontThreads = 256;  // 4 waves, one row each
+constexpr int kCompactThreads = 1024;
+
+// ---------------------------------------------------------------------------
+// Active-slot compaction: ballot + popcount per wave, wave offsets in LDS.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kCompactThreads) void compact_slots_kernel(
+    const uint8_t* __restrict__ occupancy, int num_slots, int32_t* __restrict__ active,
+    int32_t* __restrict__ count) {
+  __shared__ int wave_counts[kCompactThreads / kWave];
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  int base = 0;
+  for (int start = 0; start < num_slots; start += kCompactThreads) {
+    const int slot = start + static_cast<int>(threadIdx.x);
+    const bool live = slot < num_slots && occupancy[slot] != 0;
+    const uint64_t mask = __ballot(live);
+    if (lane == 0) wave_counts[wave] = __popcll(mask);
+    __syncthreads();
+    int offset = base;
+    int chunk = 0;
+    for (int w = 0; w < kCompactThreads / kWave; ++w) {
+      offset += w < wave ? wave_counts[w] : 0;
+      chunk += wave_counts[w];
+    }
+    if (live) active[offset + __popcll(mask & lanemask_lt())] = slot;
+    base += chunk;
+    __syncthreads();
+  }
+  for (int i = base + static_cast<int>(threadIdx.x); i < num_slots; i += kCompactThreads)
+    active[i] = -1;
+  if (threadIdx.x == 0) *count = base;
+}
+
+// ---------------------------------------------------------------------------
+// Routing: one wave per row, NPL logits per lane (E <= 64 * NPL).
+// ---------------------------------------------------------------------------
+template <bool kF32>
+__device__ __forceinline__ float load_logit(const void* row, int column) {
+  if constexpr (kF32) return static_cast<const float*>(row)[column];
+  return bf16_to_f32(static_cast<const uint16_t*>(row)[column]);
+}
+
+// route_kernel's ranking key (kernels.py:364-368): the order-preserving
+// unsigned image of the fp32 bits, truncated to its bf16 half, with
+// 65535 - column below it so equal values rank the lower expert first.
+__device__ __forceinline__ uint32_t route_key(float value, int column) {
+  const uint32_t bits = __float_as_uint(value);
+  const uint32_t ordered = bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+  return (ordered & 0xffff0000u) | (65535u - static_cast<uint32_t>(column));
+}
+
+template <int NPL, bool kF32>
+__global__ __launch_bounds__(kFrontThreads) void route_kernel(
+    const void* __restrict__ logits, int64_t stride, int rows, int num_experts, int top_k,
+    const int32_t* __restrict__ row_index, const int32_t* __restrict__ row_count,
+    int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, void* __restrict__ weights,
+    int weights_f32) {
+  const int row = (blockIdx.x * kFrontThreads + threadIdx.x) / kWave;
+  const int lane = lane_id();
+  if (row >= live_rows(row_count, rows)) return;  // uniform per wave
+  const int source = row_index != nullptr ? row_index[row] : row;
+  const char* base = static_cast<const char*>(logits) +
+                     static_cast<int64_t>(source) * stride * (kF32 ? 4 : 2);
+
+  float values[NPL];
+  uint32_t keys[NPL];
+  float row_max = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int column = lane + j * kWave;
+    if (column < num_experts) {
+      values[j] = load_logit<kF32>(base, column);
+      keys[j] = route_key(values[j], column);
+      row_max = fmaxf(row_max, values[j]);
+    } else {
+      values[j] = -INFINITY;
+      keys[j] = 0u;  // below every valid key (65535 - column > 0)
+    }
+  }
+  row_max = segment_max<kWave>(row_max);
+  float denominator = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) denominator += expf(values[j] - row_max);
+  denominator = segment_sum<kWave>(denominator);
+
+  // Top-k by repeated wave arg-max over unique keys; lane k keeps rank k.
+  int selected = -1;
+  for (int k = 0; k < top_k; ++k) {
+    uint32_t best = 0u;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) best = keys[j] > best ? keys[j] : best;
+    best = wave_max_u32(best);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) keys[j] = keys[j] == best ? 0u : keys[j];
+    if (lane == k) selected = 65535 - static_cast<int>(best & 0xffffu);
+  }
+  float probability = 0.0f;
+  if (lane < top_k) probability = expf(load_logit<kF32>(base, selected) - row_max) / denominator;
+  const float total = segment_sum<kWave>(probability);
+  if (lane < top_k) {
+    const int64_t out = static_cast<int64_t>(row) * top_k + lane;
+    const float weight = probability / total;
+    if (ids32 != nullptr) ids32[out] = selected;
+    if (ids64 != nullptr) ids64[out] = selected;
+    if (weights_f32)
+      static_cast<float*>(weights)[out] = weight;
+    else
+      static_cast<uint16_t*>(weights)[out] = f32_to_bf16(weight);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Quantisation: one wave per row; 8 elements per lane, 16 lanes per group.
+// ---------------------------------------------------------------------------
+template <bool kPrepare>
+__global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
+    const uint16_t* __restrict__ x, int64_t stride, int rows, int width,
+    const int32_t* __restrict__ row_index, const int32_t* __restrict__ row_count,
+    uint8_t* __restrict__ q, float* __restrict__ scales, int transposed,
+    // prepare_moe_input extras
+    const void* __restrict__ router, int router_f32, int64_t router_stride, int num_experts,
+    const void* __restrict__ row_slots, int row_slots_i64, int64_t padding_start,
+    float* __restrict__ logits_out) {
+  const int row = (blockIdx.x * kFrontThreads + threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int live = live_rows(row_count, rows);
+  if (row >= live) return;
+  const int source = row_index != nullptr ? row_index[row] : row;
+  const uint16_t* in = x + static_cast<int64_t>(source) * stride;
+  uint8_t* out = q + static_cast<int64_t>(row) * width;
+  const int groups = width / kGroup;
+  for (int base = 0; base < width; base += 8 * kWave) {
+    const int column = base + lane * 8;
+    const bool inside = column < width;  // whole 16-lane groups agree
+    uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+    if (inside) raw = *reinterpret_cast<const uint4*>(in + column);
+    const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+    float v[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(words[i] << 16);
+      v[2 * i + 1] = __uint_as_float(words[i] & 0xffff0000u);
+      amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
+    }
+    amax = segment_max<16>(amax);
+    const float scale = group_scale(amax);
+    uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo |= quantize_one(v[i], scale) << (8 * i);
+      hi |= quantize_one(v[i + 4], scale) << (8 * i);
+    }
+    if (inside) {
+      *reinterpret_cast<uint2*>(out + column) = make_uint2(lo, hi);
+      if ((lane & 15) == 0) {
+        const int group = column / kGroup;
+        if (transposed)
+          scales[static_cast<int64_t>(group) * rows + row] = scale;
+        else
+          scales[static_cast<int64_t>(row) * groups + group] = scale;
+      }
+    }
+  }
+  if constexpr (kPrepare) {
+    // Reserved padding rows reuse row 0's routing (moe_input.py:31-37).
+    int router_row = row;
+    if (row_slots != nullptr) {
+      const int64_t slot = row_slots_i64 ? static_cast<const int64_t*>(row_slots)[row]
+                                         : static_cast<const int32_t*>(row_slots)[row];
+      if (slot >= padding_start) router_row = 0;
+    }
+    const char* src = static_cast<const char*>(router) +
+                      static_cast<int64_t>(router_row) * router_stride * (router_f32 ? 4 : 2);
+    for (int column = lane; column < num_experts; column += kWave) {
+      const float value = router_f32 ? reinterpret_cast<const float*>(src)[column]
+                                     : bf16_to_f32(reinterpret_cast<const uint16_t*>(src)[column]);
+      logits_out[static_cast<int64_t>(row) * num_experts + column] = value;
+    }
+  }
+}
+
+inline int wave_blocks(int rows) { return (rows + kFrontThreads / kWave - 1) / (kFrontThreads / kWave); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace d3
+
+using namespace d3;
+
+extern "C" int d3_compact_slots(const uint8_t* occupancy, int32_t num_slots, int32_t* active_slots,
+                                int32_t* count, void* stream) {
+  D3_REQUIRE(occupancy && active_slots && count, "compact_slots: null pointer");
+  D3_REQUIRE(num_slots > 0 && num_slots <= (1 << 20), "compact_slots: num_slots out of range");
+  hipLaunchKernelGGL(compact_slots_kernel, dim3(1), dim3(kCompactThreads), 0, as_stream(stream),
+                     occupancy, num_slots, active_slots, count);
+  D3_LAUNCHED("compact_slots");
+}
+
+extern "C" int d3_route(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                        int32_t rows, int32_t num_experts, int32_t top_k,
+                        const int32_t* row_index, const int32_t* row_count, int32_t* ids32,
+                        int64_t* ids64, void* weights, int32_t weights_dtype, void* stream) {
+  D3_REQUIRE(logits && weights, "route: null logits or weights");
+  D3_REQUIRE(ids32 || ids64, "route: need ids32 or ids64");
+  D3_REQUIRE(logits_dtype == D3_DTYPE_BF16 || logits_dtype == D3_DTYPE_F32,
+             "route: logits must be bf16 or f32");
+  D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
+             "route: weights must be bf16 or f32");
+  D3_REQUIRE(rows >= 0, "route: negative rows");
+  D3_SUPPORTED(num_experts >= 1 && num_experts <= 512, "route: num_experts %d not in [1, 512]",
+               num_experts);
+  D3_REQUIRE(top_k >= 1 && top_k <= 16 && top_k <= num_experts, "route: bad top_k %d", top_k);
+  D3_REQUIRE(logits_row_stride >= num_experts, "route: row stride smaller than num_experts");
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  const bool f32 = logits_dtype == D3_DTYPE_F32;
+  const int wf32 = weights_dtype == D3_DTYPE_F32;
+  const dim3 grid(wave_blocks(rows)), block(kFrontThreads);
+  hipStream_t s = as_stream(stream);
+#define D3_ROUTE_LAUNCH(NPL)                                                                   \
+  if (f32)                                                                                     \
+    hipLaunchKernelGGL((route_kernel<NPL, true>), grid, block, 0, s, logits, logits_row_stride, \
+                       rows, num_experts, top_k, row_index, row_count, ids32, ids64, weights,  \
+                       wf32);                                                                  \
+  else                                                                                         \
+    hipLaunchKernelGGL((route_kernel<NPL, false>), grid, block, 0, s, logits,                  \
+                       logits_row_stride, rows, num_experts, top_k, row_index, row_count,      \
+                       ids32, ids64, weights, wf32);
+  if (num_experts <= 64) {
+    D3_ROUTE_LAUNCH(1)
+  } else if (num_experts <= 128) {
+    D3_ROUTE_LAUNCH(2)
+  } else if (num_experts <= 256) {
+    D3_ROUTE_LAUNCH(4)
+  } else {
+    D3_ROUTE_LAUNCH(8)
+  }
+#undef D3_ROUTE_LAUNCH
+  D3_LAUNCHED("route");
+}
+
+extern "C" int d3_quantize_rows(const uint16_t* x, int64_t x_row_stride, int32_t rows,
+                                int32_t width, const int32_t* row_index,
+                                const int32_t* row_count, uint8_t* q, float* scales,
+                                int32_t scales_transposed, void* stream) {
+  D3_REQUIRE(x && q && scales, "quantize_rows: null pointer");
+  D3_REQUIRE(rows >= 0 && width > 0 && width % kGroup == 0,
+             "quantize_rows: width %d must be a positive multiple of 128", width);
+  D3_REQUIRE(x_row_stride >= width && x_row_stride % 8 == 0 && aligned16(x),
+             "quantize_rows: x rows must be 16-byte aligned (stride %% 8 == 0)");
+  D3_REQUIRE(aligned16(q), "quantize_rows: q must be 16-byte aligned");
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  hipLaunchKernelGGL(quantize_kernel<false>, dim3(wave_blocks(rows)), dim3(kFrontThreads), 0,
+                     as_stream(stream), x, x_row_stride, rows, width, row_index, row_count, q,
+                     scales, scales_transposed ? 1 : 0, nullptr, 0, 0, 0, nullptr, 0, 0,
+                     nullptr);
+  D3_LAUNCHED("quantize_rows");
+}
+
+extern "C" int d3_prepare_moe_input(const uint16_t* x, int64_t x_row_stride, const void* router,
+                                    int32_t router_dtype, int64_t router_row_stride,
+                                    int32_t rows, int32_t hidden, int32_t num_experts,
+                                    const void* row_slots, int32_t row_slots_dtype,
+                                    int64_t padding_start, uint8_t* q, float* scales,
+                                    float* logits, void* stream) {
+  D3_REQUIRE(x && router && q && scales && logits, "prepare_moe_input: null pointer");
+  D3_REQUIRE(rows >= 0 && hidden > 0 && hidden % kGroup == 0,
+             "prepare_moe_input: hidden %d must be a positive multiple of 128", hidden);
+  D3_REQUIRE(num_experts > 0 && router_row_stride >= num_experts,
+             "prepare_moe_input: bad router shape");
+  D3_REQUIRE(router_dtype == D3_DTYPE_BF16 || router_dtype == D3_DTYPE_F32,
+             "prepare_moe_input: router must be bf16 or f32");
+  D3_REQUIRE(x_row_stride >= hidden && x_row_stride % 8 == 0 && aligned16(x) && aligned16(q),
+             "prepare_moe_input: x rows must be 16-byte aligned");
+  if (row_slots != nullptr) {
+    D3_REQUIRE(row_slots_dtype == D3_DTYPE_I32 || row_slots_dtype == D3_DTYPE_I64,
+               "prepare_moe_input: row_slots must be int32 or int64");
+    D3_REQUIRE(padding_start > 0, "prepare_moe_input: padding_start must be positive");
+  }
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  hipLaunchKernelGGL(quantize_kernel<true>, dim3(wave_blocks(rows)), dim3(kFrontThreads), 0,
+                     as_stream(stream), x, x_row_stride, rows, hidden, nullptr, nullptr, q,
+                     scales, 1, router, router_dtype == D3_DTYPE_F32 ? 1 : 0, router_row_stride,
+                     num_experts, row_slots, row_slots_dtype == D3_DTYPE_I64 ? 1 : 0,
+                     padding_start, logits);
+  D3_LAUNCHED("prepare_moe_input");
+}

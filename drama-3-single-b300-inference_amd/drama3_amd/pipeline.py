@@ -1,0 +1,243 @@
+"""The packed FP8 top-k MoE step as a chain of C-ABI launches.
+
+``MoEWorkspace`` owns every intermediate buffer for one capacity (rows,
+experts, hidden, intermediate, top-k), so a step allocates nothing and can be
+captured in a HIP graph.  Row counts may live on the device (``row_count``):
+the kernels read them at run time, so one captured graph serves every
+occupancy up to the capacity.
+
+Step (one kernel each, all on the current stream):
+    route            logits -> ids, weights            (kernels.py:360-383)
+    quantize_rows    x -> e4m3 q + per-128 scales      (moe_input.py:24-27)
+    sort_routes      ids -> histogram, padded offsets, stable sorted pair list,
+                     inverse map, work items           (kernels.py:658-731)
+    expert_gemm FC1  gather q rows by route, W13, bf16 gate|up at sorted rows
+                                                       (kernels.py:290-301)
+    silu_mul_quant   SwiGLU + e4m3 requant             (kernels.py:344,748)
+    expert_gemm FC2  W2, fp32 per pair (unpermute)     (kernels.py:304-318)
+    weighted_combine sum_r w[t,r] y[t*K+r] -> bf16     (kernels.py:319-322,779)
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64, call, ptr
+
+SORT_TILE = 16  # MFMA route tile; also the padding granularity of the sorted layout
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    codes = {torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32, torch.int32: DTYPE_I32,
+             torch.int64: DTYPE_I64}
+    if dtype not in codes:
+        raise TypeError(f"unsupported dtype {dtype}")
+    return codes[dtype]
+
+
+def require_cuda(*tensors: torch.Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("MI355X MoE operators need device tensors (no CPU fallback)")
+
+
+def default_item_rows(rows: int) -> int:
+    """Routes per work item.  Up to 128 rows an expert cannot receive more
+    routes than rows, so one item covers all of an expert's routes (one weight
+    read per expert); larger batches cap items at 128 routes so busy experts
+    spread over several workgroups."""
+    if rows <= 128:
+        return max(SORT_TILE, -(-rows // SORT_TILE) * SORT_TILE)
+    return 128
+
+
+@dataclass
+class Shape:
+    rows: int
+    num_experts: int
+    hidden: int
+    intermediate: int
+    top_k: int = 8
+
+    @property
+    def pairs(self) -> int:
+        return self.rows * self.top_k
+
+
+class MoEWorkspace:
+    """Buffers of one MoE step at a fixed capacity (see module docstring)."""
+
+    def __init__(self, shape: Shape, device: torch.device | str = "cuda", tile: int = SORT_TILE,
+                 item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16):
+        lib = _lib.load()
+        self.shape = shape
+        self.device = torch.device(device)
+        self.tile = tile
+        self.item_rows = item_rows or default_item_rows(shape.rows)
+        if self.item_rows % tile:
+            raise ValueError("item_rows must be a multiple of the sort tile")
+        pairs = shape.pairs
+        self.max_rows = lib.d3_max_sorted_rows(pairs, shape.num_experts, tile)
+        self.max_items = lib.d3_max_items(pairs, shape.num_experts, self.item_rows)
+        dev = self.device
+        i32 = dict(dtype=torch.int32, device=dev)
+        h, e, i, t = shape.hidden, shape.num_experts, shape.intermediate, shape.rows
+        self.ids = torch.empty((t, shape.top_k), **i32)
+        self.weights = torch.empty((t, shape.top_k), dtype=weights_dtype, device=dev)
+        self.q = torch.empty((t, h), dtype=torch.uint8, device=dev)
+        self.x_scales = torch.empty((t, h // 128), dtype=torch.float32, device=dev)
+        self.counts = torch.empty(e, **i32)
+        self.starts = torch.empty(e, **i32)
+        self.total = torch.empty(1, **i32)
+        self.pairs_dev = torch.empty(1, **i32)
+        self.sorted_ids = torch.empty(self.max_rows, **i32)
+        self.expert_ids = torch.empty(self.max_rows // tile, **i32)
+        self.inverse = torch.empty(pairs, **i32)
+        self.items = torch.empty((max(self.max_items, 1), 4), **i32)
+        self.num_items = torch.empty(1, **i32)
+        self.gate_up = torch.empty((self.max_rows, 2 * i), dtype=torch.bfloat16, device=dev)
+        self.act = torch.empty((self.max_rows, i), dtype=torch.uint8, device=dev)
+        self.act_scales = torch.empty((self.max_rows, i // 128), dtype=torch.float32, device=dev)
+        self.down = torch.empty((pairs, h), dtype=torch.float32, device=dev)
+        self.out = torch.empty((t, h), dtype=torch.bfloat16, device=dev)
+
+    # -- stages ---------------------------------------------------------------
+    def route(self, logits: torch.Tensor, row_index=None, row_count=None, stream=None) -> None:
+        s = self.shape
+        call("d3_route", ptr(logits), dtype_code(logits.dtype), logits.stride(0), s.rows,
+             s.num_experts, s.top_k, ptr(row_index), ptr(row_count), ptr(self.ids), None,
+             ptr(self.weights), dtype_code(self.weights.dtype), stream)
+
+    def quantize(self, x: torch.Tensor, row_index=None, row_count=None, stream=None) -> None:
+        s = self.shape
+        call("d3_quantize_rows", ptr(x), x.stride(0), s.rows, s.hidden, ptr(row_index),
+             ptr(row_count), ptr(self.q), ptr(self.x_scales), 0, stream)
+
+    def sort(self, ids: torch.Tensor | None = None, row_count=None, stream=None) -> None:
+        s = self.shape
+        ids = self.ids if ids is None else ids
+        call("d3_sort_routes", ptr(ids), dtype_code(ids.dtype), s.rows, ptr(row_count), s.top_k,
+             s.num_experts, self.tile, ptr(self.counts), ptr(self.starts), ptr(self.total),
+             ptr(self.sorted_ids), ptr(self.expert_ids), self.max_rows, ptr(self.inverse),
+             self.item_rows, ptr(self.items), self.max_items, ptr(self.num_items),
+             ptr(self.pairs_dev), stream)
+
+    def fc1(self, experts, stream=None) -> None:
+        s = self.shape
+        call("d3_expert_gemm", 0, ptr(experts.w13_weight), ptr(experts.w13_scale_inv),
+             s.num_experts, 2 * s.intermediate, s.hidden, ptr(self.q), ptr(self.x_scales),
+             ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
+             ptr(self.gate_up), None, stream)
+
+    def activation(self, stream=None) -> None:
+        s = self.shape
+        call("d3_silu_mul_quant", ptr(self.gate_up), self.max_rows, s.intermediate,
+             ptr(self.total), ptr(self.sorted_ids), ptr(self.pairs_dev), 0, ptr(self.act),
+             ptr(self.act_scales), stream)
+
+    def fc2(self, experts, stream=None) -> None:
+        s = self.shape
+        call("d3_expert_gemm", 1, ptr(experts.w2_weight), ptr(experts.w2_scale_inv),
+             s.num_experts, s.hidden, s.intermediate, ptr(self.act), ptr(self.act_scales),
+             ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
+             None, ptr(self.down), stream)
+
+    def combine(self, weights: torch.Tensor | None = None, row_count=None, shared=None,
+                out=None, stream=None) -> torch.Tensor:
+        s = self.shape
+        weights = self.weights if weights is None else weights
+        out = self.out if out is None else out
+        call("d3_weighted_combine", ptr(self.down), ptr(weights), dtype_code(weights.dtype),
+             s.rows, s.top_k, s.hidden, ptr(row_count), ptr(shared), ptr(out), stream)
+        return out
+
+    # -- whole step -------------------------------------------------------------
+    def experts_forward(self, x, ids, weights, experts, row_index=None, row_count=None,
+                        shared=None, out=None, stream=None) -> torch.Tensor:
+        """Quantise, sort, FC1, SwiGLU requant, FC2, combine for given routes."""
+        stream = _lib.stream(self.device) if stream is None else stream
+        self.quantize(x, row_index, row_count, stream)
+        self.sort(ids, row_count, stream)
+        self.fc1(experts, stream)
+        self.activation(stream)
+        self.fc2(experts, stream)
+        return self.combine(weights, row_count, shared, out, stream)
+
+    def forward(self, x, logits, experts, row_index=None, row_count=None, shared=None,
+                out=None, stream=None) -> torch.Tensor:
+        """Route + experts.  ``row_index`` gathers x / logits rows (slot
+        compaction), ``row_count`` is the live row count on the device."""
+        stream = _lib.stream(self.device) if stream is None else stream
+        self.route(logits, row_index, row_count, stream)
+        return self.experts_forward(x, self.ids, self.weights, experts, row_index, row_count,
+                                    shared, out, stream)
+
+
+class DenseExpert:
+    """A dense FP8 SwiGLU expert applied to every row (config-4 shared expert),
+    run through the same kernels with the identity route list."""
+
+    def __init__(self, rows: int, hidden: int, intermediate: int, device="cuda",
+                 item_rows: int = 128):
+        self.rows, self.hidden, self.intermediate = rows, hidden, intermediate
+        dev = torch.device(device)
+        self.item_rows = item_rows
+        chunks = -(-rows // item_rows)
+        self.max_items = chunks
+        items = [[0, c * item_rows, min(item_rows, rows - c * item_rows), 0] for c in range(chunks)]
+        self.items = torch.tensor(items or [[0, 0, 0, 0]], dtype=torch.int32, device=dev)
+        self.num_items = torch.tensor([chunks], dtype=torch.int32, device=dev)
+        self.sorted_ids = torch.arange(max(rows, 1), dtype=torch.int32, device=dev)
+        self.gate_up = torch.empty((rows, 2 * intermediate), dtype=torch.bfloat16, device=dev)
+        self.act = torch.empty((rows, intermediate), dtype=torch.uint8, device=dev)
+        self.act_scales = torch.empty((rows, intermediate // 128), dtype=torch.float32, device=dev)
+        self.down = torch.empty((rows, hidden), dtype=torch.float32, device=dev)
+
+    def forward(self, q, x_scales, experts, stream=None) -> torch.Tensor:
+        """q / x_scales: the already quantised rows [rows, H]; returns fp32 [rows, H]."""
+        stream = _lib.stream(q.device) if stream is None else stream
+        h, i = self.hidden, self.intermediate
+        call("d3_expert_gemm", 0, ptr(experts.w13_weight), ptr(experts.w13_scale_inv), 1, 2 * i,
+             h, ptr(q), ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items),
+             ptr(self.num_items), self.max_items, ptr(self.gate_up), None, stream)
+        call("d3_silu_mul_quant", ptr(self.gate_up), self.rows, i, None, None, None, 0,
+             ptr(self.act), ptr(self.act_scales), stream)
+        call("d3_expert_gemm", 1, ptr(experts.w2_weight), ptr(experts.w2_scale_inv), 1, h, i,
+             ptr(self.act), ptr(self.act_scales), ptr(self.sorted_ids), 1, ptr(self.items),
+             ptr(self.num_items), self.max_items, None, ptr(self.down), stream)
+        return self.down
+
+
+def compact_slots(occupancy: torch.Tensor, active: torch.Tensor, count: torch.Tensor,
+                  stream=None) -> None:
+    """occupancy uint8 [S] -> active int32 [S] (ascending, -1 padded), count int32 [1]."""
+    require_cuda(occupancy, active, count)
+    stream = _lib.stream(occupancy.device) if stream is None else stream
+    call("d3_compact_slots", ptr(occupancy), occupancy.numel(), ptr(active), ptr(count), stream)
+
+
+class DecodeStep:
+    """The 64-slot decode MoE step: device-side slot compaction, then route +
+    experts over the live rows, everything sized for the slot capacity and
+    driven by the device count (graph-capturable, no host sync).
+
+    Output row r belongs to slot ``active[r]`` for r < ``count``.
+    """
+
+    def __init__(self, slots: int, num_experts: int, hidden: int, intermediate: int,
+                 top_k: int = 8, device="cuda", item_rows: int | None = None):
+        dev = torch.device(device)
+        self.slots = slots
+        self.active = torch.empty(slots, dtype=torch.int32, device=dev)
+        self.count = torch.empty(1, dtype=torch.int32, device=dev)
+        self.workspace = MoEWorkspace(Shape(slots, num_experts, hidden, intermediate, top_k), dev,
+                                      item_rows=item_rows)
+
+    def __call__(self, occupancy, x_slots, logits_slots, experts, stream=None) -> torch.Tensor:
+        stream = _lib.stream(x_slots.device) if stream is None else stream
+        compact_slots(occupancy, self.active, self.count, stream)
+        return self.workspace.forward(x_slots, logits_slots, experts, row_index=self.active,
+                                      row_count=self.count, stream=stream)

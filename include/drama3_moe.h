@@ -1,0 +1,250 @@
+/*
+ * drama3_moe.h -- C ABI of the MI355X (gfx950) packed FP8 top-8 MoE step.
+ *
+ * Every entry point takes raw device pointers, sizes and strides (in
+ * elements) and a hipStream_t passed as `void *stream` (NULL = legacy default
+ * stream).  Nothing here allocates or frees memory, synchronises the stream
+ * or copies device data to the host, so every call is hipGraph-capturable.
+ * Calls are re-entrant: the library keeps no mutable global state besides a
+ * thread-local error message.
+ *
+ * Data types:   bf16 = uint16_t bit patterns;  fp8 = uint8_t OCP e4m3fn codes;
+ *               fp32 block scales = float, one per 128 x 128 weight block or
+ *               per 128 contiguous activation elements.
+ * Weight layout (reference src/drama3/kernels.py:290-318):
+ *               w13 [E, 2I, H] fp8 rows [gate; up],  s13 [E, 2I/128, H/128]
+ *               w2  [E, H, I]  fp8,                  s2  [E, H/128, I/128]
+ * Device row counts: wherever `row_count` appears, a non-NULL pointer names an
+ * int32 on the device holding the live number of rows (<= the host `rows`
+ * capacity); rows at or beyond it are left untouched.  NULL means all `rows`.
+ *
+ * Return value: D3_OK or a D3_ERR_* code; d3_last_error() describes the
+ * failure of the last call made on the calling thread.
+ */
+#ifndef DRAMA3_MOE_H
+#define DRAMA3_MOE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define D3_OK 0
+#define D3_ERR_INVALID_ARGUMENT 1 /* shape / stride / pointer contract violated */
+#define D3_ERR_UNSUPPORTED 2      /* shape outside the compiled kernel set */
+#define D3_ERR_HIP 3              /* a HIP runtime call failed */
+
+#define D3_DTYPE_BF16 0
+#define D3_DTYPE_F32 1
+#define D3_DTYPE_I32 2
+#define D3_DTYPE_I64 3
+
+/* Version of this ABI (bumped on any signature change). */
+int d3_abi_version(void);
+
+/* Message for the last failed call on this thread ("" after success). */
+const char *d3_last_error(void);
+
+/*
+ * A1  Active-slot compaction.
+ * Replaces the host-side filter of live requests and slot list assembly of
+ * the reference engine (src/drama3/engine.py:637-647, engine.py:136-144).
+ * occupancy[num_slots] (nonzero = live) -> active_slots[0..n) ascending,
+ * active_slots[n..num_slots) = -1, *count = n.  One workgroup; no padding
+ * rows (the reference pads to a graph bucket with reserved slots instead).
+ */
+int d3_compact_slots(const uint8_t *occupancy, int32_t num_slots, int32_t *active_slots,
+                     int32_t *count, void *stream);
+
+/*
+ * A3  Top-k softmax routing.
+ * Replaces route() / route_kernel (src/drama3/kernels.py:360-383).
+ * logits[row_index ? row_index[r] : r] (bf16 or f32, row stride in elements,
+ * unit column stride) -> ids (int32 and/or int64, [rows, top_k]) and weights
+ * ([rows, top_k] bf16 or f32).  Ranking key: the bf16 value of the logit,
+ * ties to the lower expert index; output in descending key order; weights are
+ * the fp32 softmax probabilities of the selected experts renormalised to sum
+ * to one.  num_experts <= 512, top_k <= 16.  ids32 / ids64 may be NULL.
+ */
+int d3_route(const void *logits, int32_t logits_dtype, int64_t logits_row_stride, int32_t rows,
+             int32_t num_experts, int32_t top_k, const int32_t *row_index,
+             const int32_t *row_count, int32_t *ids32, int64_t *ids64, void *weights,
+             int32_t weights_dtype, void *stream);
+
+/*
+ * A4  Per-128 FP8 activation quantisation.
+ * Replaces Fish Speech quantize_groups(quant_kernel, x, H) as called at
+ * src/drama3/kernels.py:332,732 and model.py:554 (its rule restated by
+ * prepare_kernel, src/drama3/moe_input.py:24-27).
+ * x[row_index ? row_index[r] : r] bf16 [rows, width] -> q fp8 [rows, width]
+ * and scales f32: [rows, width/128] (scales_transposed = 0) or
+ * [width/128, rows] (scales_transposed = 1).  width % 128 == 0.
+ */
+int d3_quantize_rows(const uint16_t *x, int64_t x_row_stride, int32_t rows, int32_t width,
+                     const int32_t *row_index, const int32_t *row_count, uint8_t *q,
+                     float *scales, int32_t scales_transposed, void *stream);
+
+/*
+ * A4  Fused MoE input preparation.
+ * Replaces prepare_moe_input / prepare_kernel (src/drama3/moe_input.py:8-79).
+ * x bf16 [rows, hidden] -> q fp8 [rows, hidden], scales f32 [hidden/128, rows]
+ * (transposed layout), logits f32 [rows, num_experts] converted from the
+ * router (bf16 or f32).  When row_slots != NULL (int32 or int64, one per
+ * row), rows whose slot >= padding_start read router row 0.
+ */
+int d3_prepare_moe_input(const uint16_t *x, int64_t x_row_stride, const void *router,
+                         int32_t router_dtype, int64_t router_row_stride, int32_t rows,
+                         int32_t hidden, int32_t num_experts, const void *row_slots,
+                         int32_t row_slots_dtype, int64_t padding_start, uint8_t *q,
+                         float *scales, float *logits, void *stream);
+
+/*
+ * A5-A7  Expert histogram, padded offsets and stable route sort.
+ * Replaces expert_counts_kernel, expert_offsets_kernel and
+ * expert_scatter_kernel (src/drama3/kernels.py:658-699) with the buffer
+ * sizing of native_moe (kernels.py:710-731).
+ * ids (int32 or int64) [rows, top_k]; pairs = live rows * top_k.
+ *   counts[E], starts[E] (exclusive scan of counts padded to `tile`), *total;
+ *   sorted_ids[max_rows]: pair ids grouped by expert in ascending pair order,
+ *     padding and every slot from *total on hold the sentinel `pairs`;
+ *   expert_ids[max_rows / tile]: expert of each tile, -1 from *total/tile on;
+ *   inverse[pairs] (optional, NULL to skip): sorted position of each pair;
+ *   items[max_items][4] (optional): work items {expert, sorted start, routes,
+ *     0} covering each expert's routes in chunks of item_rows (a multiple of
+ *     tile), with *num_items.  max_items must be >= d3_max_items(...).
+ *   *pairs_out (optional): the live pair count, i.e. the sentinel value.
+ * One workgroup; deterministic.
+ */
+int d3_sort_routes(const void *ids, int32_t ids_dtype, int32_t rows, const int32_t *row_count,
+                   int32_t top_k, int32_t num_experts, int32_t tile, int32_t *counts,
+                   int32_t *starts, int32_t *total, int32_t *sorted_ids, int32_t *expert_ids,
+                   int32_t max_rows, int32_t *inverse, int32_t item_rows, int32_t *items,
+                   int32_t max_items, int32_t *num_items, int32_t *pairs_out, void *stream);
+
+/* Capacity helpers for d3_sort_routes (host-side arithmetic only). */
+int32_t d3_max_sorted_rows(int32_t pairs, int32_t num_experts, int32_t tile);
+int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);
+
+/*
+ * A8-A11  Grouped FP8 expert GEMM over sorted routes (FC1 or FC2).
+ * Replaces expert_up_kernel / expert_down_kernel (src/drama3/kernels.py:290-322)
+ * and Fish fused_moe_gemm as driven by native_moe (kernels.py:734-778).
+ * For every work item {e, start, n}: rows p in [start, start+n) of the
+ * sorted route list contract with expert e's weight w[e] (fp8 [N, K], block
+ * scales ws[e] [N/128, K/128]) on MFMA 16x16x128 FP8 tiles:
+ *   out[p, j] = sum_k (w[e,j,k] ws[e,j/128,k/128]) (a[r,k] as[r,k/128])
+ * accumulated in fp32, where the activation row r is
+ *   mode 0 (FC1): token sorted_ids[p] / top_k of a [*, K] (gather = permute),
+ *                 output bf16 at sorted position p: out_bf16[p, N];
+ *   mode 1 (FC2): sorted position p of a [max_rows, K],
+ *                 output fp32 at pair sorted_ids[p]: out_f32[pair, N]
+ *                 (scatter = unpermute).
+ * Work items cover live routes only, so padding slots are never read.
+ * The grid is max_items x (N / row tile); items at or beyond *num_items exit.
+ * Supported: K in {256, 512, 768, 1024, 1536, 2048}; N a multiple of the
+ * workgroup row tile (64 for K >= 1024, 128 for K = 512/768, 256 for K = 256).
+ */
+int d3_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32_t num_experts,
+                   int32_t n, int32_t k, const uint8_t *a, const float *a_scales,
+                   const int32_t *sorted_ids, int32_t top_k, const int32_t *items,
+                   const int32_t *num_items, int32_t max_items, uint16_t *out_bf16,
+                   float *out_f32, void *stream);
+
+/*
+ * A10  SwiGLU + per-128 FP8 requantisation of FC1 rows.
+ * Replaces Fish quantize_groups(silu_mul_quant_kernel, gate_up, I)
+ * (src/drama3/kernels.py:344,748).  gate_up bf16 [rows, 2I] ([gate | up]) ->
+ * a = silu(gate) * up in fp32 -> act fp8 [rows, I] + act_scales f32
+ * [rows, I/128].  When sorted_ids != NULL, row p is processed only if
+ * sorted_ids[p] < pairs (live routes); rows = capacity, row_count optional.
+ */
+int d3_silu_mul_quant(const uint16_t *gate_up, int32_t rows, int32_t intermediate,
+                      const int32_t *row_count, const int32_t *sorted_ids,
+                      const int32_t *pairs_dev, int32_t pairs, uint8_t *act, float *act_scales,
+                      void *stream);
+
+/*
+ * A11  Weighted combine (unpermute + top-k reduction).
+ * Replaces the fused combine of expert_down_kernel (src/drama3/kernels.py:319-322)
+ * and native_moe's down.view(T, 8, H).sum(1) (kernels.py:779).
+ * out[t, :] = bf16( sum_{r=0..top_k-1} w[t,r] * down[t*top_k + r, :] ) in
+ * rank order, fp32 accumulation; w bf16 or f32 [rows, top_k].  When
+ * shared != NULL (fp32 [rows, hidden]), out = bf16(out + bf16(shared)): a
+ * dense shared expert added to the routed output.
+ */
+int d3_weighted_combine(const float *down, const void *weights, int32_t weights_dtype,
+                        int32_t rows, int32_t top_k, int32_t hidden, const int32_t *row_count,
+                        const float *shared, uint16_t *out, void *stream);
+
+/*
+ * A12  Routed + gated shared expert combine.
+ * Replaces combine_experts (src/drama3/kernels.py:427-445):
+ * out = bf16(routed + bf16(shared * bf16(sigmoid(gate[r * gate_stride])))).
+ */
+int d3_combine_experts(const uint16_t *routed, const uint16_t *shared, const uint16_t *gate,
+                       int64_t gate_stride, int32_t rows, int32_t width, uint16_t *out,
+                       void *stream);
+
+/*
+ * A12  Combine + residual update + (1 + w) RMSNorm.
+ * Replaces combine_experts_add_norm and combine_experts_add_norm_inverse
+ * (src/drama3/kernels.py:448-556).  Row r reads MoE row inverse[r] when
+ * inverse != NULL (int64), else r.  combined is the single-rounding bf16
+ * FMA shared * bf16(sigmoid(gate)) + routed; residual[r] is updated in place
+ * to bf16(combined + residual[r]); out[r] = bf16(residual * rsqrt(mean(
+ * residual^2) + eps) * (1 + weight)).  width <= 8192.
+ */
+int d3_combine_experts_add_norm(const uint16_t *routed, const uint16_t *shared,
+                                const uint16_t *gate, int64_t gate_stride,
+                                const int64_t *inverse, uint16_t *residual,
+                                const uint16_t *weight, float eps, int32_t rows, int32_t width,
+                                uint16_t *out, void *stream);
+
+/*
+ * Residual add + RMSNorm without the MoE combine.
+ * Replaces add_norm (src/drama3/kernels.py:405-424).
+ */
+int d3_add_norm(const uint16_t *x, uint16_t *residual, const uint16_t *weight, float eps,
+                int32_t rows, int32_t width, uint16_t *out, void *stream);
+
+/*
+ * BF16 SwiGLU of a [gate | up] projection (shared expert input).
+ * Replaces silu_mul (src/drama3/kernels.py:386-402).
+ */
+int d3_silu_mul(const uint16_t *projected, int64_t row_stride, int32_t rows, int32_t width,
+                uint16_t *out, void *stream);
+
+/*
+ * A13  Ragged packed-row metadata.
+ * Replaces row_metadata (src/drama3/packed_prefill.py:51-78).
+ * cu_seqlens int32 [sequences + 1], sequence_slots int64 [sequences] ->
+ * positions int64 [capacity], row_slots int64 [capacity] and, when frames !=
+ * NULL, labels int64 [capacity, codes] (next row's frame inside the sequence,
+ * else eos / 0).  frames int64 [capacity, codes].
+ */
+int d3_row_metadata(const int32_t *cu_seqlens, const int64_t *sequence_slots,
+                    int32_t sequences, int32_t capacity, const int64_t *frames, int32_t codes,
+                    int64_t eos, int64_t *positions, int64_t *row_slots, int64_t *labels,
+                    void *stream);
+
+/*
+ * A1  Per-slot request state gather / update.
+ * Replace DeviceRequests.load / .save and their _load / _save kernels
+ * (src/drama3/runtime_state.py:10-56,94-124).  State layout: last [S, 11],
+ * history [S, 16], metadata [S, 4] = {position, count, limit, done}, codes
+ * [S, max_frames, 10]; all int64.  slots int64 [rows].
+ */
+int d3_requests_load(const int64_t *last, const int64_t *history, const int64_t *metadata,
+                     const int64_t *slots, int32_t rows, int64_t max_length,
+                     int64_t padding_start, int64_t *frames_out, int64_t *history_out,
+                     int64_t *positions_out, void *stream);
+int d3_requests_save(int64_t *last, int64_t *history, int64_t *metadata, int64_t *codes,
+                     const int64_t *slots, int32_t rows, const int64_t *output, int64_t eos,
+                     int64_t limit, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DRAMA3_MOE_H */

@@ -1,0 +1,101 @@
+"""The C-ABI library loads, exports every entry point declared in
+include/drama3_moe.h with the declared arity, and rejects contract
+violations before launching anything (CPU only: no kernel is run)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "drama3_moe.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for match in re.finditer(r"\b(?:int|int32_t|const char \*)\s*(d3_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = match.group(2).strip()
+        out[match.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from drama3_amd import _lib
+
+    if not _lib.LIBRARY.exists():
+        pytest.skip("library not built")
+    return _lib.load()
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for required in ("d3_compact_slots", "d3_route", "d3_quantize_rows", "d3_prepare_moe_input",
+                     "d3_sort_routes", "d3_expert_gemm", "d3_silu_mul_quant",
+                     "d3_weighted_combine", "d3_combine_experts", "d3_combine_experts_add_norm",
+                     "d3_row_metadata", "d3_requests_load", "d3_requests_save"):
+        assert required in names
+
+
+def test_every_declared_symbol_is_exported_with_its_arity(lib):
+    from drama3_amd import _lib
+
+    declared = declared_functions()
+    assert set(declared) == set(_lib.SIGNATURES), "header and ctypes table disagree"
+    for name, arity in declared.items():
+        assert hasattr(lib, name), name
+        assert len(_lib.SIGNATURES[name][1]) == arity, name
+
+
+def test_capacity_helpers(lib):
+    from oracle import moe as om
+
+    for pairs, experts, tile in ((32, 16, 16), (384, 128, 16), (33280, 128, 64), (0, 8, 16)):
+        assert lib.d3_max_sorted_rows(pairs, experts, tile) == om.max_sorted_rows(pairs, experts, tile)
+    assert lib.d3_max_items(384, 128, 64) == (384 + 128 * 63) // 64
+    assert lib.d3_abi_version() == 1
+
+
+def test_contract_violations_raise_value_error(lib):
+    from drama3_amd import _lib
+
+    with pytest.raises(ValueError, match="null"):
+        _lib.call("d3_route", None, 0, 16, 4, 16, 8, None, None, None, None, None, 0, None)
+    with pytest.raises(ValueError, match="num_experts"):
+        _lib.call("d3_route", 16, 0, 1024, 4, 1024, 8, None, None, 16, None, 16, 0, None)
+    with pytest.raises(ValueError, match="multiple of 128"):
+        _lib.call("d3_quantize_rows", 16, 200, 4, 200, None, None, 16, 16, 0, None)
+    with pytest.raises(ValueError, match="max_rows"):
+        _lib.call("d3_sort_routes", 16, 3, 4, None, 8, 16, 16, 16, 16, 16, 16, 16, 8, None, 16,
+                  None, 0, None, None, None)
+    with pytest.raises(ValueError, match="K="):
+        _lib.call("d3_expert_gemm", 0, 16, 16, 4, 512, 384, 16, 16, 16, 8, 16, 16, 4, 16, None,
+                  None)
+    assert "K=" in lib.d3_last_error().decode()
+
+
+def test_product_code_does_not_import_the_oracle():
+    package = ROOT / "drama-3-single-b300-inference_amd"
+    for path in package.rglob("*.py"):
+        text = path.read_text()
+        assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", text, flags=re.M), path
+
+
+def test_no_cpu_fallback_when_library_missing(monkeypatch, tmp_path):
+    from drama3_amd import _lib
+
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setenv("DRAMA3_MOE_LIBRARY", str(tmp_path / "missing.so"))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        _lib.load()
+
+
+def test_ctypes_types_are_plain():
+    from drama3_amd import _lib
+
+    allowed = {ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_char_p}
+    for restype, argtypes in _lib.SIGNATURES.values():
+        assert restype in allowed and all(a in allowed for a in argtypes)
