@@ -22,6 +22,17 @@
 //     0-15 = k in [16g, 16g+16), bytes 16-31 = k in [64+16g, 64+16g+16)), so
 //     each 16-byte load covers 64 contiguous bytes per row per instruction.
 //     The product is invariant under any k permutation applied to both.
+//   * Two arithmetic paths, chosen per work item (uniform per workgroup):
+//     - exact path (items with <= exact_routes routes: decode, bandwidth
+//       bound): the FP8 bytes are widened to bf16 in registers (exact, e4m3
+//       is a subset of bf16) and contracted with MFMA 16x16x32 bf16, whose
+//       products are exact and whose accumulation has fp32 accuracy;
+//     - contraction path (larger items: prefill): MFMA 16x16x128 FP8 at twice
+//       the bf16 rate.  The FP8 instruction aligns the products of each
+//       output element before summing with limited precision (measured on
+//       MI355X: error up to ~1e-4 of sum|products|, exact when the products
+//       share an exponent range), the same class of rounding as FP8 tensor
+//       core GEMMs.
 #include "common.h"
 #include "status.h"
 
@@ -30,6 +41,8 @@ namespace {
 
 typedef int int32x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kGemmWaves = 4;
 constexpr int kGemmThreads = kGemmWaves * kWave;
@@ -51,12 +64,38 @@ __device__ __forceinline__ floatx4 mfma_fp8(const int32x8& a, const int32x8& b) 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
 }
 
+// 32 e4m3 bytes -> 4 x 8 bf16, exactly (scale 1.0).  Element i of part j is
+// byte 8j + i, for both operands alike.
+__device__ __forceinline__ void widen_fp8(const int32x8& v, bf16x8 out[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[2 * j], 1.0f, false);
+    const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[2 * j], 1.0f, true);
+    const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[2 * j + 1], 1.0f, false);
+    const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[2 * j + 1], 1.0f, true);
+    out[j] = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+  }
+}
+
+// One K128 block on the exact path: four chained bf16 MFMAs.  The weight
+// fragment is passed through an empty asm so the widening cannot be hoisted
+// out of the route-tile loop (that would hold every K block in bf16 at once).
+__device__ __forceinline__ floatx4 mfma_block_bf16(int32x8 a, const bf16x8 b[4]) {
+  asm volatile("" : "+v"(a));
+  bf16x8 wide[4];
+  widen_fp8(a, wide);
+  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wide[j], b[j], acc, 0, 0, 0);
+  return acc;
+}
+
 template <int KB, int RT, int MODE>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void expert_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows,
     const uint8_t* __restrict__ act, const float* __restrict__ act_scales,
     const int32_t* __restrict__ sorted_ids, int top_k, const int4* __restrict__ items,
-    const int32_t* __restrict__ num_items, uint16_t* __restrict__ out_bf16,
+    const int32_t* __restrict__ num_items, int exact_routes, uint16_t* __restrict__ out_bf16,
     float* __restrict__ out_f32) {
   constexpr int K = KB * kGroup;
   constexpr int kRowsPerWave = RT * 16;
@@ -75,6 +114,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   const int expert = item.x;
   const int first = item.y;
   const int routes = item.z;  // every route of an item is live (no padding)
+  const bool exact = routes <= exact_routes;
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -125,14 +165,31 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint8_t* brow = b_tile + row16 * kStride;
+    if (exact) {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      const int32x8 b_frag = load_fragment(brow, kb, group);
-      const float b_scale = b_scales[row16 * KB + kb];
+      for (int kb = 0; kb < KB; ++kb) {
+        bf16x8 b_wide[4];
+        widen_fp8(load_fragment(brow, kb, group), b_wide);
+        const float b_scale = b_scales[row16 * KB + kb];
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const floatx4 partial = mfma_fp8(a_frag[rt][kb], b_frag);
-        acc[rt] += partial * (w_scale[rt][kb] * b_scale);
+        for (int rt = 0; rt < RT; ++rt) {
+          const floatx4 partial = mfma_block_bf16(a_frag[rt][kb], b_wide);
+          acc[rt] += partial * (w_scale[rt][kb] * b_scale);
+        }
+        // Keep one K block's widened operands live at a time (the weights
+        // already occupy most of the register file).
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int32x8 b_frag = load_fragment(brow, kb, group);
+        const float b_scale = b_scales[row16 * KB + kb];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const floatx4 partial = mfma_fp8(a_frag[rt][kb], b_frag);
+          acc[rt] += partial * (w_scale[rt][kb] * b_scale);
+        }
       }
     }
     const int target = b_target[row16];
@@ -254,10 +311,11 @@ __global__ __launch_bounds__(kRowThreads) void weighted_combine_kernel(
 template <int KB, int RT, int MODE>
 void launch_gemm(dim3 grid, hipStream_t s, const uint8_t* w, const float* ws, int n,
                  const uint8_t* a, const float* as, const int32_t* sorted_ids, int top_k,
-                 const int4* items, const int32_t* num_items, uint16_t* out_bf16,
-                 float* out_f32) {
+                 const int4* items, const int32_t* num_items, int exact_routes,
+                 uint16_t* out_bf16, float* out_f32) {
   hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE>), grid, dim3(kGemmThreads), 0, s, w, ws,
-                     n, a, as, sorted_ids, top_k, items, num_items, out_bf16, out_f32);
+                     n, a, as, sorted_ids, top_k, items, num_items, exact_routes, out_bf16,
+                     out_f32);
 }
 
 // Row tiles per wave: keep each wave's register-resident weights near 32 KiB.
@@ -266,8 +324,8 @@ constexpr int rt_for(int kb) { return kb >= 8 ? 1 : (kb >= 4 ? 2 : 4); }
 template <int KB>
 int dispatch_gemm(int mode, int n, dim3 items_grid, hipStream_t s, const uint8_t* w,
                   const float* ws, const uint8_t* a, const float* as, const int32_t* sorted_ids,
-                  int top_k, const int4* items, const int32_t* num_items, uint16_t* out_bf16,
-                  float* out_f32) {
+                  int top_k, const int4* items, const int32_t* num_items, int exact_routes,
+                  uint16_t* out_bf16, float* out_f32) {
   constexpr int RT = rt_for(KB);
   constexpr int rows_per_group = kGemmWaves * RT * 16;
   D3_SUPPORTED(n % rows_per_group == 0, "expert_gemm: N=%d must be a multiple of %d for K=%d", n,
@@ -275,10 +333,10 @@ int dispatch_gemm(int mode, int n, dim3 items_grid, hipStream_t s, const uint8_t
   const dim3 grid(items_grid.x * (n / rows_per_group));
   if (mode == 0)
     launch_gemm<KB, RT, 0>(grid, s, w, ws, n, a, as, sorted_ids, top_k, items, num_items,
-                           out_bf16, out_f32);
+                           exact_routes, out_bf16, out_f32);
   else
     launch_gemm<KB, RT, 1>(grid, s, w, ws, n, a, as, sorted_ids, top_k, items, num_items,
-                           out_bf16, out_f32);
+                           exact_routes, out_bf16, out_f32);
   return D3_OK;
 }
 
@@ -292,7 +350,7 @@ using namespace d3;
 extern "C" int d3_expert_gemm(int32_t mode, const uint8_t* w, const float* ws, int32_t num_experts,
                               int32_t n, int32_t k, const uint8_t* a, const float* a_scales,
                               const int32_t* sorted_ids, int32_t top_k, const int32_t* items,
-                              const int32_t* num_items,
+                              const int32_t* num_items, int32_t exact_routes,
                               int32_t max_items, uint16_t* out_bf16, float* out_f32,
                               void* stream) {
   D3_REQUIRE(mode == 0 || mode == 1, "expert_gemm: mode must be 0 (FC1) or 1 (FC2)");
@@ -317,7 +375,7 @@ extern "C" int d3_expert_gemm(int32_t mode, const uint8_t* w, const float* ws, i
 #define D3_GEMM_CASE(KB)                                                                       \
   case KB:                                                                                     \
     status = dispatch_gemm<KB>(mode, n, items_grid, s, w, ws, a, a_scales, sorted_ids, top_k,  \
-                               it, num_items, out_bf16, out_f32);                              \
+                               it, num_items, exact_routes, out_bf16, out_f32);                \
     break;
     D3_GEMM_CASE(2)
     D3_GEMM_CASE(4)

@@ -28,6 +28,9 @@ from . import _lib
 from ._lib import DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64, call, ptr
 
 SORT_TILE = 16  # MFMA route tile; also the padding granularity of the sorted layout
+# Work items with at most this many routes take the exact (bf16-MFMA) path of
+# the expert GEMM; larger items are real contractions and take FP8 MFMAs.
+EXACT_ROUTES = 64
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -44,14 +47,13 @@ def require_cuda(*tensors: torch.Tensor | None) -> None:
             raise ValueError("MI355X MoE operators need device tensors (no CPU fallback)")
 
 
-def default_item_rows(rows: int) -> int:
-    """Routes per work item.  Up to 128 rows an expert cannot receive more
-    routes than rows, so one item covers all of an expert's routes (one weight
-    read per expert); larger batches cap items at 128 routes so busy experts
-    spread over several workgroups."""
-    if rows <= 128:
-        return max(SORT_TILE, -(-rows // SORT_TILE) * SORT_TILE)
-    return 128
+def default_item_rows(rows: int, tile: int = SORT_TILE) -> int:
+    """Routes per work item (a multiple of ``tile``).  Up to 128 rows an
+    expert cannot receive more routes than rows, so one item covers all of an
+    expert's routes (one weight read per expert); larger batches cap items at
+    128 routes so busy experts spread over several workgroups."""
+    rows = min(rows, 128) if rows > 128 else rows
+    return max(tile, -(-rows // tile) * tile)
 
 
 @dataclass
@@ -71,12 +73,14 @@ class MoEWorkspace:
     """Buffers of one MoE step at a fixed capacity (see module docstring)."""
 
     def __init__(self, shape: Shape, device: torch.device | str = "cuda", tile: int = SORT_TILE,
-                 item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16):
+                 item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
+                 exact_routes: int = EXACT_ROUTES):
         lib = _lib.load()
         self.shape = shape
         self.device = torch.device(device)
         self.tile = tile
-        self.item_rows = item_rows or default_item_rows(shape.rows)
+        self.exact_routes = exact_routes
+        self.item_rows = item_rows or default_item_rows(shape.rows, tile)
         if self.item_rows % tile:
             raise ValueError("item_rows must be a multiple of the sort tile")
         pairs = shape.pairs
@@ -105,19 +109,22 @@ class MoEWorkspace:
         self.out = torch.empty((t, h), dtype=torch.bfloat16, device=dev)
 
     # -- stages ---------------------------------------------------------------
+    def _stream(self, stream):
+        return _lib.stream(self.device) if stream is None else stream
+
     def route(self, logits: torch.Tensor, row_index=None, row_count=None, stream=None) -> None:
-        s = self.shape
+        s, stream = self.shape, self._stream(stream)
         call("d3_route", ptr(logits), dtype_code(logits.dtype), logits.stride(0), s.rows,
              s.num_experts, s.top_k, ptr(row_index), ptr(row_count), ptr(self.ids), None,
              ptr(self.weights), dtype_code(self.weights.dtype), stream)
 
     def quantize(self, x: torch.Tensor, row_index=None, row_count=None, stream=None) -> None:
-        s = self.shape
+        s, stream = self.shape, self._stream(stream)
         call("d3_quantize_rows", ptr(x), x.stride(0), s.rows, s.hidden, ptr(row_index),
              ptr(row_count), ptr(self.q), ptr(self.x_scales), 0, stream)
 
     def sort(self, ids: torch.Tensor | None = None, row_count=None, stream=None) -> None:
-        s = self.shape
+        s, stream = self.shape, self._stream(stream)
         ids = self.ids if ids is None else ids
         call("d3_sort_routes", ptr(ids), dtype_code(ids.dtype), s.rows, ptr(row_count), s.top_k,
              s.num_experts, self.tile, ptr(self.counts), ptr(self.starts), ptr(self.total),
@@ -126,28 +133,28 @@ class MoEWorkspace:
              ptr(self.pairs_dev), stream)
 
     def fc1(self, experts, stream=None) -> None:
-        s = self.shape
+        s, stream = self.shape, self._stream(stream)
         call("d3_expert_gemm", 0, ptr(experts.w13_weight), ptr(experts.w13_scale_inv),
              s.num_experts, 2 * s.intermediate, s.hidden, ptr(self.q), ptr(self.x_scales),
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
-             ptr(self.gate_up), None, stream)
+             self.exact_routes, ptr(self.gate_up), None, stream)
 
     def activation(self, stream=None) -> None:
-        s = self.shape
+        s, stream = self.shape, self._stream(stream)
         call("d3_silu_mul_quant", ptr(self.gate_up), self.max_rows, s.intermediate,
              ptr(self.total), ptr(self.sorted_ids), ptr(self.pairs_dev), 0, ptr(self.act),
              ptr(self.act_scales), stream)
 
     def fc2(self, experts, stream=None) -> None:
-        s = self.shape
+        s, stream = self.shape, self._stream(stream)
         call("d3_expert_gemm", 1, ptr(experts.w2_weight), ptr(experts.w2_scale_inv),
              s.num_experts, s.hidden, s.intermediate, ptr(self.act), ptr(self.act_scales),
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
-             None, ptr(self.down), stream)
+             self.exact_routes, None, ptr(self.down), stream)
 
     def combine(self, weights: torch.Tensor | None = None, row_count=None, shared=None,
                 out=None, stream=None) -> torch.Tensor:
-        s = self.shape
+        s, stream = self.shape, self._stream(stream)
         weights = self.weights if weights is None else weights
         out = self.out if out is None else out
         call("d3_weighted_combine", ptr(self.down), ptr(weights), dtype_code(weights.dtype),
@@ -181,8 +188,9 @@ class DenseExpert:
     run through the same kernels with the identity route list."""
 
     def __init__(self, rows: int, hidden: int, intermediate: int, device="cuda",
-                 item_rows: int = 128):
+                 item_rows: int = 128, exact_routes: int = EXACT_ROUTES):
         self.rows, self.hidden, self.intermediate = rows, hidden, intermediate
+        self.exact_routes = exact_routes
         dev = torch.device(device)
         self.item_rows = item_rows
         chunks = -(-rows // item_rows)
@@ -202,12 +210,14 @@ class DenseExpert:
         h, i = self.hidden, self.intermediate
         call("d3_expert_gemm", 0, ptr(experts.w13_weight), ptr(experts.w13_scale_inv), 1, 2 * i,
              h, ptr(q), ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items),
-             ptr(self.num_items), self.max_items, ptr(self.gate_up), None, stream)
+             ptr(self.num_items), self.max_items, self.exact_routes, ptr(self.gate_up), None,
+             stream)
         call("d3_silu_mul_quant", ptr(self.gate_up), self.rows, i, None, None, None, 0,
              ptr(self.act), ptr(self.act_scales), stream)
         call("d3_expert_gemm", 1, ptr(experts.w2_weight), ptr(experts.w2_scale_inv), 1, h, i,
              ptr(self.act), ptr(self.act_scales), ptr(self.sorted_ids), 1, ptr(self.items),
-             ptr(self.num_items), self.max_items, None, ptr(self.down), stream)
+             ptr(self.num_items), self.max_items, self.exact_routes, None, ptr(self.down),
+             stream)
         return self.down
 
 

@@ -140,6 +140,9 @@ int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);
  *   mode 1 (FC2): sorted position p of a [max_rows, K],
  *                 output fp32 at pair sorted_ids[p]: out_f32[pair, N]
  *                 (scatter = unpermute).
+ * Items with <= exact_routes routes contract on bf16 MFMAs after an exact
+ * FP8 -> bf16 widening (fp32-accurate sums); larger items use FP8 MFMAs,
+ * whose in-instruction product alignment rounds at ~1e-4 of sum|products|.
  * Work items cover live routes only, so padding slots are never read.
  * The grid is max_items x (N / row tile); items at or beyond *num_items exit.
  * Supported: K in {256, 512, 768, 1024, 1536, 2048}; N a multiple of the
@@ -148,8 +151,8 @@ int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);
 int d3_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32_t num_experts,
                    int32_t n, int32_t k, const uint8_t *a, const float *a_scales,
                    const int32_t *sorted_ids, int32_t top_k, const int32_t *items,
-                   const int32_t *num_items, int32_t max_items, uint16_t *out_bf16,
-                   float *out_f32, void *stream);
+                   const int32_t *num_items, int32_t max_items, int32_t exact_routes,
+                   uint16_t *out_bf16, float *out_f32, void *stream);
 
 /*
  * A10  SwiGLU + per-128 FP8 requantisation of FC1 rows.

@@ -9,15 +9,25 @@ import torch
 from oracle import moe as om
 from oracle.numerics import bf16_to_f32
 
-# bf16 outputs of the expert FFN: the reference's own threshold for
-# same-quantisation implementations (scripts/benchmark_native_moe.py:50,
-# tune_prefill_moe.py:89) is RRMS < 0.003.  The device path differs from the
-# oracle only by fp32 accumulation order, so it is held to a tighter bound
-# as well: RRMS < 1e-3 and every element within 2 bf16 ulps of the oracle or
-# 2^-6 of the row RMS (FP8 requantisation flips at 2^-4 relative steps touch
-# single activation bytes; their effect on an output is bounded by this).
+# Tolerances of the bf16 expert outputs against the exact-arithmetic oracle.
+#
+# Exact path (work items with <= EXACT_ROUTES routes: every decode config):
+# bf16 MFMAs on exactly widened FP8 operands, fp32-accurate sums.  It differs
+# from the oracle only by fp32 summation order, which occasionally moves a
+# bf16 rounding (1 ulp) and, more rarely, an FP8 requantisation byte of the
+# SwiGLU activation (one e4m3 step, 2^-3 relative, of one of I terms).  Bound:
+# RRMS < 1e-3 and every element within 2 bf16 ulps or 2^-6 of the row RMS.
+#
+# FP8 contraction path (larger items: prefill and mixed batches): FP8 MFMAs
+# round the aligned products at ~1e-4 of sum|products| per instruction, as
+# FP8 tensor-core GEMMs do.  Bound: the reference's own threshold for
+# same-quantisation implementations, RRMS < 0.003
+# (scripts/benchmark_native_moe.py:50, tune_prefill_moe.py:89), and every
+# element within 4 ulps or 2^-3 of the row RMS.
 RRMS_REFERENCE = 3e-3
 RRMS_TIGHT = 1e-3
+EXACT = dict(ulps=2, row_floor=2.0 ** -6, rrms_max=RRMS_TIGHT)
+CONTRACTION = dict(ulps=4, row_floor=2.0 ** -3, rrms_max=RRMS_REFERENCE)
 
 
 def np_bf16(t: torch.Tensor) -> np.ndarray:
@@ -43,6 +53,12 @@ def rrms(actual: np.ndarray, expected: np.ndarray) -> float:
     return float(np.sqrt(np.mean((a - e) ** 2) / max(np.mean(e ** 2), 1e-30)))
 
 
+def bf16_ulp(values: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 numbers at each value (normal range)."""
+    mag = np.maximum(np.abs(values.astype(np.float64)), 2.0 ** -126)
+    return np.exp2(np.floor(np.log2(mag)) - 7)
+
+
 def assert_bf16_close(actual_bits: np.ndarray, expected_bits: np.ndarray, ulps: int = 2,
                       row_floor: float = 2.0 ** -6, rrms_max: float = RRMS_TIGHT) -> dict:
     a = bf16_to_f32(actual_bits).astype(np.float64)
@@ -50,7 +66,7 @@ def assert_bf16_close(actual_bits: np.ndarray, expected_bits: np.ndarray, ulps: 
     err = rrms(a, e)
     assert err < rrms_max, f"RRMS {err:.3g} >= {rrms_max}"
     row_rms = np.sqrt(np.mean(e ** 2, axis=-1, keepdims=True))
-    bound = np.abs(e) * ulps * 2.0 ** -8 + row_floor * row_rms
+    bound = bf16_ulp(e) * ulps + row_floor * row_rms
     bad = np.abs(a - e) > bound
     assert not bad.any(), f"{int(bad.sum())} elements outside tolerance; worst {np.abs(a - e).max()}"
     return {"rrms": err, "max_abs": float(np.abs(a - e).max()),

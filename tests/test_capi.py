@@ -72,8 +72,8 @@ def test_contract_violations_raise_value_error(lib):
         _lib.call("d3_sort_routes", 16, 3, 4, None, 8, 16, 16, 16, 16, 16, 16, 16, 8, None, 16,
                   None, 0, None, None, None)
     with pytest.raises(ValueError, match="K="):
-        _lib.call("d3_expert_gemm", 0, 16, 16, 4, 512, 384, 16, 16, 16, 8, 16, 16, 4, 16, None,
-                  None)
+        _lib.call("d3_expert_gemm", 0, 16, 16, 4, 512, 384, 16, 16, 16, 8, 16, 16, 4, 64, 16,
+                  None, None)
     assert "K=" in lib.d3_last_error().decode()
 
 

@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import RRMS_REFERENCE, assert_bf16_close, np_bf16, np_f32, oracle_weights, rrms
+from helpers import (CONTRACTION, EXACT, RRMS_REFERENCE, assert_bf16_close, np_bf16, np_f32,
+                     oracle_weights, rrms)
 from oracle import moe as om
 from oracle.numerics import bf16_to_f32
 
@@ -53,8 +54,8 @@ def test_decode_configs(device, config):
     weights, ids = om.route(logits)
     check_integer_state(ds.workspace, ids, w.num_experts, n)
     expected = om.expert_ffn(x, ids, weights, oracle_weights(w.experts))
-    stats = assert_bf16_close(np_bf16(out)[:n], expected)
-    assert stats["rrms"] < RRMS_REFERENCE
+    # decode items never exceed the exact-path route limit (rows <= 64)
+    stats = assert_bf16_close(np_bf16(out)[:n], expected, **EXACT)
     print(f"config {config}: rows {n} {stats}")
 
 
@@ -87,7 +88,7 @@ def test_prefill_with_shared_expert(device):
     sw = oracle_weights(w.shared)
     shared_expected = om.dense_ffn(np_bf16(x), sw.w13[0], sw.s13[0], sw.w2[0], sw.s2[0])
     expected = om.add_shared(routed, shared_expected)
-    stats = assert_bf16_close(np_bf16(out), expected)
+    stats = assert_bf16_close(np_bf16(out), expected, **CONTRACTION)
     print(f"config 4: rows {rows} {stats}")
 
 
@@ -140,7 +141,7 @@ def test_mixed_batching_sequence(device):
         weights, ids = om.route(np_f32(logits))
         check_integer_state(ws, ids, w.num_experts, capacity)
         expected = om.expert_ffn(np_bf16(x), ids, weights, wt)
-        stats = assert_bf16_close(np_bf16(out), expected)
+        stats = assert_bf16_close(np_bf16(out), expected, **CONTRACTION)
         print(f"config 5 step {index}: {stats}")
 
 
@@ -182,7 +183,7 @@ def test_decode_step_graph_replays(device):
         if n:
             weights, ids = om.route(np_f32(step.logits_slots)[active])
             expected = om.expert_ffn(np_bf16(step.x_slots)[active], ids, weights, wt)
-            assert_bf16_close(got[:n], expected)
+            assert_bf16_close(got[:n], expected, **EXACT)
 
 
 def test_reference_api_small_and_native(device):
@@ -201,5 +202,5 @@ def test_reference_api_small_and_native(device):
     assert torch.equal(a, b)
     ow, oids = om.route(np_f32(logits))
     expected = om.expert_ffn(np_bf16(x), oids, ow, oracle_weights(w.experts))
-    assert_bf16_close(np_bf16(a), expected)
+    assert_bf16_close(np_bf16(a), expected, **EXACT)
     assert rrms(bf16_to_f32(np_bf16(a)), bf16_to_f32(expected)) < RRMS_REFERENCE
