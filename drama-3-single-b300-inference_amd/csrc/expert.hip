@@ -350,9 +350,8 @@ using namespace d3;
 extern "C" int d3_expert_gemm(int32_t mode, const uint8_t* w, const float* ws, int32_t num_experts,
                               int32_t n, int32_t k, const uint8_t* a, const float* a_scales,
                               const int32_t* sorted_ids, int32_t top_k, const int32_t* items,
-                              const int32_t* num_items, int32_t exact_routes,
-                              int32_t max_items, uint16_t* out_bf16, float* out_f32,
-                              void* stream) {
+                              const int32_t* num_items, int32_t max_items, int32_t exact_routes,
+                              uint16_t* out_bf16, float* out_f32, void* stream) {
   D3_REQUIRE(mode == 0 || mode == 1, "expert_gemm: mode must be 0 (FC1) or 1 (FC2)");
   D3_REQUIRE(w && ws && a && a_scales && sorted_ids && items && num_items,
              "expert_gemm: null pointer");

@@ -31,6 +31,32 @@ def lib():
     return _lib.load()
 
 
+def _params(signature: str):
+    names = []
+    for param in signature.split(","):
+        param = param.strip()
+        if param in ("", "void"):
+            continue
+        names.append(re.findall(r"(\w+)\s*$", param)[0])
+    return names
+
+
+def test_definitions_match_header_parameter_order():
+    """Same-typed parameters in a different order compile silently; compare
+    the names of every extern "C" definition with its declaration."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    declared = {m.group(1): _params(m.group(2)) for m in re.finditer(
+        r"\b(?:int|int32_t|const char \*)\s*(d3_\w+)\s*\(([^)]*)\)\s*;", text)}
+    defined = {}
+    for src in (ROOT / "drama-3-single-b300-inference_amd" / "csrc").glob("*.*"):
+        for m in re.finditer(r'extern "C" (?:int|int32_t|const char\*) (d3_\w+)\(([^)]*)\)\s*\{',
+                             src.read_text()):
+            defined[m.group(1)] = _params(m.group(2))
+    assert set(defined) == set(declared)
+    for name, params in declared.items():
+        assert defined[name] == params, name
+
+
 def test_header_declares_the_boundary():
     names = declared_functions()
     for required in ("d3_compact_slots", "d3_route", "d3_quantize_rows", "d3_prepare_moe_input",
