@@ -122,7 +122,40 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   const int group = lane >> 4;
   const int n0 = (blockIdx.x % tiles) * kRowsPerGroup + wave * kRowsPerWave;
 
-  // Weights for the whole contraction, issued before any dependent work.
+  // The first route tile's activation rows are fetched before the weights:
+  // memory returns are counted in issue order, so staging issued behind the
+  // weights would wait for all of them before the first MFMA.
+  const int stage_col = threadIdx.x >> 4;   // route column staged by this thread
+  const int stage_part = threadIdx.x & 15;  // 16 threads per route row
+  constexpr int kChunks = K / 256;          // 16-byte chunks per thread and row
+  int4 b_stage[kChunks];
+  float b_stage_scale = 0.0f;
+  int b_stage_target = -1;
+  auto fetch_tile = [&](int m0) {
+    const int r = m0 + stage_col;
+    const bool live = r < routes;
+    const int position = first + r;
+    const int pair = live ? sorted_ids[position] : 0;
+    const size_t a_row = MODE == 0 ? static_cast<size_t>(pair / top_k) : static_cast<size_t>(position);
+    const uint8_t* src = act + a_row * K;
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) {
+      b_stage[j] = make_int4(0, 0, 0, 0);
+      if (live) b_stage[j] = *reinterpret_cast<const int4*>(src + j * 256 + stage_part * 16);
+    }
+    b_stage_scale = (live && stage_part < KB) ? act_scales[a_row * KB + stage_part] : 0.0f;
+    b_stage_target = live ? (MODE == 0 ? position : pair) : -1;
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j)
+      *reinterpret_cast<int4*>(b_tile + stage_col * kStride + j * 256 + stage_part * 16) = b_stage[j];
+    if (stage_part < KB) b_scales[stage_col * KB + stage_part] = b_stage_scale;
+    if (stage_part == 0) b_target[stage_col] = b_stage_target;
+  };
+  fetch_tile(0);
+
+  // Weights for the whole contraction: the bulk of the HBM stream.
   const uint8_t* wexp = w + static_cast<size_t>(expert) * n_rows * K;
   int32x8 a_frag[RT][KB];
 #pragma unroll
@@ -138,27 +171,12 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) w_scale[rt][kb] = wsexp[((n0 + rt * 16) / kGroup) * KB + kb];
 
-  const int stage_col = threadIdx.x >> 4;   // route column staged by this thread
-  const int stage_part = threadIdx.x & 15;  // 16 threads per route row
   for (int m0 = 0; m0 < routes; m0 += 16) {
-    __syncthreads();  // previous tile fully consumed
-    {
-      const int r = m0 + stage_col;
-      const bool live = r < routes;
-      const int position = first + r;
-      const int pair = live ? sorted_ids[position] : 0;
-      const size_t a_row = MODE == 0 ? static_cast<size_t>(pair / top_k) : static_cast<size_t>(position);
-      const uint8_t* src = act + a_row * K;
-#pragma unroll
-      for (int j = 0; j < K / 256; ++j) {
-        const int offset = j * 256 + stage_part * 16;
-        int4 v = make_int4(0, 0, 0, 0);
-        if (live) v = *reinterpret_cast<const int4*>(src + offset);
-        *reinterpret_cast<int4*>(b_tile + stage_col * kStride + offset) = v;
-      }
-      if (stage_part < KB) b_scales[stage_col * KB + stage_part] = live ? act_scales[a_row * KB + stage_part] : 0.0f;
-      if (stage_part == 0) b_target[stage_col] = live ? (MODE == 0 ? position : pair) : -1;
+    if (m0 > 0) {
+      __syncthreads();  // previous tile fully consumed
+      fetch_tile(m0);
     }
+    store_tile();
     __syncthreads();
 
     floatx4 acc[RT];

@@ -7,6 +7,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "route_sort.h"
 #include "status.h"
 
 namespace d3 {
@@ -64,19 +65,13 @@ __device__ __forceinline__ uint32_t route_key(float value, int column) {
   return (ordered & 0xffff0000u) | (65535u - static_cast<uint32_t>(column));
 }
 
+// Routes one row (one wave): top-k ids of the row at `base` (E <= 64 * NPL)
+// into ids[out_row * top_k + rank], weights likewise.
 template <int NPL, bool kF32>
-__global__ __launch_bounds__(kFrontThreads) void route_kernel(
-    const void* __restrict__ logits, int64_t stride, int rows, int num_experts, int top_k,
-    const int32_t* __restrict__ row_index, const int32_t* __restrict__ row_count,
-    int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, void* __restrict__ weights,
-    int weights_f32) {
-  const int row = (blockIdx.x * kFrontThreads + threadIdx.x) / kWave;
+__device__ __forceinline__ void route_row(const char* base, int num_experts, int top_k,
+                                          int64_t out_row, int32_t* ids32, int64_t* ids64,
+                                          void* weights, int weights_f32) {
   const int lane = lane_id();
-  if (row >= live_rows(row_count, rows)) return;  // uniform per wave
-  const int source = row_index != nullptr ? row_index[row] : row;
-  const char* base = static_cast<const char*>(logits) +
-                     static_cast<int64_t>(source) * stride * (kF32 ? 4 : 2);
-
   float values[NPL];
   uint32_t keys[NPL];
   float row_max = -INFINITY;
@@ -113,7 +108,7 @@ __global__ __launch_bounds__(kFrontThreads) void route_kernel(
   if (lane < top_k) probability = expf(load_logit<kF32>(base, selected) - row_max) / denominator;
   const float total = segment_sum<kWave>(probability);
   if (lane < top_k) {
-    const int64_t out = static_cast<int64_t>(row) * top_k + lane;
+    const int64_t out = out_row * top_k + lane;
     const float weight = probability / total;
     if (ids32 != nullptr) ids32[out] = selected;
     if (ids64 != nullptr) ids64[out] = selected;
@@ -124,32 +119,44 @@ __global__ __launch_bounds__(kFrontThreads) void route_kernel(
   }
 }
 
+template <int NPL, bool kF32>
+__global__ __launch_bounds__(kFrontThreads) void route_kernel(
+    const void* __restrict__ logits, int64_t stride, int rows, int num_experts, int top_k,
+    const int32_t* __restrict__ row_index, const int32_t* __restrict__ row_count,
+    int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, void* __restrict__ weights,
+    int weights_f32) {
+  const int row = (blockIdx.x * kFrontThreads + threadIdx.x) / kWave;
+  if (row >= live_rows(row_count, rows)) return;  // uniform per wave
+  const int source = row_index != nullptr ? row_index[row] : row;
+  const char* base = static_cast<const char*>(logits) +
+                     static_cast<int64_t>(source) * stride * (kF32 ? 4 : 2);
+  route_row<NPL, kF32>(base, num_experts, top_k, row, ids32, ids64, weights, weights_f32);
+}
+
 // ---------------------------------------------------------------------------
 // Quantisation: one wave per row; 8 elements per lane, 16 lanes per group.
 // ---------------------------------------------------------------------------
-template <bool kPrepare>
-__global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
-    const uint16_t* __restrict__ x, int64_t stride, int rows, int width,
-    const int32_t* __restrict__ row_index, const int32_t* __restrict__ row_count,
-    uint8_t* __restrict__ q, float* __restrict__ scales, int transposed,
-    // prepare_moe_input extras
-    const void* __restrict__ router, int router_f32, int64_t router_stride, int num_experts,
-    const void* __restrict__ row_slots, int row_slots_i64, int64_t padding_start,
-    float* __restrict__ logits_out) {
-  const int row = (blockIdx.x * kFrontThreads + threadIdx.x) / kWave;
+constexpr int kMaxRowChunks = 8;  // rows up to 8 * 512 = 4096 elements
+
+// Quantises one row (one wave) of `width` bf16 values: q row + per-128 scales
+// at scales[group * scale_stride].  All loads of the row are issued before
+// any arithmetic so the row costs one memory latency.
+__device__ __forceinline__ void quantize_row(const uint16_t* in, int width, uint8_t* out,
+                                             float* scales, int64_t scale_stride) {
   const int lane = lane_id();
-  const int live = live_rows(row_count, rows);
-  if (row >= live) return;
-  const int source = row_index != nullptr ? row_index[row] : row;
-  const uint16_t* in = x + static_cast<int64_t>(source) * stride;
-  uint8_t* out = q + static_cast<int64_t>(row) * width;
-  const int groups = width / kGroup;
-  for (int base = 0; base < width; base += 8 * kWave) {
-    const int column = base + lane * 8;
+  uint4 raw[kMaxRowChunks];
+#pragma unroll
+  for (int c = 0; c < kMaxRowChunks; ++c) {
+    const int column = c * 8 * kWave + lane * 8;
+    raw[c] = make_uint4(0u, 0u, 0u, 0u);
+    if (column < width) raw[c] = *reinterpret_cast<const uint4*>(in + column);
+  }
+#pragma unroll
+  for (int c = 0; c < kMaxRowChunks; ++c) {
+    const int column = c * 8 * kWave + lane * 8;
+    if (c * 8 * kWave >= width) break;  // uniform
     const bool inside = column < width;  // whole 16-lane groups agree
-    uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-    if (inside) raw = *reinterpret_cast<const uint4*>(in + column);
-    const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+    const uint32_t words[4] = {raw[c].x, raw[c].y, raw[c].z, raw[c].w};
     float v[8];
     float amax = 0.0f;
 #pragma unroll
@@ -168,15 +175,30 @@ __global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
     }
     if (inside) {
       *reinterpret_cast<uint2*>(out + column) = make_uint2(lo, hi);
-      if ((lane & 15) == 0) {
-        const int group = column / kGroup;
-        if (transposed)
-          scales[static_cast<int64_t>(group) * rows + row] = scale;
-        else
-          scales[static_cast<int64_t>(row) * groups + group] = scale;
-      }
+      if ((lane & 15) == 0) scales[static_cast<int64_t>(column / kGroup) * scale_stride] = scale;
     }
   }
+}
+
+template <bool kPrepare>
+__global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
+    const uint16_t* __restrict__ x, int64_t stride, int rows, int width,
+    const int32_t* __restrict__ row_index, const int32_t* __restrict__ row_count,
+    uint8_t* __restrict__ q, float* __restrict__ scales, int transposed,
+    // prepare_moe_input extras
+    const void* __restrict__ router, int router_f32, int64_t router_stride, int num_experts,
+    const void* __restrict__ row_slots, int row_slots_i64, int64_t padding_start,
+    float* __restrict__ logits_out) {
+  const int row = (blockIdx.x * kFrontThreads + threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int live = live_rows(row_count, rows);
+  if (row >= live) return;
+  const int source = row_index != nullptr ? row_index[row] : row;
+  const int groups = width / kGroup;
+  quantize_row(x + static_cast<int64_t>(source) * stride, width,
+               q + static_cast<int64_t>(row) * width,
+               transposed ? scales + row : scales + static_cast<int64_t>(row) * groups,
+               transposed ? rows : 1);
   if constexpr (kPrepare) {
     // Reserved padding rows reuse row 0's routing (moe_input.py:31-37).
     int router_row = row;
@@ -192,6 +214,103 @@ __global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
                                      : bf16_to_f32(reinterpret_cast<const uint16_t*>(src)[column]);
       logits_out[static_cast<int64_t>(row) * num_experts + column] = value;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused front end of one MoE step: slot compaction + routing + quantisation
+// (4 rows per workgroup, one per wave) and, in the last workgroup to finish,
+// the route sort.  The last workgroup is found with an atomic ticket after a
+// release fence; nobody waits, so the launch cannot deadlock, and the last
+// workgroup resets the ticket so the next launch (or graph replay) starts at 0.
+// ---------------------------------------------------------------------------
+constexpr int kMaxFrontExperts = 512;
+constexpr int kFrontSortInts = sort_shared_ints(kFrontThreads, kMaxFrontExperts);
+
+struct FrontArgs {
+  const uint8_t* occupancy;
+  int num_slots;
+  int32_t* active;
+  int32_t* count;
+  const uint16_t* x;
+  int64_t x_stride;
+  const void* logits;
+  int64_t logits_stride;
+  int rows;
+  const int32_t* row_index;
+  const int32_t* row_count;
+  int hidden;
+  int num_experts;
+  int top_k;
+  int32_t* ids;
+  void* weights;
+  int weights_f32;
+  uint8_t* q;
+  float* scales;
+  int tile;
+  int item_rows;
+  SortOutputs sort;
+  int32_t* ticket;
+};
+
+template <int NPL, bool kF32, bool kSort>
+__global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
+  __shared__ int smem[kSort ? kFrontSortInts : 1];
+  __shared__ int ticket_shared;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int row = blockIdx.x * (kFrontThreads / kWave) + wave;
+
+  int live;
+  int source = -1;
+  if (a.occupancy != nullptr) {
+    // Every wave scans the occupancy (a few ballots) to find the count and
+    // the slot of its row; workgroup 0 also writes the ascending slot list.
+    int running = 0;
+    for (int base = 0, chunk = 0; base < a.num_slots; base += kWave, ++chunk) {
+      const bool on = base + lane < a.num_slots && a.occupancy[base + lane] != 0;
+      const uint64_t mask = __ballot(on);
+      const int rank = __popcll(mask & lanemask_lt());
+      const int here = __popcll(mask);
+      if (row >= running && row < running + here) {
+        const uint64_t hit = __ballot(on && rank == row - running);
+        source = base + __ffsll(static_cast<unsigned long long>(hit)) - 1;
+      }
+      if (blockIdx.x == 0 && (chunk % (kFrontThreads / kWave)) == wave && on)
+        a.active[running + rank] = base + lane;
+      running += here;
+    }
+    live = running;
+    if (blockIdx.x == 0) {
+      for (int i = live + static_cast<int>(threadIdx.x); i < a.num_slots; i += kFrontThreads)
+        a.active[i] = -1;
+      if (threadIdx.x == 0) *a.count = live;
+    }
+  } else {
+    live = live_rows(a.row_count, a.rows);
+    if (row < live) source = a.row_index != nullptr ? a.row_index[row] : row;
+  }
+
+  if (row < live) {
+    const char* lbase = static_cast<const char*>(a.logits) +
+                        static_cast<int64_t>(source) * a.logits_stride * (kF32 ? 4 : 2);
+    route_row<NPL, kF32>(lbase, a.num_experts, a.top_k, row, a.ids, nullptr, a.weights,
+                         a.weights_f32);
+    quantize_row(a.x + static_cast<int64_t>(source) * a.x_stride, a.hidden,
+                 a.q + static_cast<int64_t>(row) * a.hidden,
+                 a.scales + static_cast<int64_t>(row) * (a.hidden / kGroup), 1);
+  }
+
+  if constexpr (kSort) {
+    __threadfence();  // release this workgroup's ids
+    __syncthreads();
+    if (threadIdx.x == 0) ticket_shared = atomicAdd(a.ticket, 1);
+    __syncthreads();
+    if (ticket_shared != static_cast<int>(gridDim.x) - 1) return;
+    __threadfence();  // acquire every other workgroup's ids
+    sort_routes_block<kFrontThreads, false>(a.ids, live * a.top_k, a.num_experts, a.tile,
+                                             a.item_rows, smem, a.sort);
+    if (threadIdx.x == 0) atomicExch(a.ticket, 0);
   }
 }
 
@@ -265,6 +384,7 @@ extern "C" int d3_quantize_rows(const uint16_t* x, int64_t x_row_stride, int32_t
   D3_REQUIRE(x && q && scales, "quantize_rows: null pointer");
   D3_REQUIRE(rows >= 0 && width > 0 && width % kGroup == 0,
              "quantize_rows: width %d must be a positive multiple of 128", width);
+  D3_SUPPORTED(width <= kMaxRowChunks * 8 * kWave, "quantize_rows: width %d > 4096", width);
   D3_REQUIRE(x_row_stride >= width && x_row_stride % 8 == 0 && aligned16(x),
              "quantize_rows: x rows must be 16-byte aligned (stride %% 8 == 0)");
   D3_REQUIRE(aligned16(q), "quantize_rows: q must be 16-byte aligned");
@@ -288,6 +408,7 @@ extern "C" int d3_prepare_moe_input(const uint16_t* x, int64_t x_row_stride, con
   D3_REQUIRE(x && router && q && scales && logits, "prepare_moe_input: null pointer");
   D3_REQUIRE(rows >= 0 && hidden > 0 && hidden % kGroup == 0,
              "prepare_moe_input: hidden %d must be a positive multiple of 128", hidden);
+  D3_SUPPORTED(hidden <= kMaxRowChunks * 8 * kWave, "prepare_moe_input: hidden %d > 4096", hidden);
   D3_REQUIRE(num_experts > 0 && router_row_stride >= num_experts,
              "prepare_moe_input: bad router shape");
   D3_REQUIRE(router_dtype == D3_DTYPE_BF16 || router_dtype == D3_DTYPE_F32,
@@ -309,4 +430,93 @@ extern "C" int d3_prepare_moe_input(const uint16_t* x, int64_t x_row_stride, con
                      num_experts, row_slots, row_slots_dtype == D3_DTYPE_I64 ? 1 : 0,
                      padding_start, logits);
   D3_LAUNCHED("prepare_moe_input");
+}
+
+extern "C" int d3_moe_front(const uint8_t* occupancy, int32_t num_slots, int32_t* active_slots,
+                            int32_t* count, const uint16_t* x, int64_t x_row_stride,
+                            const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                            int32_t rows, const int32_t* row_index, const int32_t* row_count,
+                            int32_t hidden, int32_t num_experts, int32_t top_k, int32_t* ids,
+                            void* weights, int32_t weights_dtype, uint8_t* q, float* scales,
+                            int32_t tile, int32_t item_rows, int32_t* counts, int32_t* starts,
+                            int32_t* total, int32_t* sorted_ids, int32_t* expert_ids,
+                            int32_t max_rows, int32_t* inverse, int32_t* items,
+                            int32_t max_items, int32_t* num_items, int32_t* pairs_out,
+                            int32_t* ticket, void* stream) {
+  D3_REQUIRE(x && logits && ids && weights && q && scales, "moe_front: null pointer");
+  D3_REQUIRE(logits_dtype == D3_DTYPE_BF16 || logits_dtype == D3_DTYPE_F32,
+             "moe_front: logits must be bf16 or f32");
+  D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
+             "moe_front: weights must be bf16 or f32");
+  if (occupancy != nullptr) {
+    D3_REQUIRE(active_slots && count, "moe_front: occupancy needs active_slots and count");
+    D3_REQUIRE(num_slots > 0 && num_slots <= 4096, "moe_front: num_slots %d not in [1, 4096]",
+               num_slots);
+    D3_REQUIRE(row_index == nullptr && row_count == nullptr,
+               "moe_front: occupancy excludes row_index / row_count");
+    rows = num_slots;
+  }
+  D3_REQUIRE(rows >= 0, "moe_front: negative rows");
+  D3_REQUIRE(hidden > 0 && hidden % kGroup == 0 && hidden <= kMaxRowChunks * 8 * kWave,
+             "moe_front: hidden %d must be a multiple of 128 up to 4096", hidden);
+  D3_REQUIRE(x_row_stride >= hidden && x_row_stride % 8 == 0 && aligned16(x) && aligned16(q),
+             "moe_front: x rows must be 16-byte aligned");
+  D3_SUPPORTED(num_experts >= 1 && num_experts <= kMaxFrontExperts,
+               "moe_front: num_experts %d not in [1, %d]", num_experts, kMaxFrontExperts);
+  D3_REQUIRE(top_k >= 1 && top_k <= 16 && top_k <= num_experts, "moe_front: bad top_k %d", top_k);
+  D3_REQUIRE(logits_row_stride >= num_experts, "moe_front: logits row stride < num_experts");
+  const bool sort = sorted_ids != nullptr;
+  SortOutputs out{};
+  if (sort) {
+    D3_REQUIRE(counts && starts && total && expert_ids && ticket, "moe_front: sort outputs");
+    D3_REQUIRE(tile >= 1 && tile <= 1024, "moe_front: bad tile %d", tile);
+    const int64_t pairs = static_cast<int64_t>(rows) * top_k;
+    D3_SUPPORTED(pairs <= 8192, "moe_front: %lld pairs exceed the fused sort (use d3_sort_routes)",
+                 static_cast<long long>(pairs));
+    const int32_t need = d3_max_sorted_rows(static_cast<int32_t>(pairs), num_experts, tile);
+    D3_REQUIRE(max_rows >= need && max_rows % tile == 0, "moe_front: max_rows %d < required %d",
+               max_rows, need);
+    if (items != nullptr) {
+      D3_REQUIRE(num_items != nullptr && item_rows >= tile && item_rows % tile == 0,
+                 "moe_front: items need num_items and item_rows a multiple of tile");
+      const int32_t need_items = d3_max_items(static_cast<int32_t>(pairs), num_experts, item_rows);
+      D3_REQUIRE(max_items >= need_items, "moe_front: max_items %d < required %d", max_items,
+                 need_items);
+    } else {
+      item_rows = tile;
+    }
+    out = SortOutputs{counts, starts, total, sorted_ids, expert_ids, max_rows, inverse,
+                      reinterpret_cast<int4*>(items), max_items, num_items, pairs_out};
+  }
+  if (rows == 0 && !sort && occupancy == nullptr) {
+    clear_error();
+    return D3_OK;
+  }
+  const FrontArgs args{occupancy, num_slots, active_slots, count, x, x_row_stride, logits,
+                       logits_row_stride, rows, row_index, row_count, hidden, num_experts, top_k,
+                       ids, weights, weights_dtype == D3_DTYPE_F32 ? 1 : 0, q, scales, tile,
+                       item_rows, out, ticket};
+  const dim3 grid(rows > 0 ? wave_blocks(rows) : 1), block(kFrontThreads);
+  hipStream_t s = as_stream(stream);
+  const bool f32 = logits_dtype == D3_DTYPE_F32;
+#define D3_FRONT_LAUNCH(NPL)                                                                  \
+  if (f32 && sort)                                                                            \
+    hipLaunchKernelGGL((moe_front_kernel<NPL, true, true>), grid, block, 0, s, args);         \
+  else if (f32)                                                                               \
+    hipLaunchKernelGGL((moe_front_kernel<NPL, true, false>), grid, block, 0, s, args);        \
+  else if (sort)                                                                              \
+    hipLaunchKernelGGL((moe_front_kernel<NPL, false, true>), grid, block, 0, s, args);        \
+  else                                                                                        \
+    hipLaunchKernelGGL((moe_front_kernel<NPL, false, false>), grid, block, 0, s, args);
+  if (num_experts <= 64) {
+    D3_FRONT_LAUNCH(1)
+  } else if (num_experts <= 128) {
+    D3_FRONT_LAUNCH(2)
+  } else if (num_experts <= 256) {
+    D3_FRONT_LAUNCH(4)
+  } else {
+    D3_FRONT_LAUNCH(8)
+  }
+#undef D3_FRONT_LAUNCH
+  D3_LAUNCHED("moe_front");
 }

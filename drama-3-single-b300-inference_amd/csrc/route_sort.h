@@ -1,0 +1,180 @@
+// Expert histogram, padded exclusive scan and stable route sort, as a
+// workgroup-level device function (any multiple of 64 threads up to 1024).
+//
+// Semantics (reference src/drama3/kernels.py:658-731):
+//   counts[e]  = #{p : ids[p] == e}
+//   starts[e]  = exclusive scan of counts padded to `tile`, *total = sum
+//   sorted_ids: pairs of expert e in ascending pair order at starts[e] + rank,
+//               padding up to the padded end (and everything from *total on)
+//               holds the sentinel `pairs`
+//   expert_ids: expert of each tile, -1 from *total / tile on
+// plus the unpermute map inverse[p] and work items {e, start, routes, 0}
+// covering each expert's routes in chunks of item_rows.
+//
+// The stable scatter needs, for every pair, the number of earlier pairs of
+// the same expert.  Each wave finds the lanes holding the same expert with
+// one ballot per expert-id bit (lanes agree on every bit <=> same expert), so
+// a lane's rank inside its wave is a popcount; per-wave counts in LDS give the
+// rank inside a chunk and a running per-expert base carries it across chunks.
+// Everything is integer, so the result does not depend on scheduling.
+#pragma once
+
+#include "common.h"
+
+namespace d3 {
+
+// LDS ints needed by sort_routes_block for `threads` threads and E experts.
+constexpr int sort_shared_ints(int threads, int experts) {
+  return (4 + threads / kWave) * experts + threads / kWave;
+}
+
+template <bool kI64>
+__device__ __forceinline__ int load_route_id(const void* ids, int p) {
+  if constexpr (kI64) return static_cast<int>(static_cast<const int64_t*>(ids)[p]);
+  return static_cast<const int32_t*>(ids)[p];
+}
+
+// Inclusive scan of one int per thread across the workgroup; *total gets the sum.
+template <int THREADS>
+__device__ __forceinline__ int block_inclusive_scan(int value, int* wave_totals, int* total) {
+  constexpr int kWaves = THREADS / kWave;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int offset = 1; offset < kWave; offset <<= 1) {
+    const int other = __shfl_up(value, offset);
+    if (lane >= offset) value += other;
+  }
+  if (lane == kWave - 1) wave_totals[wave] = value;
+  __syncthreads();
+  int prefix = 0;
+  int sum = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    prefix += w < wave ? wave_totals[w] : 0;
+    sum += wave_totals[w];
+  }
+  __syncthreads();  // wave_totals is reused by the next scan
+  *total = sum;
+  return value + prefix;
+}
+
+struct SortOutputs {
+  int32_t* counts;
+  int32_t* starts;
+  int32_t* total;
+  int32_t* sorted_ids;
+  int32_t* expert_ids;
+  int max_rows;
+  int32_t* inverse;  // optional
+  int4* items;       // optional
+  int max_items;
+  int32_t* num_items;  // optional
+  int32_t* pairs_out;  // optional
+};
+
+// All THREADS threads of the workgroup must call this (it synchronises).
+// num_experts <= THREADS; `smem` holds sort_shared_ints(THREADS, E) ints.
+template <int THREADS, bool kI64>
+__device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int num_experts,
+                                  int tile, int item_rows, int* smem, const SortOutputs& out) {
+  constexpr int kWaves = THREADS / kWave;
+  int* counts = smem;                           // [E]
+  int* starts = counts + num_experts;           // [E]
+  int* running = starts + num_experts;          // [E]
+  int* first_item = running + num_experts;      // [E]
+  int* wave_counts = first_item + num_experts;  // [kWaves][E]
+  int* wave_totals = wave_counts + kWaves * num_experts;  // [kWaves]
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+
+  for (int e = tid; e < num_experts; e += THREADS) {
+    counts[e] = 0;
+    running[e] = 0;
+  }
+  for (int i = tid; i < kWaves * num_experts; i += THREADS) wave_counts[i] = 0;
+  __syncthreads();
+
+  for (int p = tid; p < pairs; p += THREADS) {
+    const int e = load_route_id<kI64>(ids, p);
+    if (e >= 0 && e < num_experts) atomicAdd(&counts[e], 1);
+  }
+  __syncthreads();
+
+  // Padded exclusive scan and work-item offsets: one expert per thread.
+  const int count = tid < num_experts ? counts[tid] : 0;
+  const int padded = (count + tile - 1) / tile * tile;
+  int total = 0;
+  const int start = block_inclusive_scan<THREADS>(padded, wave_totals, &total) - padded;
+  const int my_items = (count + item_rows - 1) / item_rows;
+  int total_items = 0;
+  const int item_base = block_inclusive_scan<THREADS>(my_items, wave_totals, &total_items) - my_items;
+  if (tid < num_experts) {
+    starts[tid] = start;
+    first_item[tid] = item_base;
+  }
+  __syncthreads();
+
+  int bits = 0;
+  while ((1 << bits) < num_experts) ++bits;
+  const uint64_t below = lanemask_lt();
+  for (int chunk = 0; chunk < pairs; chunk += THREADS) {
+    const int p = chunk + tid;
+    const int e = p < pairs ? load_route_id<kI64>(ids, p) : -1;
+    const bool valid = e >= 0 && e < num_experts;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < bits; ++b) {
+      const bool bit = valid && ((e >> b) & 1);
+      const uint64_t set = __ballot(bit);
+      peers &= bit ? set : ~set;
+    }
+    const int rank = __popcll(peers & below);
+    const bool leader = valid && rank == 0;
+    if (leader) wave_counts[wave * num_experts + e] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int position = starts[e] + running[e] + rank;
+      for (int w = 0; w < wave; ++w) position += wave_counts[w * num_experts + e];
+      out.sorted_ids[position] = p;
+      if (out.inverse != nullptr) out.inverse[p] = position;
+    } else if (p < pairs && out.inverse != nullptr) {
+      out.inverse[p] = -1;
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&running[e], __popcll(peers));
+      wave_counts[wave * num_experts + e] = 0;
+    }
+    __syncthreads();
+  }
+
+  for (int e = tid; e < num_experts; e += THREADS) {
+    const int c = counts[e];
+    const int s = starts[e];
+    const int pad = (c + tile - 1) / tile * tile;
+    for (int i = c; i < pad; ++i) out.sorted_ids[s + i] = pairs;
+    for (int b = 0; b < pad / tile; ++b) out.expert_ids[s / tile + b] = e;
+    out.counts[e] = c;
+    out.starts[e] = s;
+    if (out.items != nullptr) {
+      const int n = (c + item_rows - 1) / item_rows;
+      for (int j = 0; j < n; ++j) {
+        const int routes = c - j * item_rows < item_rows ? c - j * item_rows : item_rows;
+        out.items[first_item[e] + j] = make_int4(e, s + j * item_rows, routes, 0);
+      }
+    }
+  }
+  for (int i = total + tid; i < out.max_rows; i += THREADS) out.sorted_ids[i] = pairs;
+  for (int i = total / tile + tid; i < out.max_rows / tile; i += THREADS) out.expert_ids[i] = -1;
+  if (out.items != nullptr)
+    for (int i = total_items + tid; i < out.max_items; i += THREADS)
+      out.items[i] = make_int4(-1, 0, 0, 0);
+  if (tid == 0) {
+    *out.total = total;
+    if (out.num_items != nullptr) *out.num_items = total_items;
+    if (out.pairs_out != nullptr) *out.pairs_out = pairs;
+  }
+}
+
+}  // namespace d3

@@ -45,6 +45,9 @@ SIGNATURES = {
     "d3_sort_routes": (
         _i32, [_p, _i32, _i32, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _i32, _p, _i32, _p,
                _i32, _p, _p, _p]),
+    "d3_moe_front": (
+        _i32, [_p, _i32, _p, _p, _p, _i64, _p, _i32, _i64, _i32, _p, _p, _i32, _i32, _i32, _p, _p,
+               _i32, _p, _p, _i32, _i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _p, _p, _p, _p]),
     "d3_max_sorted_rows": (_i32, [_i32, _i32, _i32]),
     "d3_max_items": (_i32, [_i32, _i32, _i32]),
     "d3_expert_gemm": (

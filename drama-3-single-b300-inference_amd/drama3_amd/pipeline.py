@@ -31,6 +31,9 @@ SORT_TILE = 16  # MFMA route tile; also the padding granularity of the sorted la
 # Work items with at most this many routes take the exact (bf16-MFMA) path of
 # the expert GEMM; larger items are real contractions and take FP8 MFMAs.
 EXACT_ROUTES = 64
+# Up to this many (row, rank) pairs the route sort runs inside the fused front
+# kernel (its last workgroup); larger batches use the 1024-thread sort kernel.
+FUSED_SORT_PAIRS = 8192
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -102,6 +105,7 @@ class MoEWorkspace:
         self.inverse = torch.empty(pairs, **i32)
         self.items = torch.empty((max(self.max_items, 1), 4), **i32)
         self.num_items = torch.empty(1, **i32)
+        self.ticket = torch.zeros(1, **i32)  # fused-sort ticket: 0 between launches
         self.gate_up = torch.empty((self.max_rows, 2 * i), dtype=torch.bfloat16, device=dev)
         self.act = torch.empty((self.max_rows, i), dtype=torch.uint8, device=dev)
         self.act_scales = torch.empty((self.max_rows, i // 128), dtype=torch.float32, device=dev)
@@ -131,6 +135,29 @@ class MoEWorkspace:
              ptr(self.sorted_ids), ptr(self.expert_ids), self.max_rows, ptr(self.inverse),
              self.item_rows, ptr(self.items), self.max_items, ptr(self.num_items),
              ptr(self.pairs_dev), stream)
+
+    def front(self, x, logits, row_index=None, row_count=None, occupancy=None, active=None,
+              count=None, stream=None) -> None:
+        """Route + quantise every live row, and sort the routes, in one launch
+        (two when the batch exceeds the fused sort).  With ``occupancy`` the
+        rows are the live slots (``active`` / ``count`` receive the list)."""
+        s, stream = self.shape, self._stream(stream)
+        fused = s.pairs <= FUSED_SORT_PAIRS
+        slots = occupancy.numel() if occupancy is not None else 0
+        if occupancy is not None and slots != s.rows:
+            raise ValueError("slot mode needs a workspace with one row per slot")
+        sort_args = ((ptr(self.counts), ptr(self.starts), ptr(self.total), ptr(self.sorted_ids),
+                      ptr(self.expert_ids), self.max_rows, ptr(self.inverse), ptr(self.items),
+                      self.max_items, ptr(self.num_items), ptr(self.pairs_dev), ptr(self.ticket))
+                     if fused else (None, None, None, None, None, 0, None, None, 0, None, None,
+                                    None))
+        call("d3_moe_front", ptr(occupancy), slots, ptr(active), ptr(count), ptr(x), x.stride(0),
+             ptr(logits), dtype_code(logits.dtype), logits.stride(0), s.rows, ptr(row_index),
+             ptr(row_count), s.hidden, s.num_experts, s.top_k, ptr(self.ids), ptr(self.weights),
+             dtype_code(self.weights.dtype), ptr(self.q), ptr(self.x_scales), self.tile,
+             self.item_rows, *sort_args, stream)
+        if not fused:
+            self.sort(None, count if occupancy is not None else row_count, stream)
 
     def fc1(self, experts, stream=None) -> None:
         s, stream = self.shape, self._stream(stream)
@@ -178,9 +205,16 @@ class MoEWorkspace:
         """Route + experts.  ``row_index`` gathers x / logits rows (slot
         compaction), ``row_count`` is the live row count on the device."""
         stream = _lib.stream(self.device) if stream is None else stream
-        self.route(logits, row_index, row_count, stream)
-        return self.experts_forward(x, self.ids, self.weights, experts, row_index, row_count,
-                                    shared, out, stream)
+        self.front(x, logits, row_index, row_count, stream=stream)
+        return self.experts(experts, row_count, shared, out, stream)
+
+    def experts(self, experts, row_count=None, shared=None, out=None, stream=None):
+        """FC1, SwiGLU requant, FC2 and combine over the routes sorted by front()."""
+        stream = _lib.stream(self.device) if stream is None else stream
+        self.fc1(experts, stream)
+        self.activation(stream)
+        self.fc2(experts, stream)
+        return self.combine(None, row_count, shared, out, stream)
 
 
 class DenseExpert:
@@ -248,6 +282,7 @@ class DecodeStep:
 
     def __call__(self, occupancy, x_slots, logits_slots, experts, stream=None) -> torch.Tensor:
         stream = _lib.stream(x_slots.device) if stream is None else stream
-        compact_slots(occupancy, self.active, self.count, stream)
-        return self.workspace.forward(x_slots, logits_slots, experts, row_index=self.active,
-                                      row_count=self.count, stream=stream)
+        ws = self.workspace
+        ws.front(x_slots, logits_slots, occupancy=occupancy, active=self.active,
+                 count=self.count, stream=stream)
+        return ws.experts(experts, self.count, stream=stream)

@@ -122,6 +122,34 @@ int d3_sort_routes(const void *ids, int32_t ids_dtype, int32_t rows, const int32
                    int32_t max_rows, int32_t *inverse, int32_t item_rows, int32_t *items,
                    int32_t max_items, int32_t *num_items, int32_t *pairs_out, void *stream);
 
+/*
+ * A1 + A3 + A4 + A5-A7  Fused front end of one MoE step (one launch).
+ * Replaces the engine's host-side slot filtering (src/drama3/engine.py:
+ * 637-647) followed by route / quantize_groups / expert_counts_kernel /
+ * expert_offsets_kernel / expert_scatter_kernel (kernels.py:360-383,
+ * 658-731; moe_input.py:24-27).  Results are those of d3_compact_slots,
+ * d3_route (ids int32), d3_quantize_rows (native scale layout) and
+ * d3_sort_routes, bit for bit.
+ * Rows: with occupancy != NULL the live slots of occupancy[num_slots] in
+ * ascending order (active_slots / *count written as d3_compact_slots; rows =
+ * num_slots, row_index and row_count must be NULL); otherwise rows r <
+ * (row_count ? *row_count : rows) reading source row row_index ? row_index[r]
+ * : r of x and logits.  Row r of ids / weights / q / scales is output row r.
+ * With sorted_ids != NULL the last workgroup to finish also sorts the routes
+ * (rows * top_k <= 8192); `ticket` is a device int32 that must hold 0 before
+ * the first launch and is left at 0 by every launch.
+ */
+int d3_moe_front(const uint8_t *occupancy, int32_t num_slots, int32_t *active_slots,
+                 int32_t *count, const uint16_t *x, int64_t x_row_stride, const void *logits,
+                 int32_t logits_dtype, int64_t logits_row_stride, int32_t rows,
+                 const int32_t *row_index, const int32_t *row_count, int32_t hidden,
+                 int32_t num_experts, int32_t top_k, int32_t *ids, void *weights,
+                 int32_t weights_dtype, uint8_t *q, float *scales, int32_t tile,
+                 int32_t item_rows, int32_t *counts, int32_t *starts, int32_t *total,
+                 int32_t *sorted_ids, int32_t *expert_ids, int32_t max_rows, int32_t *inverse,
+                 int32_t *items, int32_t max_items, int32_t *num_items, int32_t *pairs_out,
+                 int32_t *ticket, void *stream);
+
 /* Capacity helpers for d3_sort_routes (host-side arithmetic only). */
 int32_t d3_max_sorted_rows(int32_t pairs, int32_t num_experts, int32_t tile);
 int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);

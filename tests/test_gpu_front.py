@@ -1,0 +1,95 @@
+"""The fused front end (d3_moe_front: compaction + routing + quantisation +
+last-workgroup route sort) against the standalone kernels and the oracle,
+bit for bit, including repeated launches (the ticket must return to 0)."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import np_f32, np_u8
+from oracle import moe as om
+from oracle.numerics import bf16_to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(device, slots, hidden, experts, seed):
+    gen = torch.Generator("cpu").manual_seed(seed)
+    x = torch.randn((slots, hidden), generator=gen).to(torch.bfloat16)
+    logits = torch.randn((slots, experts), generator=gen).to(torch.bfloat16)
+    return x, logits, x.to(device), logits.to(device)
+
+
+def _state(ws, count):
+    t = int(ws.total.item())
+    return dict(ids=ws.ids.cpu().numpy()[:count], weights=ws.weights.cpu()[:count],
+                q=np_u8(ws.q)[:count], scales=np_f32(ws.x_scales)[:count],
+                counts=ws.counts.cpu().numpy(), starts=ws.starts.cpu().numpy(), total=t,
+                sorted=ws.sorted_ids.cpu().numpy().copy(), experts=ws.expert_ids.cpu().numpy().copy(),
+                inverse=ws.inverse.cpu().numpy()[:count * 8], items=ws.items.cpu().numpy().copy(),
+                num_items=int(ws.num_items.item()), pairs=int(ws.pairs_dev.item()))
+
+
+@pytest.mark.parametrize("hidden,experts,p", [(1024, 16, 0.07), (2048, 128, 0.75), (1024, 16, 1.0),
+                                              (2048, 256, 0.5), (1024, 16, 0.0)])
+def test_fused_front_matches_standalone_kernels(device, hidden, experts, p):
+    from drama3_amd.pipeline import MoEWorkspace, Shape, compact_slots
+
+    slots = 64
+    x, logits, xd, ld = _inputs(device, slots, hidden, experts, int(p * 100) + experts)
+    occ = (np.random.default_rng(experts).uniform(size=slots) < p).astype(np.uint8)
+    occ_d = torch.from_numpy(occ).to(device)
+    fused = MoEWorkspace(Shape(slots, experts, hidden, 256), device)
+    active = torch.empty(slots, dtype=torch.int32, device=device)
+    count = torch.empty(1, dtype=torch.int32, device=device)
+    for launch in range(3):  # the ticket must be back to 0 after every launch
+        fused.front(xd, ld, occupancy=occ_d, active=active, count=count)
+        torch.cuda.synchronize()
+        assert int(fused.ticket.item()) == 0
+    n = int(count.item())
+    o_active, on = om.compact_slots(occ)
+    assert n == on and np.array_equal(active.cpu().numpy()[:n], o_active)
+    assert np.all(active.cpu().numpy()[n:] == -1)
+
+    ref = MoEWorkspace(Shape(slots, experts, hidden, 256), device)
+    a2 = torch.empty_like(active)
+    c2 = torch.empty_like(count)
+    compact_slots(occ_d, a2, c2)
+    ref.route(ld, a2, c2)
+    ref.quantize(xd, a2, c2)
+    ref.sort(None, c2)
+    torch.cuda.synchronize()
+    got, want = _state(fused, n), _state(ref, n)
+    for key in got:
+        if key == "weights":
+            assert torch.equal(got[key], want[key])
+        elif key == "items":
+            assert np.array_equal(got[key][:got["num_items"]], want[key][:want["num_items"]])
+        else:
+            assert np.array_equal(np.asarray(got[key]), np.asarray(want[key])), key
+    if n:
+        weights, ids = om.route(np_f32(logits)[o_active])
+        assert np.array_equal(got["ids"], ids)
+        q, s = om.quantize_rows(bf16_to_f32(x.view(torch.int16).numpy().view(np.uint16))[o_active])
+        assert np.array_equal(got["q"], q) and np.array_equal(got["scales"], s)
+
+
+def test_fused_front_row_mode_with_index(device):
+    """Row mode (mixed batches): row_index gathers rows, the sort is fused
+    while pairs <= 8192 and falls back to the sort kernel beyond."""
+    from drama3_amd.pipeline import MoEWorkspace, Shape
+
+    for rows in (560, 1100):  # 4480 pairs (fused) and 8800 pairs (standalone sort)
+        x, logits, xd, ld = _inputs(device, rows + 7, 1024, 16, rows)
+        index = torch.from_numpy(np.random.default_rng(rows).permutation(rows + 7)[:rows]).to(torch.int32)
+        ws = MoEWorkspace(Shape(rows, 16, 1024, 256), device)
+        ws.front(xd, ld, row_index=index.to(device))
+        torch.cuda.synchronize()
+        idx = index.numpy()
+        weights, ids = om.route(np_f32(logits)[idx])
+        assert np.array_equal(ws.ids.cpu().numpy(), ids)
+        o = om.sort_routes(ids, 16, ws.tile)
+        assert int(ws.total.item()) == o.total
+        assert np.array_equal(ws.sorted_ids.cpu().numpy()[:o.total], o.sorted_ids)
+        assert np.array_equal(ws.inverse.cpu().numpy(), o.inverse)
+        assert int(ws.ticket.item()) == 0

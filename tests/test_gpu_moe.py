@@ -73,14 +73,9 @@ def test_prefill_with_shared_expert(device):
     dense = DenseExpert(rows, w.hidden, w.shared.intermediate, device)
     experts, shared = w.experts.to(device), w.shared.to(device)
     xd, ld = x.to(device), logits.to(device)
-    ws.route(ld)
-    ws.quantize(xd)
+    ws.front(xd, ld)  # 29k pairs: fused route + quantise, then the sort kernel
     shared_y = dense.forward(ws.q, ws.x_scales, shared)
-    ws.sort()
-    ws.fc1(experts)
-    ws.activation()
-    ws.fc2(experts)
-    out = ws.combine(shared=shared_y)
+    out = ws.experts(experts, shared=shared_y)
     torch.cuda.synchronize()
     weights, ids = om.route(np_f32(logits))
     check_integer_state(ws, ids, w.num_experts, rows)

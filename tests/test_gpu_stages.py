@@ -201,11 +201,12 @@ def test_fc1_stage(device, hidden, inter, experts, tokens, path):
     valid = sorted_ids < ids.size
     got = np_bf16(ws.gate_up)[:total][valid]
     if path == "exact":  # fp32-accurate sums: at most one bf16 rounding apart
-        stats = assert_bf16_close(got, expected[sorted_ids[valid]], ulps=1, row_floor=2.0**-14)
+        stats = assert_bf16_close(got, expected[sorted_ids[valid]], ulps=1, row_floor=2.0**-14,
+                                  outlier_fraction=0.0)
         assert stats["exact_fraction"] > 0.99
     else:
         stats = assert_bf16_close(got, expected[sorted_ids[valid]], ulps=2, row_floor=2.0**-8,
-                                  rrms_max=4e-3)
+                                  rrms_max=4e-3, outlier_fraction=0.0)
     print(path, stats)
 
 
@@ -216,7 +217,7 @@ def test_fp8_mfma_exact_for_narrow_exponent_range(device):
     from drama3_amd.workloads import Experts
 
     gen = torch.Generator("cpu").manual_seed(1)
-    e, h, i, t = 4, 1024, 256, 32
+    e, h, i, t = 8, 1024, 256, 32
     codes = (torch.randint(0, 8, (e, 2 * i, h), generator=gen) + 0x38)
     codes |= torch.randint(0, 2, codes.shape, generator=gen) * 0x80
     w13 = codes.to(torch.uint8).view(torch.float8_e4m3fn)
