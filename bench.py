@@ -146,6 +146,16 @@ def main():
         + routes * 2 * i * 2
     fc2_bytes = used * (h * i + 4 * (h // 128) * (i // 128)) + routes * i + routes * (i // 128) * 4 \
         + routes * h * 4
+    # Practical streaming rate of this GPU for context: a large device copy
+    # (torch), counting bytes read plus bytes written.
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    copy_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(copy_graph):
+        dst.copy_(src)
+    time_graphs(torch, [copy_graph], 2)
+    copy_gbs = 2 * src.numel() / time_graphs(torch, [copy_graph], 5) / 1e3
+    del src, dst
     fc1_gbs = fc1_bytes / fc1_us / 1e3
     fc2_gbs = fc2_bytes / fc2_us / 1e3
     step_gbs = step_bytes / step_us / 1e3
@@ -196,6 +206,7 @@ def main():
                      "algorithmic_bytes_per_launch": fc1_bytes},
         "fc2": {"us_per_launch": round(fc2_us, 2), "GB_s": round(fc2_gbs, 1),
                 "algorithmic_bytes_per_launch": fc2_bytes},
+        "device_copy_GB_s": round(copy_gbs, 1),
         "cpu_baseline": cpu,
         "parity": parity,
     }

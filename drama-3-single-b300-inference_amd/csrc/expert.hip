@@ -90,13 +90,95 @@ __device__ __forceinline__ floatx4 mfma_block_bf16(int32x8 a, const bf16x8 b[4])
   return acc;
 }
 
-template <int KB, int RT, int MODE>
+// SwiGLU + e4m3 requantisation of one 128-column group held by 16 lanes
+// (8 gate and 8 up bf16 values per lane): a = (g * sigmoid(g)) * u in fp32,
+// scale = max(amax, 1e-10) / 448, codes of clamp(a / scale).  Shared by the
+// standalone kernel and the fused FC1 epilogue, so both give the same bytes.
+__device__ __forceinline__ float swiglu_quant_group(uint4 graw, uint4 uraw, uint2* codes) {
+  const uint32_t gw[4] = {graw.x, graw.y, graw.z, graw.w};
+  const uint32_t uw[4] = {uraw.x, uraw.y, uraw.z, uraw.w};
+  float v[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t gbits = (i & 1) ? (gw[i / 2] & 0xffff0000u) : (gw[i / 2] << 16);
+    const uint32_t ubits = (i & 1) ? (uw[i / 2] & 0xffff0000u) : (uw[i / 2] << 16);
+    const float g = __uint_as_float(gbits);
+    const float u = __uint_as_float(ubits);
+    const float sig = 1.0f / (1.0f + expf(-g));
+    v[i] = (g * sig) * u;
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  amax = segment_max<16>(amax);
+  const float scale = group_scale(amax);
+  uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo |= quantize_one(v[i], scale) << (8 * i);
+    hi |= quantize_one(v[i + 4], scale) << (8 * i);
+  }
+  *codes = make_uint2(lo, hi);
+  return scale;
+}
+
+__device__ __forceinline__ float route_weight(const void* weights, int weights_f32, size_t index) {
+  return weights_f32 ? static_cast<const float*>(weights)[index]
+                     : bf16_to_f32(static_cast<const uint16_t*>(weights)[index]);
+}
+
+// out[token, column .. column+3] = sum_r w[token, r] * down[token*top_k + r, ...]
+// with one fused multiply-add per rank in rank order (fp32), before rounding.
+__device__ __forceinline__ float4 combine4(const float* down, const void* weights, int weights_f32,
+                                           int token, int top_k, int hidden, int column) {
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int r = 0; r < top_k; ++r) {
+    const float w = route_weight(weights, weights_f32, static_cast<size_t>(token) * top_k + r);
+    const float4 y = *reinterpret_cast<const float4*>(
+        down + (static_cast<size_t>(token) * top_k + r) * hidden + column);
+    acc.x = fmaf(w, y.x, acc.x);
+    acc.y = fmaf(w, y.y, acc.y);
+    acc.z = fmaf(w, y.z, acc.z);
+    acc.w = fmaf(w, y.w, acc.w);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ uint2 pack_bf16x4(float4 v) {
+  const uint32_t lo = f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
+  const uint32_t hi = f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+  return make_uint2(lo, hi);
+}
+
+// Fused epilogues of the expert GEMM.  Each output group is finished by the
+// last workgroup that contributes to it: contributors publish their tile
+// (release fence), take a ticket with one atomic add, and the one holding
+// the final ticket reads every contribution back (acquire fence), finishes
+// the group and resets its ticket to 0 for the next launch.  Nobody waits.
+enum Fuse : int {
+  kFuseNone = 0,
+  kFuseSwiglu = 1,   // FC1: SwiGLU + requant of each (route, 128-column) group
+  kFuseCombine = 2,  // FC2: weighted top-k combine of each (token, column tile)
+};
+
+struct EpilogueArgs {
+  int32_t* tickets;
+  // kFuseSwiglu
+  int intermediate;
+  uint8_t* act_out;
+  float* act_scales_out;
+  // kFuseCombine
+  const void* route_weights;
+  int route_weights_f32;
+  uint16_t* combined;
+};
+
+template <int KB, int RT, int MODE, int FUSE>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void expert_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows,
     const uint8_t* __restrict__ act, const float* __restrict__ act_scales,
     const int32_t* __restrict__ sorted_ids, int top_k, const int4* __restrict__ items,
     const int32_t* __restrict__ num_items, int exact_routes, uint16_t* __restrict__ out_bf16,
-    float* __restrict__ out_f32) {
+    float* __restrict__ out_f32, EpilogueArgs epi) {
   constexpr int K = KB * kGroup;
   constexpr int kRowsPerWave = RT * 16;
   constexpr int kRowsPerGroup = kGemmWaves * kRowsPerWave;
@@ -106,6 +188,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   __shared__ __attribute__((aligned(16))) uint8_t b_tile[16 * kStride];
   __shared__ float b_scales[16 * KB];
   __shared__ int b_target[16];  // FC1: sorted position, FC2: pair id; -1 = no route
+  __shared__ int finish[16];    // fused epilogue: group this workgroup finishes, or -1
 
   const int tiles = n_rows / kRowsPerGroup;
   const int item_index = blockIdx.x / tiles;
@@ -122,9 +205,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   const int group = lane >> 4;
   const int n0 = (blockIdx.x % tiles) * kRowsPerGroup + wave * kRowsPerWave;
 
-  // The first route tile's activation rows are fetched before the weights:
-  // memory returns are counted in issue order, so staging issued behind the
-  // weights would wait for all of them before the first MFMA.
+  // Issue order of the first tile (memory returns are counted in issue
+  // order): the first half of the weights, then the route ids (scalar loads,
+  // counted apart from the vector stream) and the activation rows they name,
+  // then the second half of the weights.  The staging wait then covers only
+  // the first half, whose MFMAs overlap the second half's transfer.
   const int stage_col = threadIdx.x >> 4;   // route column staged by this thread
   const int stage_part = threadIdx.x & 15;  // 16 threads per route row
   constexpr int kChunks = K / 256;          // 16-byte chunks per thread and row
@@ -132,10 +217,15 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   float b_stage_scale = 0.0f;
   int b_stage_target = -1;
   auto fetch_tile = [&](int m0) {
+    int pair = 0;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {  // uniform loads of the tile's 16 route ids
+      const int id = m0 + c < routes ? sorted_ids[first + m0 + c] : 0;
+      pair = stage_col == c ? id : pair;
+    }
     const int r = m0 + stage_col;
     const bool live = r < routes;
     const int position = first + r;
-    const int pair = live ? sorted_ids[position] : 0;
     const size_t a_row = MODE == 0 ? static_cast<size_t>(pair / top_k) : static_cast<size_t>(position);
     const uint8_t* src = act + a_row * K;
 #pragma unroll
@@ -153,16 +243,24 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     if (stage_part < KB) b_scales[stage_col * KB + stage_part] = b_stage_scale;
     if (stage_part == 0) b_target[stage_col] = b_stage_target;
   };
-  fetch_tile(0);
 
-  // Weights for the whole contraction: the bulk of the HBM stream.
   const uint8_t* wexp = w + static_cast<size_t>(expert) * n_rows * K;
+  constexpr int kFirstHalf = KB > 1 ? KB / 2 : KB;
   int32x8 a_frag[RT][KB];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const uint8_t* row = wexp + static_cast<size_t>(n0 + rt * 16 + row16) * K;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) a_frag[rt][kb] = load_fragment(row, kb, group);
+    for (int kb = 0; kb < kFirstHalf; ++kb) a_frag[rt][kb] = load_fragment(row, kb, group);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  fetch_tile(0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const uint8_t* row = wexp + static_cast<size_t>(n0 + rt * 16 + row16) * K;
+#pragma unroll
+    for (int kb = kFirstHalf; kb < KB; ++kb) a_frag[rt][kb] = load_fragment(row, kb, group);
   }
   float w_scale[RT][KB];
   const float* wsexp = ws + static_cast<size_t>(expert) * (n_rows / kGroup) * KB;
@@ -226,6 +324,63 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
         }
       }
     }
+    if constexpr (FUSE != kFuseNone) {
+      const int tile_n0 = (blockIdx.x % tiles) * kRowsPerGroup;
+      __threadfence();  // release this tile's outputs
+      __syncthreads();
+      if (threadIdx.x < 16) {
+        const int c = threadIdx.x;
+        const int t = b_target[c];
+        int done = -1;
+        if (t >= 0) {
+          if constexpr (FUSE == kFuseSwiglu) {
+            // (sorted row, act group): 128 / tile gate tiles + as many up tiles
+            const bool up = tile_n0 >= epi.intermediate;
+            const int g = (up ? tile_n0 - epi.intermediate : tile_n0) / kGroup;
+            const int contributors = 2 * (kGroup / kRowsPerGroup);
+            const int index = t * (epi.intermediate / kGroup) + g;
+            if (atomicAdd(&epi.tickets[index], 1) == contributors - 1) done = index;
+          } else {
+            // (token, column tile): one contribution per routed expert
+            const int index = (t / top_k) * tiles + (blockIdx.x % tiles);
+            if (atomicAdd(&epi.tickets[index], 1) == top_k - 1) done = index;
+          }
+        }
+        finish[c] = done;
+      }
+      __syncthreads();
+      const int seg = threadIdx.x >> 4;  // one 16-thread segment per route column
+      const int part = threadIdx.x & 15;
+      const int index = finish[seg];
+      if (index >= 0) {
+        __threadfence();  // acquire the other contributors' outputs
+        if constexpr (FUSE == kFuseSwiglu) {
+          const int groups = epi.intermediate / kGroup;
+          const int row = index / groups;
+          const int g = index % groups;
+          const uint16_t* gate = out_bf16 + static_cast<size_t>(row) * n_rows + g * kGroup + part * 8;
+          const uint4 graw = *reinterpret_cast<const uint4*>(gate);
+          const uint4 uraw = *reinterpret_cast<const uint4*>(gate + epi.intermediate);
+          uint2 codes;
+          const float scale = swiglu_quant_group(graw, uraw, &codes);
+          *reinterpret_cast<uint2*>(epi.act_out + static_cast<size_t>(row) * epi.intermediate +
+                                    g * kGroup + part * 8) = codes;
+          if (part == 0) {
+            epi.act_scales_out[static_cast<size_t>(row) * groups + g] = scale;
+            atomicExch(&epi.tickets[index], 0);
+          }
+        } else {
+          const int token = index / tiles;
+          for (int column = tile_n0 + part * 4; column < tile_n0 + kRowsPerGroup; column += 64) {
+            const float4 v = combine4(out_f32, epi.route_weights, epi.route_weights_f32, token,
+                                      top_k, n_rows, column);
+            *reinterpret_cast<uint2*>(epi.combined + static_cast<size_t>(token) * n_rows + column) =
+                pack_bf16x4(v);
+          }
+          if (part == 0) atomicExch(&epi.tickets[index], 0);
+        }
+      }
+    }
   }
 }
 
@@ -258,30 +413,10 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(
       graw = *reinterpret_cast<const uint4*>(gate + column);
       uraw = *reinterpret_cast<const uint4*>(up + column);
     }
-    const uint32_t gw[4] = {graw.x, graw.y, graw.z, graw.w};
-    const uint32_t uw[4] = {uraw.x, uraw.y, uraw.z, uraw.w};
-    float v[8];
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t gbits = (i & 1) ? (gw[i / 2] & 0xffff0000u) : (gw[i / 2] << 16);
-      const uint32_t ubits = (i & 1) ? (uw[i / 2] & 0xffff0000u) : (uw[i / 2] << 16);
-      const float g = __uint_as_float(gbits);
-      const float u = __uint_as_float(ubits);
-      const float sig = 1.0f / (1.0f + expf(-g));
-      v[i] = (g * sig) * u;
-      amax = fmaxf(amax, fabsf(v[i]));
-    }
-    amax = segment_max<16>(amax);
-    const float scale = group_scale(amax);
-    uint32_t lo = 0u, hi = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lo |= quantize_one(v[i], scale) << (8 * i);
-      hi |= quantize_one(v[i + 4], scale) << (8 * i);
-    }
+    uint2 codes;
+    const float scale = swiglu_quant_group(graw, uraw, &codes);
     if (inside) {
-      *reinterpret_cast<uint2*>(out + column) = make_uint2(lo, hi);
+      *reinterpret_cast<uint2*>(out + column) = codes;
       if ((lane & 15) == 0) act_scales[static_cast<size_t>(row) * groups + column / kGroup] = scale;
     }
   }
@@ -296,22 +431,8 @@ __global__ __launch_bounds__(kRowThreads) void weighted_combine_kernel(
     const float* __restrict__ shared, uint16_t* __restrict__ out) {
   const int row = blockIdx.x;
   if (row >= live_rows(row_count, rows)) return;
-  float w[16];
-  for (int r = 0; r < top_k; ++r) {
-    const size_t index = static_cast<size_t>(row) * top_k + r;
-    w[r] = weights_f32 ? static_cast<const float*>(weights)[index]
-                       : bf16_to_f32(static_cast<const uint16_t*>(weights)[index]);
-  }
   for (int column = threadIdx.x * 4; column < hidden; column += kRowThreads * 4) {
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int r = 0; r < top_k; ++r) {
-      const float4 y = *reinterpret_cast<const float4*>(
-          down + (static_cast<size_t>(row) * top_k + r) * hidden + column);
-      acc.x = fmaf(w[r], y.x, acc.x);
-      acc.y = fmaf(w[r], y.y, acc.y);
-      acc.z = fmaf(w[r], y.z, acc.z);
-      acc.w = fmaf(w[r], y.w, acc.w);
-    }
+    float4 acc = combine4(down, weights, weights_f32, row, top_k, hidden, column);
     if (shared != nullptr) {
       // Dense shared expert added to the routed output, each rounded to bf16.
       const float4 s = *reinterpret_cast<const float4*>(shared + static_cast<size_t>(row) * hidden + column);
@@ -320,50 +441,107 @@ __global__ __launch_bounds__(kRowThreads) void weighted_combine_kernel(
       acc.z = bf16_to_f32(f32_to_bf16(acc.z)) + bf16_to_f32(f32_to_bf16(s.z));
       acc.w = bf16_to_f32(f32_to_bf16(acc.w)) + bf16_to_f32(f32_to_bf16(s.w));
     }
-    const uint32_t lo = f32_to_bf16(acc.x) | (static_cast<uint32_t>(f32_to_bf16(acc.y)) << 16);
-    const uint32_t hi = f32_to_bf16(acc.z) | (static_cast<uint32_t>(f32_to_bf16(acc.w)) << 16);
-    *reinterpret_cast<uint2*>(out + static_cast<size_t>(row) * hidden + column) = make_uint2(lo, hi);
+    *reinterpret_cast<uint2*>(out + static_cast<size_t>(row) * hidden + column) = pack_bf16x4(acc);
   }
 }
 
-template <int KB, int RT, int MODE>
-void launch_gemm(dim3 grid, hipStream_t s, const uint8_t* w, const float* ws, int n,
-                 const uint8_t* a, const float* as, const int32_t* sorted_ids, int top_k,
-                 const int4* items, const int32_t* num_items, int exact_routes,
-                 uint16_t* out_bf16, float* out_f32) {
-  hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE>), grid, dim3(kGemmThreads), 0, s, w, ws,
-                     n, a, as, sorted_ids, top_k, items, num_items, exact_routes, out_bf16,
-                     out_f32);
+struct GemmLaunch {
+  int mode;
+  int fuse;
+  const uint8_t* w;
+  const float* ws;
+  int n;
+  const uint8_t* a;
+  const float* as;
+  const int32_t* sorted_ids;
+  int top_k;
+  const int4* items;
+  const int32_t* num_items;
+  int max_items;
+  int exact_routes;
+  uint16_t* out_bf16;
+  float* out_f32;
+  EpilogueArgs epi;
+};
+
+template <int KB, int RT, int MODE, int FUSE>
+void launch_gemm(dim3 grid, hipStream_t s, const GemmLaunch& g) {
+  hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE>), grid, dim3(kGemmThreads), 0, s,
+                     g.w, g.ws, g.n, g.a, g.as, g.sorted_ids, g.top_k, g.items, g.num_items,
+                     g.exact_routes, g.out_bf16, g.out_f32, g.epi);
 }
 
 // Row tiles per wave: keep each wave's register-resident weights near 32 KiB.
 constexpr int rt_for(int kb) { return kb >= 8 ? 1 : (kb >= 4 ? 2 : 4); }
+constexpr int tile_rows_for(int kb) { return kGemmWaves * rt_for(kb) * 16; }
 
 template <int KB>
-int dispatch_gemm(int mode, int n, dim3 items_grid, hipStream_t s, const uint8_t* w,
-                  const float* ws, const uint8_t* a, const float* as, const int32_t* sorted_ids,
-                  int top_k, const int4* items, const int32_t* num_items, int exact_routes,
-                  uint16_t* out_bf16, float* out_f32) {
+int dispatch_gemm(const GemmLaunch& g, hipStream_t s) {
   constexpr int RT = rt_for(KB);
-  constexpr int rows_per_group = kGemmWaves * RT * 16;
-  D3_SUPPORTED(n % rows_per_group == 0, "expert_gemm: N=%d must be a multiple of %d for K=%d", n,
-               rows_per_group, KB * kGroup);
-  const dim3 grid(items_grid.x * (n / rows_per_group));
-  if (mode == 0)
-    launch_gemm<KB, RT, 0>(grid, s, w, ws, n, a, as, sorted_ids, top_k, items, num_items,
-                           exact_routes, out_bf16, out_f32);
+  constexpr int rows_per_group = tile_rows_for(KB);
+  D3_SUPPORTED(g.n % rows_per_group == 0, "expert_gemm: N=%d must be a multiple of %d for K=%d",
+               g.n, rows_per_group, KB * kGroup);
+  const dim3 grid(g.max_items * (g.n / rows_per_group));
+  if (g.fuse == kFuseSwiglu) {
+    if constexpr (rows_per_group <= kGroup) {
+      launch_gemm<KB, RT, 0, kFuseSwiglu>(grid, s, g);
+      return D3_OK;
+    }
+    return set_error(D3_ERR_UNSUPPORTED, "expert_fc1_swiglu: K=%d tiles %d rows (> 128)",
+                     KB * kGroup, rows_per_group);
+  }
+  if (g.fuse == kFuseCombine)
+    launch_gemm<KB, RT, 1, kFuseCombine>(grid, s, g);
+  else if (g.mode == 0)
+    launch_gemm<KB, RT, 0, kFuseNone>(grid, s, g);
   else
-    launch_gemm<KB, RT, 1>(grid, s, w, ws, n, a, as, sorted_ids, top_k, items, num_items,
-                           exact_routes, out_bf16, out_f32);
+    launch_gemm<KB, RT, 1, kFuseNone>(grid, s, g);
   return D3_OK;
 }
 
+int run_gemm(const GemmLaunch& g, int k, hipStream_t s) {
+  switch (k / kGroup) {
+    case 2: return dispatch_gemm<2>(g, s);
+    case 4: return dispatch_gemm<4>(g, s);
+    case 6: return dispatch_gemm<6>(g, s);
+    case 8: return dispatch_gemm<8>(g, s);
+    case 12: return dispatch_gemm<12>(g, s);
+    case 16: return dispatch_gemm<16>(g, s);
+    default: return set_error(D3_ERR_UNSUPPORTED, "expert_gemm: K=%d not in the compiled set", k);
+  }
+}
+
+int tile_rows(int k) {
+  switch (k / kGroup) {
+    case 2: return tile_rows_for(2);
+    case 4: return tile_rows_for(4);
+    case 6: return tile_rows_for(6);
+    case 8: return tile_rows_for(8);
+    case 12: return tile_rows_for(12);
+    case 16: return tile_rows_for(16);
+    default: return -1;
+  }
+}
+
 bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+int check_gemm(const GemmLaunch& g, int num_experts, int k, const char* name) {
+  D3_REQUIRE(g.w && g.ws && g.a && g.as && g.sorted_ids && g.items && g.num_items,
+             "%s: null pointer", name);
+  D3_REQUIRE(num_experts >= 1 && g.n > 0 && k > 0 && g.n % kGroup == 0 && k % kGroup == 0,
+             "%s: N=%d, K=%d must be positive multiples of 128", name, g.n, k);
+  D3_REQUIRE(g.top_k >= 1 && g.max_items >= 0, "%s: bad top_k/max_items", name);
+  D3_REQUIRE(aligned(g.w, 16) && aligned(g.a, 16), "%s: operands must be 16-byte aligned", name);
+  D3_SUPPORTED(k % 256 == 0 && tile_rows(k) > 0, "%s: K=%d not in the compiled set", name, k);
+  return D3_OK;
+}
 
 }  // namespace
 }  // namespace d3
 
 using namespace d3;
+
+extern "C" int32_t d3_expert_tile_rows(int32_t k) { return k % kGroup ? -1 : tile_rows(k); }
 
 extern "C" int d3_expert_gemm(int32_t mode, const uint8_t* w, const float* ws, int32_t num_experts,
                               int32_t n, int32_t k, const uint8_t* a, const float* a_scales,
@@ -371,41 +549,82 @@ extern "C" int d3_expert_gemm(int32_t mode, const uint8_t* w, const float* ws, i
                               const int32_t* num_items, int32_t max_items, int32_t exact_routes,
                               uint16_t* out_bf16, float* out_f32, void* stream) {
   D3_REQUIRE(mode == 0 || mode == 1, "expert_gemm: mode must be 0 (FC1) or 1 (FC2)");
-  D3_REQUIRE(w && ws && a && a_scales && sorted_ids && items && num_items,
-             "expert_gemm: null pointer");
   D3_REQUIRE(mode == 0 ? out_bf16 != nullptr : out_f32 != nullptr, "expert_gemm: null output");
-  D3_REQUIRE(num_experts >= 1 && n > 0 && k > 0 && n % kGroup == 0 && k % kGroup == 0,
-             "expert_gemm: N=%d, K=%d must be positive multiples of 128", n, k);
-  D3_REQUIRE(top_k >= 1 && max_items >= 0, "expert_gemm: bad top_k/max_items");
-  D3_REQUIRE(aligned(w, 16) && aligned(a, 16), "expert_gemm: operands must be 16-byte aligned");
   D3_REQUIRE(mode == 0 ? aligned(out_bf16, 8) : aligned(out_f32, 16),
              "expert_gemm: output alignment");
+  const GemmLaunch g{mode, kFuseNone, w, ws, n, a, a_scales, sorted_ids, top_k,
+                     reinterpret_cast<const int4*>(items), num_items, max_items, exact_routes,
+                     out_bf16, out_f32, EpilogueArgs{}};
+  int status = check_gemm(g, num_experts, k, "expert_gemm");
+  if (status != D3_OK) return status;
   if (max_items == 0) {
     clear_error();
     return D3_OK;
   }
-  hipStream_t s = as_stream(stream);
-  const dim3 items_grid(max_items);
-  const int4* it = reinterpret_cast<const int4*>(items);
-  int status;
-  switch (k / kGroup) {
-#define D3_GEMM_CASE(KB)                                                                       \
-  case KB:                                                                                     \
-    status = dispatch_gemm<KB>(mode, n, items_grid, s, w, ws, a, a_scales, sorted_ids, top_k,  \
-                               it, num_items, exact_routes, out_bf16, out_f32);                \
-    break;
-    D3_GEMM_CASE(2)
-    D3_GEMM_CASE(4)
-    D3_GEMM_CASE(6)
-    D3_GEMM_CASE(8)
-    D3_GEMM_CASE(12)
-    D3_GEMM_CASE(16)
-#undef D3_GEMM_CASE
-    default:
-      return set_error(D3_ERR_UNSUPPORTED, "expert_gemm: K=%d not in the compiled set", k);
-  }
+  status = run_gemm(g, k, as_stream(stream));
   if (status != D3_OK) return status;
   D3_LAUNCHED("expert_gemm");
+}
+
+extern "C" int d3_expert_fc1_swiglu(const uint8_t* w13, const float* s13, int32_t num_experts,
+                                    int32_t intermediate, int32_t hidden, const uint8_t* q,
+                                    const float* x_scales, const int32_t* sorted_ids,
+                                    int32_t top_k, const int32_t* items,
+                                    const int32_t* num_items, int32_t max_items,
+                                    int32_t exact_routes, uint16_t* gate_up, uint8_t* act,
+                                    float* act_scales, int32_t* tickets, void* stream) {
+  D3_REQUIRE(gate_up && act && act_scales && tickets, "expert_fc1_swiglu: null output");
+  D3_REQUIRE(intermediate > 0 && intermediate % kGroup == 0,
+             "expert_fc1_swiglu: intermediate %d must be a multiple of 128", intermediate);
+  D3_REQUIRE(aligned(gate_up, 16) && aligned(act, 8), "expert_fc1_swiglu: output alignment");
+  EpilogueArgs epi{};
+  epi.tickets = tickets;
+  epi.intermediate = intermediate;
+  epi.act_out = act;
+  epi.act_scales_out = act_scales;
+  const GemmLaunch g{0, kFuseSwiglu, w13, s13, 2 * intermediate, q, x_scales, sorted_ids, top_k,
+                     reinterpret_cast<const int4*>(items), num_items, max_items, exact_routes,
+                     gate_up, nullptr, epi};
+  int status = check_gemm(g, num_experts, hidden, "expert_fc1_swiglu");
+  if (status != D3_OK) return status;
+  if (max_items == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  status = run_gemm(g, hidden, as_stream(stream));
+  if (status != D3_OK) return status;
+  D3_LAUNCHED("expert_fc1_swiglu");
+}
+
+extern "C" int d3_expert_fc2_combine(const uint8_t* w2, const float* s2, int32_t num_experts,
+                                     int32_t hidden, int32_t intermediate, const uint8_t* act,
+                                     const float* act_scales, const int32_t* sorted_ids,
+                                     int32_t top_k, const int32_t* items,
+                                     const int32_t* num_items, int32_t max_items,
+                                     int32_t exact_routes, float* down, const void* weights,
+                                     int32_t weights_dtype, uint16_t* out, int32_t* tickets,
+                                     void* stream) {
+  D3_REQUIRE(down && weights && out && tickets, "expert_fc2_combine: null output");
+  D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
+             "expert_fc2_combine: weights must be bf16 or f32");
+  D3_REQUIRE(aligned(down, 16) && aligned(out, 8), "expert_fc2_combine: output alignment");
+  EpilogueArgs epi{};
+  epi.tickets = tickets;
+  epi.route_weights = weights;
+  epi.route_weights_f32 = weights_dtype == D3_DTYPE_F32 ? 1 : 0;
+  epi.combined = out;
+  const GemmLaunch g{1, kFuseCombine, w2, s2, hidden, act, act_scales, sorted_ids, top_k,
+                     reinterpret_cast<const int4*>(items), num_items, max_items, exact_routes,
+                     nullptr, down, epi};
+  int status = check_gemm(g, num_experts, intermediate, "expert_fc2_combine");
+  if (status != D3_OK) return status;
+  if (max_items == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  status = run_gemm(g, intermediate, as_stream(stream));
+  if (status != D3_OK) return status;
+  D3_LAUNCHED("expert_fc2_combine");
 }
 
 extern "C" int d3_silu_mul_quant(const uint16_t* gate_up, int32_t rows, int32_t intermediate,

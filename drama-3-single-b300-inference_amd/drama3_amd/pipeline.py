@@ -77,7 +77,7 @@ class MoEWorkspace:
 
     def __init__(self, shape: Shape, device: torch.device | str = "cuda", tile: int = SORT_TILE,
                  item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
-                 exact_routes: int = EXACT_ROUTES):
+                 exact_routes: int = EXACT_ROUTES, fused: bool = True):
         lib = _lib.load()
         self.shape = shape
         self.device = torch.device(device)
@@ -111,6 +111,13 @@ class MoEWorkspace:
         self.act_scales = torch.empty((self.max_rows, i // 128), dtype=torch.float32, device=dev)
         self.down = torch.empty((pairs, h), dtype=torch.float32, device=dev)
         self.out = torch.empty((t, h), dtype=torch.bfloat16, device=dev)
+        # Fused epilogues (SwiGLU requant in FC1, combine in FC2) when the
+        # tiling allows; their tickets start at 0 and every launch leaves 0.
+        fc1_tile, fc2_tile = lib.d3_expert_tile_rows(h), lib.d3_expert_tile_rows(i)
+        self.fuse_fc1 = fused and 0 < fc1_tile <= 128
+        self.fuse_fc2 = fused and fc2_tile > 0
+        self.fc1_tickets = torch.zeros(self.max_rows * (i // 128) if self.fuse_fc1 else 1, **i32)
+        self.fc2_tickets = torch.zeros(t * (h // fc2_tile) if self.fuse_fc2 else 1, **i32)
 
     # -- stages ---------------------------------------------------------------
     def _stream(self, stream):
@@ -208,11 +215,36 @@ class MoEWorkspace:
         self.front(x, logits, row_index, row_count, stream=stream)
         return self.experts(experts, row_count, shared, out, stream)
 
+    def fc1_swiglu(self, experts, stream=None) -> None:
+        s, stream = self.shape, self._stream(stream)
+        call("d3_expert_fc1_swiglu", ptr(experts.w13_weight), ptr(experts.w13_scale_inv),
+             s.num_experts, s.intermediate, s.hidden, ptr(self.q), ptr(self.x_scales),
+             ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
+             self.exact_routes, ptr(self.gate_up), ptr(self.act), ptr(self.act_scales),
+             ptr(self.fc1_tickets), stream)
+
+    def fc2_combine(self, experts, out=None, stream=None) -> torch.Tensor:
+        s, stream = self.shape, self._stream(stream)
+        out = self.out if out is None else out
+        call("d3_expert_fc2_combine", ptr(experts.w2_weight), ptr(experts.w2_scale_inv),
+             s.num_experts, s.hidden, s.intermediate, ptr(self.act), ptr(self.act_scales),
+             ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
+             self.exact_routes, ptr(self.down), ptr(self.weights), dtype_code(self.weights.dtype),
+             ptr(out), ptr(self.fc2_tickets), stream)
+        return out
+
     def experts(self, experts, row_count=None, shared=None, out=None, stream=None):
-        """FC1, SwiGLU requant, FC2 and combine over the routes sorted by front()."""
+        """FC1, SwiGLU requant, FC2 and combine over the routes sorted by front().
+        Uses the fused epilogues when available (two launches instead of four);
+        a dense shared expert is added by the separate combine."""
         stream = _lib.stream(self.device) if stream is None else stream
-        self.fc1(experts, stream)
-        self.activation(stream)
+        if self.fuse_fc1:
+            self.fc1_swiglu(experts, stream)
+        else:
+            self.fc1(experts, stream)
+            self.activation(stream)
+        if self.fuse_fc2 and shared is None:
+            return self.fc2_combine(experts, out, stream)
         self.fc2(experts, stream)
         return self.combine(None, row_count, shared, out, stream)
 

@@ -182,6 +182,41 @@ int d3_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32_t num_
                    const int32_t *num_items, int32_t max_items, int32_t exact_routes,
                    uint16_t *out_bf16, float *out_f32, void *stream);
 
+/* Weight rows per workgroup tile of d3_expert_gemm for contraction length k. */
+int32_t d3_expert_tile_rows(int32_t k);
+
+/*
+ * A9 + A10  FC1 with the SwiGLU requantisation fused into its epilogue.
+ * d3_expert_gemm mode 0 (gate_up bf16 at sorted positions, n = 2I, k = H)
+ * after which, for every (sorted row, 128-column activation group), the last
+ * workgroup to write one of the group's gate / up tiles computes the group
+ * exactly as d3_silu_mul_quant: act fp8 [rows, I], act_scales [rows, I/128].
+ * tickets: int32 [max sorted rows * I/128], all 0 before the first launch and
+ * left at 0.  Needs d3_expert_tile_rows(hidden) <= 128.
+ */
+int d3_expert_fc1_swiglu(const uint8_t *w13, const float *s13, int32_t num_experts,
+                         int32_t intermediate, int32_t hidden, const uint8_t *q,
+                         const float *x_scales, const int32_t *sorted_ids, int32_t top_k,
+                         const int32_t *items, const int32_t *num_items, int32_t max_items,
+                         int32_t exact_routes, uint16_t *gate_up, uint8_t *act, float *act_scales,
+                         int32_t *tickets, void *stream);
+
+/*
+ * A11  FC2 with the weighted top-k combine fused into its epilogue.
+ * d3_expert_gemm mode 1 (down fp32 by pair, n = H, k = I) after which, for
+ * every (token, column tile), the last of its top_k contributing workgroups
+ * writes out[token, tile] = bf16(sum_r w[t,r] down[t*top_k+r, tile]) in rank
+ * order, exactly as d3_weighted_combine without a shared expert.
+ * tickets: int32 [tokens * hidden / d3_expert_tile_rows(intermediate)], all
+ * 0 before the first launch and left at 0.
+ */
+int d3_expert_fc2_combine(const uint8_t *w2, const float *s2, int32_t num_experts, int32_t hidden,
+                          int32_t intermediate, const uint8_t *act, const float *act_scales,
+                          const int32_t *sorted_ids, int32_t top_k, const int32_t *items,
+                          const int32_t *num_items, int32_t max_items, int32_t exact_routes,
+                          float *down, const void *weights, int32_t weights_dtype, uint16_t *out,
+                          int32_t *tickets, void *stream);
+
 /*
  * A10  SwiGLU + per-128 FP8 requantisation of FC1 rows.
  * Replaces Fish quantize_groups(silu_mul_quant_kernel, gate_up, I)

@@ -93,3 +93,36 @@ def test_fused_front_row_mode_with_index(device):
         assert np.array_equal(ws.sorted_ids.cpu().numpy()[:o.total], o.sorted_ids)
         assert np.array_equal(ws.inverse.cpu().numpy(), o.inverse)
         assert int(ws.ticket.item()) == 0
+
+
+@pytest.mark.parametrize("config", [1, 2, 3])
+def test_fused_epilogues_match_unfused_chain(device, config):
+    """FC1 + fused SwiGLU requant and FC2 + fused combine give exactly the
+    bytes of the four-kernel chain, and leave every ticket at 0."""
+    from drama3_amd import workloads
+    from drama3_amd.pipeline import MoEWorkspace, Shape
+
+    w = workloads.CONFIGS[config]()
+    step = w.steps[0]
+    experts = w.experts.to(device)
+    occ = step.occupancy.to(device)
+    xs, ls = step.x_slots.to(device), step.logits_slots.to(device)
+    outs = {}
+    for fused in (False, True):
+        ws = MoEWorkspace(Shape(64, w.num_experts, w.hidden, w.intermediate), device, fused=fused)
+        active = torch.empty(64, dtype=torch.int32, device=device)
+        count = torch.empty(1, dtype=torch.int32, device=device)
+        for _ in range(2):  # second launch proves the tickets were reset
+            ws.front(xs, ls, occupancy=occ, active=active, count=count)
+            out = ws.experts(experts, count)
+        torch.cuda.synchronize()
+        n = int(count.item())
+        total = int(ws.total.item())
+        valid = ws.sorted_ids.cpu().numpy()[:total] < n * 8
+        outs[fused] = (out[:n].cpu(), np_u8(ws.act)[:total][valid], np_f32(ws.act_scales)[:total][valid])
+        if fused:
+            assert ws.fuse_fc1 and ws.fuse_fc2
+            assert int(ws.fc1_tickets.abs().sum()) == 0 and int(ws.fc2_tickets.abs().sum()) == 0
+    assert torch.equal(outs[True][0], outs[False][0])
+    assert np.array_equal(outs[True][1], outs[False][1])
+    assert np.array_equal(outs[True][2], outs[False][2])
