@@ -115,6 +115,40 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
+// ---------------------------------------------------------------------------
+// Cross-workgroup hand-off without cache-wide fences.
+// On gfx950 every XCD has its own L2; an agent-scope fence writes back and
+// invalidates that whole L2.  Data handed from one workgroup to another is
+// instead stored and loaded with agent-scope relaxed atomics (write-through /
+// coherent accesses, sc1), the stores are waited for before a workgroup
+// barrier, and only then is the hand-off ticket taken with an agent-scope
+// atomic add.  The reader, having seen the final ticket, loads the data with
+// coherent loads.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void publish_u64(void* p, uint64_t v) {
+  __hip_atomic_store(static_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_u32(void* p, uint32_t v) {
+  __hip_atomic_store(static_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t collect_u64(const void* p) {
+  return __hip_atomic_load(static_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t collect_u32(const void* p) {
+  return __hip_atomic_load(static_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+// Every store of the calling thread has completed (reached the coherent
+// level for published stores) before it proceeds.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+__device__ __forceinline__ int take_ticket(int32_t* ticket) {
+  return __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_ticket(int32_t* ticket) {
+  __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Row count visible to graph-captured kernels: a device scalar when given,
 // otherwise the host capacity.
 __device__ __forceinline__ int live_rows(const int32_t* count, int capacity) {

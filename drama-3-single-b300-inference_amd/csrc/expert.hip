@@ -128,13 +128,22 @@ __device__ __forceinline__ float route_weight(const void* weights, int weights_f
 
 // out[token, column .. column+3] = sum_r w[token, r] * down[token*top_k + r, ...]
 // with one fused multiply-add per rank in rank order (fp32), before rounding.
+// kCollect: `down` was published by other workgroups (coherent loads).
+template <bool kCollect = false>
 __device__ __forceinline__ float4 combine4(const float* down, const void* weights, int weights_f32,
                                            int token, int top_k, int hidden, int column) {
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (int r = 0; r < top_k; ++r) {
     const float w = route_weight(weights, weights_f32, static_cast<size_t>(token) * top_k + r);
-    const float4 y = *reinterpret_cast<const float4*>(
-        down + (static_cast<size_t>(token) * top_k + r) * hidden + column);
+    const float* src = down + (static_cast<size_t>(token) * top_k + r) * hidden + column;
+    float4 y;
+    if constexpr (kCollect) {
+      const uint64_t lo = collect_u64(src), hi = collect_u64(src + 2);
+      y = make_float4(__uint_as_float(static_cast<uint32_t>(lo)), __uint_as_float(static_cast<uint32_t>(lo >> 32)),
+                      __uint_as_float(static_cast<uint32_t>(hi)), __uint_as_float(static_cast<uint32_t>(hi >> 32)));
+    } else {
+      y = *reinterpret_cast<const float4*>(src);
+    }
     acc.x = fmaf(w, y.x, acc.x);
     acc.y = fmaf(w, y.y, acc.y);
     acc.z = fmaf(w, y.z, acc.z);
@@ -151,9 +160,10 @@ __device__ __forceinline__ uint2 pack_bf16x4(float4 v) {
 
 // Fused epilogues of the expert GEMM.  Each output group is finished by the
 // last workgroup that contributes to it: contributors publish their tile
-// (release fence), take a ticket with one atomic add, and the one holding
-// the final ticket reads every contribution back (acquire fence), finishes
-// the group and resets its ticket to 0 for the next launch.  Nobody waits.
+// (coherent stores, waited for), take a ticket with one atomic add, and the
+// one holding the final ticket reads every contribution back with coherent
+// loads, finishes the group and resets its ticket to 0 for the next launch.
+// Nobody waits on another workgroup.
 enum Fuse : int {
   kFuseNone = 0,
   kFuseSwiglu = 1,   // FC1: SwiGLU + requant of each (route, 128-column) group
@@ -316,17 +326,27 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
         if constexpr (MODE == 0) {
           const uint32_t lo = f32_to_bf16(acc[rt][0]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][1])) << 16);
           const uint32_t hi = f32_to_bf16(acc[rt][2]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][3])) << 16);
-          *reinterpret_cast<uint2*>(out_bf16 + static_cast<size_t>(target) * n_rows + n) =
-              make_uint2(lo, hi);
+          uint16_t* dst = out_bf16 + static_cast<size_t>(target) * n_rows + n;
+          if constexpr (FUSE == kFuseSwiglu)
+            publish_u64(dst, (static_cast<uint64_t>(hi) << 32) | lo);
+          else
+            *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
         } else {
-          *reinterpret_cast<float4*>(out_f32 + static_cast<size_t>(target) * n_rows + n) =
-              make_float4(acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]);
+          float* dst = out_f32 + static_cast<size_t>(target) * n_rows + n;
+          if constexpr (FUSE == kFuseCombine) {
+            publish_u64(dst, (static_cast<uint64_t>(__float_as_uint(acc[rt][1])) << 32) |
+                                 __float_as_uint(acc[rt][0]));
+            publish_u64(dst + 2, (static_cast<uint64_t>(__float_as_uint(acc[rt][3])) << 32) |
+                                     __float_as_uint(acc[rt][2]));
+          } else {
+            *reinterpret_cast<float4*>(dst) = make_float4(acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]);
+          }
         }
       }
     }
     if constexpr (FUSE != kFuseNone) {
       const int tile_n0 = (blockIdx.x % tiles) * kRowsPerGroup;
-      __threadfence();  // release this tile's outputs
+      wait_stores();  // this tile's published outputs are visible device-wide
       __syncthreads();
       if (threadIdx.x < 16) {
         const int c = threadIdx.x;
@@ -339,11 +359,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
             const int g = (up ? tile_n0 - epi.intermediate : tile_n0) / kGroup;
             const int contributors = 2 * (kGroup / kRowsPerGroup);
             const int index = t * (epi.intermediate / kGroup) + g;
-            if (atomicAdd(&epi.tickets[index], 1) == contributors - 1) done = index;
+            if (take_ticket(&epi.tickets[index]) == contributors - 1) done = index;
           } else {
             // (token, column tile): one contribution per routed expert
             const int index = (t / top_k) * tiles + (blockIdx.x % tiles);
-            if (atomicAdd(&epi.tickets[index], 1) == top_k - 1) done = index;
+            if (take_ticket(&epi.tickets[index]) == top_k - 1) done = index;
           }
         }
         finish[c] = done;
@@ -353,31 +373,35 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       const int part = threadIdx.x & 15;
       const int index = finish[seg];
       if (index >= 0) {
-        __threadfence();  // acquire the other contributors' outputs
         if constexpr (FUSE == kFuseSwiglu) {
           const int groups = epi.intermediate / kGroup;
           const int row = index / groups;
           const int g = index % groups;
           const uint16_t* gate = out_bf16 + static_cast<size_t>(row) * n_rows + g * kGroup + part * 8;
-          const uint4 graw = *reinterpret_cast<const uint4*>(gate);
-          const uint4 uraw = *reinterpret_cast<const uint4*>(gate + epi.intermediate);
+          const uint64_t g0 = collect_u64(gate), g1 = collect_u64(gate + 4);
+          const uint64_t u0 = collect_u64(gate + epi.intermediate);
+          const uint64_t u1 = collect_u64(gate + epi.intermediate + 4);
+          const uint4 graw = make_uint4(static_cast<uint32_t>(g0), static_cast<uint32_t>(g0 >> 32),
+                                        static_cast<uint32_t>(g1), static_cast<uint32_t>(g1 >> 32));
+          const uint4 uraw = make_uint4(static_cast<uint32_t>(u0), static_cast<uint32_t>(u0 >> 32),
+                                        static_cast<uint32_t>(u1), static_cast<uint32_t>(u1 >> 32));
           uint2 codes;
           const float scale = swiglu_quant_group(graw, uraw, &codes);
           *reinterpret_cast<uint2*>(epi.act_out + static_cast<size_t>(row) * epi.intermediate +
                                     g * kGroup + part * 8) = codes;
           if (part == 0) {
             epi.act_scales_out[static_cast<size_t>(row) * groups + g] = scale;
-            atomicExch(&epi.tickets[index], 0);
+            reset_ticket(&epi.tickets[index]);
           }
         } else {
           const int token = index / tiles;
           for (int column = tile_n0 + part * 4; column < tile_n0 + kRowsPerGroup; column += 64) {
-            const float4 v = combine4(out_f32, epi.route_weights, epi.route_weights_f32, token,
-                                      top_k, n_rows, column);
+            const float4 v = combine4<true>(out_f32, epi.route_weights, epi.route_weights_f32,
+                                            token, top_k, n_rows, column);
             *reinterpret_cast<uint2*>(epi.combined + static_cast<size_t>(token) * n_rows + column) =
                 pack_bf16x4(v);
           }
-          if (part == 0) atomicExch(&epi.tickets[index], 0);
+          if (part == 0) reset_ticket(&epi.tickets[index]);
         }
       }
     }

@@ -67,7 +67,8 @@ __device__ __forceinline__ uint32_t route_key(float value, int column) {
 
 // Routes one row (one wave): top-k ids of the row at `base` (E <= 64 * NPL)
 // into ids[out_row * top_k + rank], weights likewise.
-template <int NPL, bool kF32>
+// kPublish: ids are read by another workgroup (coherent stores).
+template <int NPL, bool kF32, bool kPublish = false>
 __device__ __forceinline__ void route_row(const char* base, int num_experts, int top_k,
                                           int64_t out_row, int32_t* ids32, int64_t* ids64,
                                           void* weights, int weights_f32) {
@@ -110,7 +111,12 @@ __device__ __forceinline__ void route_row(const char* base, int num_experts, int
   if (lane < top_k) {
     const int64_t out = out_row * top_k + lane;
     const float weight = probability / total;
-    if (ids32 != nullptr) ids32[out] = selected;
+    if (ids32 != nullptr) {
+      if constexpr (kPublish)
+        publish_u32(ids32 + out, static_cast<uint32_t>(selected));
+      else
+        ids32[out] = selected;
+    }
     if (ids64 != nullptr) ids64[out] = selected;
     if (weights_f32)
       static_cast<float*>(weights)[out] = weight;
@@ -294,23 +300,22 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
   if (row < live) {
     const char* lbase = static_cast<const char*>(a.logits) +
                         static_cast<int64_t>(source) * a.logits_stride * (kF32 ? 4 : 2);
-    route_row<NPL, kF32>(lbase, a.num_experts, a.top_k, row, a.ids, nullptr, a.weights,
-                         a.weights_f32);
+    route_row<NPL, kF32, kSort>(lbase, a.num_experts, a.top_k, row, a.ids, nullptr, a.weights,
+                                a.weights_f32);
     quantize_row(a.x + static_cast<int64_t>(source) * a.x_stride, a.hidden,
                  a.q + static_cast<int64_t>(row) * a.hidden,
                  a.scales + static_cast<int64_t>(row) * (a.hidden / kGroup), 1);
   }
 
   if constexpr (kSort) {
-    __threadfence();  // release this workgroup's ids
+    wait_stores();  // this workgroup's published ids are visible device-wide
     __syncthreads();
-    if (threadIdx.x == 0) ticket_shared = atomicAdd(a.ticket, 1);
+    if (threadIdx.x == 0) ticket_shared = take_ticket(a.ticket);
     __syncthreads();
     if (ticket_shared != static_cast<int>(gridDim.x) - 1) return;
-    __threadfence();  // acquire every other workgroup's ids
-    sort_routes_block<kFrontThreads, false>(a.ids, live * a.top_k, a.num_experts, a.tile,
-                                             a.item_rows, smem, a.sort);
-    if (threadIdx.x == 0) atomicExch(a.ticket, 0);
+    sort_routes_block<kFrontThreads, false, true>(a.ids, live * a.top_k, a.num_experts, a.tile,
+                                                   a.item_rows, smem, a.sort);
+    if (threadIdx.x == 0) reset_ticket(a.ticket);
   }
 }
 

@@ -28,9 +28,11 @@ constexpr int sort_shared_ints(int threads, int experts) {
   return (4 + threads / kWave) * experts + threads / kWave;
 }
 
-template <bool kI64>
+// kCollect: the ids were published by other workgroups (coherent loads).
+template <bool kI64, bool kCollect = false>
 __device__ __forceinline__ int load_route_id(const void* ids, int p) {
   if constexpr (kI64) return static_cast<int>(static_cast<const int64_t*>(ids)[p]);
+  if constexpr (kCollect) return static_cast<int>(collect_u32(static_cast<const int32_t*>(ids) + p));
   return static_cast<const int32_t*>(ids)[p];
 }
 
@@ -75,7 +77,7 @@ struct SortOutputs {
 
 // All THREADS threads of the workgroup must call this (it synchronises).
 // num_experts <= THREADS; `smem` holds sort_shared_ints(THREADS, E) ints.
-template <int THREADS, bool kI64>
+template <int THREADS, bool kI64, bool kCollect = false>
 __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int num_experts,
                                   int tile, int item_rows, int* smem, const SortOutputs& out) {
   constexpr int kWaves = THREADS / kWave;
@@ -97,7 +99,7 @@ __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int n
   __syncthreads();
 
   for (int p = tid; p < pairs; p += THREADS) {
-    const int e = load_route_id<kI64>(ids, p);
+    const int e = load_route_id<kI64, kCollect>(ids, p);
     if (e >= 0 && e < num_experts) atomicAdd(&counts[e], 1);
   }
   __syncthreads();
@@ -121,7 +123,7 @@ __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int n
   const uint64_t below = lanemask_lt();
   for (int chunk = 0; chunk < pairs; chunk += THREADS) {
     const int p = chunk + tid;
-    const int e = p < pairs ? load_route_id<kI64>(ids, p) : -1;
+    const int e = p < pairs ? load_route_id<kI64, kCollect>(ids, p) : -1;
     const bool valid = e >= 0 && e < num_experts;
     uint64_t peers = __ballot(valid);
     for (int b = 0; b < bits; ++b) {

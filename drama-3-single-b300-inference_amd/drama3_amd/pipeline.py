@@ -77,7 +77,7 @@ class MoEWorkspace:
 
     def __init__(self, shape: Shape, device: torch.device | str = "cuda", tile: int = SORT_TILE,
                  item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
-                 exact_routes: int = EXACT_ROUTES, fused: bool = True):
+                 exact_routes: int = EXACT_ROUTES, fused_epilogues: bool = False):
         lib = _lib.load()
         self.shape = shape
         self.device = torch.device(device)
@@ -111,11 +111,15 @@ class MoEWorkspace:
         self.act_scales = torch.empty((self.max_rows, i // 128), dtype=torch.float32, device=dev)
         self.down = torch.empty((pairs, h), dtype=torch.float32, device=dev)
         self.out = torch.empty((t, h), dtype=torch.bfloat16, device=dev)
-        # Fused epilogues (SwiGLU requant in FC1, combine in FC2) when the
-        # tiling allows; their tickets start at 0 and every launch leaves 0.
+        # Optional fused epilogues (SwiGLU requant in FC1, combine in FC2)
+        # when the tiling allows; their tickets start at 0 and every launch
+        # leaves 0.  Off by default: with one short workgroup per 16-row tile
+        # the hand-off tail (coherent stores, ticket, finisher) costs more
+        # than the two small kernels it replaces (c2 decode: 90 + 49 us fused
+        # against 71.5 + 7 + 38.4 + 7 us unfused).
         fc1_tile, fc2_tile = lib.d3_expert_tile_rows(h), lib.d3_expert_tile_rows(i)
-        self.fuse_fc1 = fused and 0 < fc1_tile <= 128
-        self.fuse_fc2 = fused and fc2_tile > 0
+        self.fuse_fc1 = fused_epilogues and 0 < fc1_tile <= 128
+        self.fuse_fc2 = fused_epilogues and fc2_tile > 0
         self.fc1_tickets = torch.zeros(self.max_rows * (i // 128) if self.fuse_fc1 else 1, **i32)
         self.fc2_tickets = torch.zeros(t * (h // fc2_tile) if self.fuse_fc2 else 1, **i32)
 
@@ -235,8 +239,8 @@ class MoEWorkspace:
 
     def experts(self, experts, row_count=None, shared=None, out=None, stream=None):
         """FC1, SwiGLU requant, FC2 and combine over the routes sorted by front().
-        Uses the fused epilogues when available (two launches instead of four);
-        a dense shared expert is added by the separate combine."""
+        With ``fused_epilogues`` two launches replace four; a dense shared
+        expert is always added by the separate combine."""
         stream = _lib.stream(self.device) if stream is None else stream
         if self.fuse_fc1:
             self.fc1_swiglu(experts, stream)

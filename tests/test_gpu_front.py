@@ -109,7 +109,8 @@ def test_fused_epilogues_match_unfused_chain(device, config):
     xs, ls = step.x_slots.to(device), step.logits_slots.to(device)
     outs = {}
     for fused in (False, True):
-        ws = MoEWorkspace(Shape(64, w.num_experts, w.hidden, w.intermediate), device, fused=fused)
+        ws = MoEWorkspace(Shape(64, w.num_experts, w.hidden, w.intermediate), device,
+                         fused_epilogues=fused)
         active = torch.empty(64, dtype=torch.int32, device=device)
         count = torch.empty(1, dtype=torch.int32, device=device)
         for _ in range(2):  # second launch proves the tickets were reset
