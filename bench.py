@@ -27,6 +27,11 @@ for _path in (ROOT, ROOT / "drama-3-single-b300-inference_amd"):
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
+# HBM bytes per FC1 launch on this workload, from two rocprofv3 --pmc runs of
+# this script (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors read off
+# the 1 GiB device copy in the same runs); profiles/expert_gemm_c2_hbm_traffic.md.
+# Re-measure whenever the FC1 kernel or its tiling changes.
+FC1_TRAFFIC_BYTES = {"kernel": "expert_gemm_kernel<16,1,0,0>", "bytes": 402153280}
 
 
 def parse():
@@ -37,7 +42,8 @@ def parse():
     p.add_argument("--copies", type=int, default=6, help="rotated weight copies (cold cache)")
     p.add_argument("--kernel-reps", type=int, default=8, help="FC1/FC2 graph repetitions per copy")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-sample-steps", type=int, default=1)
+    p.add_argument("--cpu-sample-steps", type=int, default=3,
+                   help="oracle steps timed for cpu_baseline (about 5 s each on 8 cores)")
     return p.parse_args()
 
 
@@ -63,7 +69,11 @@ def cpu_baseline(workload, step, samples):
 
     from oracle import moe as om
 
-    threads = len(os.sched_getaffinity(0))
+    import threadpoolctl
+
+    np.ones(2) @ np.ones(2)  # load the BLAS so its pool is listed
+    pools = [p["num_threads"] for p in threadpoolctl.threadpool_info() if p["user_api"] == "blas"]
+    threads = max(pools) if pools else 1
     wt = om.ExpertWeights(*(t.view(torch.uint8).numpy() if t.dtype.itemsize == 1 else t.numpy()
                             for t in workload.experts.tensors()))
     occ = step.occupancy.numpy()
@@ -173,10 +183,11 @@ def main():
                   "tolerance_rrms": 1e-3, "ok": err < 1e-3}
         cpu = {"value": round(step_bytes / cpu_us / 1e3, 3), "unit": "GB/s", "cores": threads,
                "kind": "port", "us_per_step": round(cpu_us, 1),
-               "sample": f"{args.cpu_sample_steps} full config-2 decode step(s) ({rows} rows) of the "
-                         "numpy oracle (compaction, routing, quantisation, per-expert FC1/SwiGLU/"
-                         "FC2 in float64 BLAS, combine); BLAS may use all listed cores, the "
-                         "element-wise numpy work runs on one"}
+               "sample": f"median of {args.cpu_sample_steps} full config-2 decode steps ({rows} "
+                         "rows) of the numpy oracle (compaction, routing, quantisation, "
+                         "per-expert dequantise + FC1/SwiGLU/FC2 in float64, combine); `cores` "
+                         "is the BLAS thread pool, the element-wise numpy work runs on one",
+               "host_cpus": len(os.sched_getaffinity(0))}
 
     result = {
         "metric": baseline_metric(),
@@ -202,7 +213,8 @@ def main():
                 "GB_s": round(step_bytes / hot_us / 1e3, 1)},
         "roofline": {"bound": "hbm", "kernel": "expert_gemm FC1", "achieved": round(fc1_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(fc1_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "us_per_launch": round(fc1_us, 2),
+                     "traffic": FC1_TRAFFIC_BYTES["bytes"],
+                     "traffic_kernel": FC1_TRAFFIC_BYTES["kernel"], "us_per_launch": round(fc1_us, 2),
                      "algorithmic_bytes_per_launch": fc1_bytes},
         "fc2": {"us_per_launch": round(fc2_us, 2), "GB_s": round(fc2_gbs, 1),
                 "algorithmic_bytes_per_launch": fc2_bytes},
