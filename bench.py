@@ -31,7 +31,7 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 # this script (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors read off
 # the 1 GiB device copy in the same runs); profiles/expert_gemm_c2_hbm_traffic.md.
 # Re-measure whenever the FC1 kernel or its tiling changes.
-FC1_TRAFFIC_BYTES = {"kernel": "expert_gemm_kernel<16,1,0,0>", "bytes": 402153280}
+FC1_TRAFFIC_BYTES = {"kernel": "expert_gemm_kernel<16,1,0,0,true>", "bytes": 399256914}
 
 
 def parse():
@@ -99,6 +99,7 @@ def main():
     import torch
 
     from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
     from drama3_amd.pipeline import DecodeStep
 
     device = torch.device("cuda:0")
@@ -108,6 +109,10 @@ def main():
     experts0 = w.experts.to(device)
     copies = [experts0] + [workloads.Experts(*(t.clone() for t in experts0.tensors()))
                            for _ in range(max(0, args.copies - 1))]
+    # Load-time re-layout of the fp8 codes (fragment-major), as a deployment
+    # would do once per layer; the step then streams only the packed copy.
+    for c in copies:
+        prepare_experts(c)
     occ = step.occupancy.to(device)
     x_slots, logits_slots = step.x_slots.to(device), step.logits_slots.to(device)
     ds = DecodeStep(workloads.SLOTS, w.num_experts, w.hidden, w.intermediate, device=device)

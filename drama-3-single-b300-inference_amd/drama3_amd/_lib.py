@@ -51,13 +51,16 @@ SIGNATURES = {
     "d3_max_sorted_rows": (_i32, [_i32, _i32, _i32]),
     "d3_max_items": (_i32, [_i32, _i32, _i32]),
     "d3_expert_gemm": (
-        _i32, [_i32, _p, _p, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _p]),
-    "d3_expert_tile_rows": (_i32, [_i32]),
-    "d3_expert_fc1_swiglu": (
-        _i32, [_p, _p, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _p, _p, _p]),
-    "d3_expert_fc2_combine": (
-        _i32, [_p, _p, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _i32, _p, _p,
+        _i32, [_i32, _p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p,
                _p]),
+    "d3_expert_tile_rows": (_i32, [_i32]),
+    "d3_pack_expert_weights": (_i32, [_p, _i32, _i32, _i32, _p, _p]),
+    "d3_expert_fc1_swiglu": (
+        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _p, _p,
+               _p]),
+    "d3_expert_fc2_combine": (
+        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _i32, _p,
+               _p, _p]),
     "d3_silu_mul_quant": (_i32, [_p, _i32, _i32, _p, _p, _p, _i32, _p, _p, _p]),
     "d3_weighted_combine": (_i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
     "d3_combine_experts": (_i32, [_p, _p, _p, _i64, _i32, _i32, _p, _p]),

@@ -26,6 +26,7 @@ import torch
 
 from . import _lib
 from ._lib import DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64, call, ptr
+from .expert_weights import fc1_operands, fc2_operands
 
 SORT_TILE = 16  # MFMA route tile; also the padding granularity of the sorted layout
 # Work items with at most this many routes take the exact (bf16-MFMA) path of
@@ -172,7 +173,8 @@ class MoEWorkspace:
 
     def fc1(self, experts, stream=None) -> None:
         s, stream = self.shape, self._stream(stream)
-        call("d3_expert_gemm", 0, ptr(experts.w13_weight), ptr(experts.w13_scale_inv),
+        w, ws, layout = fc1_operands(experts)
+        call("d3_expert_gemm", 0, ptr(w), ptr(ws), layout,
              s.num_experts, 2 * s.intermediate, s.hidden, ptr(self.q), ptr(self.x_scales),
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
              self.exact_routes, ptr(self.gate_up), None, stream)
@@ -185,7 +187,8 @@ class MoEWorkspace:
 
     def fc2(self, experts, stream=None) -> None:
         s, stream = self.shape, self._stream(stream)
-        call("d3_expert_gemm", 1, ptr(experts.w2_weight), ptr(experts.w2_scale_inv),
+        w, ws, layout = fc2_operands(experts)
+        call("d3_expert_gemm", 1, ptr(w), ptr(ws), layout,
              s.num_experts, s.hidden, s.intermediate, ptr(self.act), ptr(self.act_scales),
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
              self.exact_routes, None, ptr(self.down), stream)
@@ -221,8 +224,8 @@ class MoEWorkspace:
 
     def fc1_swiglu(self, experts, stream=None) -> None:
         s, stream = self.shape, self._stream(stream)
-        call("d3_expert_fc1_swiglu", ptr(experts.w13_weight), ptr(experts.w13_scale_inv),
-             s.num_experts, s.intermediate, s.hidden, ptr(self.q), ptr(self.x_scales),
+        w, ws, layout = fc1_operands(experts)
+        call("d3_expert_fc1_swiglu", ptr(w), ptr(ws), layout, s.num_experts, s.intermediate, s.hidden, ptr(self.q), ptr(self.x_scales),
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
              self.exact_routes, ptr(self.gate_up), ptr(self.act), ptr(self.act_scales),
              ptr(self.fc1_tickets), stream)
@@ -230,8 +233,8 @@ class MoEWorkspace:
     def fc2_combine(self, experts, out=None, stream=None) -> torch.Tensor:
         s, stream = self.shape, self._stream(stream)
         out = self.out if out is None else out
-        call("d3_expert_fc2_combine", ptr(experts.w2_weight), ptr(experts.w2_scale_inv),
-             s.num_experts, s.hidden, s.intermediate, ptr(self.act), ptr(self.act_scales),
+        w, ws, layout = fc2_operands(experts)
+        call("d3_expert_fc2_combine", ptr(w), ptr(ws), layout, s.num_experts, s.hidden, s.intermediate, ptr(self.act), ptr(self.act_scales),
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
              self.exact_routes, ptr(self.down), ptr(self.weights), dtype_code(self.weights.dtype),
              ptr(out), ptr(self.fc2_tickets), stream)
@@ -278,14 +281,14 @@ class DenseExpert:
         """q / x_scales: the already quantised rows [rows, H]; returns fp32 [rows, H]."""
         stream = _lib.stream(q.device) if stream is None else stream
         h, i = self.hidden, self.intermediate
-        call("d3_expert_gemm", 0, ptr(experts.w13_weight), ptr(experts.w13_scale_inv), 1, 2 * i,
-             h, ptr(q), ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items),
+        w13, s13, layout13 = fc1_operands(experts)
+        w2, s2, layout2 = fc2_operands(experts)
+        call("d3_expert_gemm", 0, ptr(w13), ptr(s13), layout13, 1, 2 * i, h, ptr(q), ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items),
              ptr(self.num_items), self.max_items, self.exact_routes, ptr(self.gate_up), None,
              stream)
         call("d3_silu_mul_quant", ptr(self.gate_up), self.rows, i, None, None, None, 0,
              ptr(self.act), ptr(self.act_scales), stream)
-        call("d3_expert_gemm", 1, ptr(experts.w2_weight), ptr(experts.w2_scale_inv), 1, h, i,
-             ptr(self.act), ptr(self.act_scales), ptr(self.sorted_ids), 1, ptr(self.items),
+        call("d3_expert_gemm", 1, ptr(w2), ptr(s2), layout2, 1, h, i, ptr(self.act), ptr(self.act_scales), ptr(self.sorted_ids), 1, ptr(self.items),
              ptr(self.num_items), self.max_items, self.exact_routes, None, ptr(self.down),
              stream)
         return self.down

@@ -14,6 +14,9 @@
  * Weight layout (reference src/drama3/kernels.py:290-318):
  *               w13 [E, 2I, H] fp8 rows [gate; up],  s13 [E, 2I/128, H/128]
  *               w2  [E, H, I]  fp8,                  s2  [E, H/128, I/128]
+ *               The fp8 codes may instead be given in the fragment-major
+ *               layout of d3_pack_expert_weights (same size, scales
+ *               unchanged), selected by a weight_layout argument.
  * Device row counts: wherever `row_count` appears, a non-NULL pointer names an
  * int32 on the device holding the live number of rows (<= the host `rows`
  * capacity); rows at or beyond it are left untouched.  NULL means all `rows`.
@@ -39,6 +42,10 @@ extern "C" {
 #define D3_DTYPE_F32 1
 #define D3_DTYPE_I32 2
 #define D3_DTYPE_I64 3
+
+/* Expert weight layouts accepted by the expert GEMM entry points. */
+#define D3_LAYOUT_REFERENCE 0 /* w [E, N, K] row-major, as the checkpoint stores it */
+#define D3_LAYOUT_FRAGMENT 1  /* fragment-major, produced by d3_pack_expert_weights */
 
 /* Version of this ABI (bumped on any signature change). */
 int d3_abi_version(void);
@@ -159,8 +166,8 @@ int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);
  * Replaces expert_up_kernel / expert_down_kernel (src/drama3/kernels.py:290-322)
  * and Fish fused_moe_gemm as driven by native_moe (kernels.py:734-778).
  * For every work item {e, start, n}: rows p in [start, start+n) of the
- * sorted route list contract with expert e's weight w[e] (fp8 [N, K], block
- * scales ws[e] [N/128, K/128]) on MFMA 16x16x128 FP8 tiles:
+ * sorted route list contract with expert e's weight w[e] (fp8 [N, K] in
+ * weight_layout, block scales ws[e] [N/128, K/128]) on MFMA tiles:
  *   out[p, j] = sum_k (w[e,j,k] ws[e,j/128,k/128]) (a[r,k] as[r,k/128])
  * accumulated in fp32, where the activation row r is
  *   mode 0 (FC1): token sorted_ids[p] / top_k of a [*, K] (gather = permute),
@@ -176,14 +183,29 @@ int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);
  * Supported: K in {256, 512, 768, 1024, 1536, 2048}; N a multiple of the
  * workgroup row tile (64 for K >= 1024, 128 for K = 512/768, 256 for K = 256).
  */
-int d3_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32_t num_experts,
-                   int32_t n, int32_t k, const uint8_t *a, const float *a_scales,
+int d3_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32_t weight_layout,
+                   int32_t num_experts, int32_t n, int32_t k, const uint8_t *a, const float *a_scales,
                    const int32_t *sorted_ids, int32_t top_k, const int32_t *items,
                    const int32_t *num_items, int32_t max_items, int32_t exact_routes,
                    uint16_t *out_bf16, float *out_f32, void *stream);
 
 /* Weight rows per workgroup tile of d3_expert_gemm for contraction length k. */
 int32_t d3_expert_tile_rows(int32_t k);
+
+/*
+ * A9/A11 weight preparation (once, at load time).
+ * Counterpart of the reference's load-time re-layout of the expert weights
+ * for its FlashInfer path (src/drama3/model.py:195-205: [up | gate] copies
+ * and blocked_moe_weight shuffling).  w fp8 [E, N, K] (reference layout) ->
+ * packed fp8, same size, fragment-major: each 16-row tile of N is stored as
+ * [K/128 blocks][2 halves][64 lanes][16 bytes], where lane l holds bytes
+ * [64*half + 16*(l/16), +16) of K block kb of row 16*tile + l%16.  One
+ * expert-GEMM wave then reads 1 KiB of contiguous memory per load
+ * instruction.  N % 16 == 0, K % 128 == 0, w and packed must not overlap.
+ * The block scales keep their layout.
+ */
+int d3_pack_expert_weights(const uint8_t *w, int32_t num_experts, int32_t n, int32_t k,
+                           uint8_t *packed, void *stream);
 
 /*
  * A9 + A10  FC1 with the SwiGLU requantisation fused into its epilogue.
@@ -194,8 +216,8 @@ int32_t d3_expert_tile_rows(int32_t k);
  * tickets: int32 [max sorted rows * I/128], all 0 before the first launch and
  * left at 0.  Needs d3_expert_tile_rows(hidden) <= 128.
  */
-int d3_expert_fc1_swiglu(const uint8_t *w13, const float *s13, int32_t num_experts,
-                         int32_t intermediate, int32_t hidden, const uint8_t *q,
+int d3_expert_fc1_swiglu(const uint8_t *w13, const float *s13, int32_t weight_layout,
+                         int32_t num_experts, int32_t intermediate, int32_t hidden, const uint8_t *q,
                          const float *x_scales, const int32_t *sorted_ids, int32_t top_k,
                          const int32_t *items, const int32_t *num_items, int32_t max_items,
                          int32_t exact_routes, uint16_t *gate_up, uint8_t *act, float *act_scales,
@@ -210,8 +232,9 @@ int d3_expert_fc1_swiglu(const uint8_t *w13, const float *s13, int32_t num_exper
  * tickets: int32 [tokens * hidden / d3_expert_tile_rows(intermediate)], all
  * 0 before the first launch and left at 0.
  */
-int d3_expert_fc2_combine(const uint8_t *w2, const float *s2, int32_t num_experts, int32_t hidden,
-                          int32_t intermediate, const uint8_t *act, const float *act_scales,
+int d3_expert_fc2_combine(const uint8_t *w2, const float *s2, int32_t weight_layout,
+                          int32_t num_experts, int32_t hidden, int32_t intermediate,
+                          const uint8_t *act, const float *act_scales,
                           const int32_t *sorted_ids, int32_t top_k, const int32_t *items,
                           const int32_t *num_items, int32_t max_items, int32_t exact_routes,
                           float *down, const void *weights, int32_t weights_dtype, uint16_t *out,

@@ -82,7 +82,7 @@ def test_capacity_helpers(lib):
     for pairs, experts, tile in ((32, 16, 16), (384, 128, 16), (33280, 128, 64), (0, 8, 16)):
         assert lib.d3_max_sorted_rows(pairs, experts, tile) == om.max_sorted_rows(pairs, experts, tile)
     assert lib.d3_max_items(384, 128, 64) == (384 + 128 * 63) // 64
-    assert lib.d3_abi_version() == 1
+    assert lib.d3_abi_version() == 2
 
 
 def test_contract_violations_raise_value_error(lib):
@@ -98,8 +98,13 @@ def test_contract_violations_raise_value_error(lib):
         _lib.call("d3_sort_routes", 16, 3, 4, None, 8, 16, 16, 16, 16, 16, 16, 16, 8, None, 16,
                   None, 0, None, None, None)
     with pytest.raises(ValueError, match="K="):
-        _lib.call("d3_expert_gemm", 0, 16, 16, 4, 512, 384, 16, 16, 16, 8, 16, 16, 4, 64, 16,
+        _lib.call("d3_expert_gemm", 0, 16, 16, 0, 4, 512, 384, 16, 16, 16, 8, 16, 16, 4, 64, 16,
                   None, None)
+    with pytest.raises(ValueError, match="weight_layout"):
+        _lib.call("d3_expert_gemm", 0, 16, 16, 7, 4, 512, 512, 16, 16, 16, 8, 16, 16, 4, 64, 16,
+                  None, None)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        _lib.call("d3_pack_expert_weights", 16, 4, 24, 128, 32, None)
     assert "K=" in lib.d3_last_error().decode()
 
 
@@ -125,3 +130,25 @@ def test_ctypes_types_are_plain():
     allowed = {ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_char_p}
     for restype, argtypes in _lib.SIGNATURES.values():
         assert restype in allowed and all(a in allowed for a in argtypes)
+
+
+def test_packed_operands_follow_their_source_tensor():
+    """prepare_experts' packed copies are used only while the checkpoint-layout
+    tensor they were made from is unchanged (host logic; no kernel runs)."""
+    import torch
+
+    from drama3_amd import expert_weights as ew
+    from drama3_amd.workloads import make_experts
+
+    ex = make_experts(torch.Generator("cpu").manual_seed(0), 2, 256, 128)
+    assert ew.fc1_operands(ex)[2] == ew.LAYOUT_REFERENCE
+    for name in ("w13", "w2"):
+        weight = getattr(ex, f"{name}_weight")
+        setattr(ex, f"d3_{name}_packed", torch.empty_like(weight))
+        setattr(ex, f"d3_{name}_source", ew._identity(weight))
+    w, scales, layout = ew.fc1_operands(ex)
+    assert layout == ew.LAYOUT_FRAGMENT and w is ex.d3_w13_packed and scales is ex.w13_scale_inv
+    ex.w2_weight.view(torch.uint8).add_(1)
+    assert ew.fc2_operands(ex)[2] == ew.LAYOUT_REFERENCE
+    ex.w13_weight = ex.w13_weight.clone()
+    assert ew.fc1_operands(ex)[2] == ew.LAYOUT_REFERENCE
