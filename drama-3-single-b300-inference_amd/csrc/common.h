@@ -83,30 +83,79 @@ __device__ __forceinline__ uint32_t quantize_one(float x, float scale) {
 }
 
 // ---------------------------------------------------------------------------
-// wave64 reductions
+// wave64 reductions on DPP lane moves (VALU operand modifiers, no LDS
+// round trip): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and
+// row_mirror reduce each 16-lane row so that every lane of the row holds the
+// result; row_bcast:15 / row_bcast:31 fold the four rows into lane 63, which
+// readlane broadcasts.  Lanes not written by a DPP move receive the
+// operation's identity.
 // ---------------------------------------------------------------------------
+constexpr int kDppQuad1032 = 0xb1;
+constexpr int kDppQuad2301 = 0x4e;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t v, uint32_t identity) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      static_cast<int>(identity), static_cast<int>(v), kCtrl, kRowMask, 0xf, false));
+}
+
+struct MaxF32 {
+  static constexpr uint32_t kIdentity = 0xff800000u;  // -inf
+  __device__ static uint32_t apply(uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }
+};
+struct SumF32 {
+  static constexpr uint32_t kIdentity = 0u;  // +0
+  __device__ static uint32_t apply(uint32_t a, uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  }
+};
+struct MaxU32 {
+  static constexpr uint32_t kIdentity = 0u;
+  __device__ static uint32_t apply(uint32_t a, uint32_t b) { return a > b ? a : b; }
+};
+
+// Every lane of each 16-lane row gets the reduction over its row.
+template <class Op>
+__device__ __forceinline__ uint32_t row_reduce(uint32_t v) {
+  v = Op::apply(v, dpp_move<kDppQuad1032>(v, Op::kIdentity));
+  v = Op::apply(v, dpp_move<kDppQuad2301>(v, Op::kIdentity));
+  v = Op::apply(v, dpp_move<kDppRowHalfMirror>(v, Op::kIdentity));
+  v = Op::apply(v, dpp_move<kDppRowMirror>(v, Op::kIdentity));
+  return v;
+}
+
+// Every lane gets the reduction over the wave (a wave-uniform value).
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t v) {
+  v = row_reduce<Op>(v);
+  v = Op::apply(v, dpp_move<kDppRowBcast15, 0xa>(v, Op::kIdentity));
+  v = Op::apply(v, dpp_move<kDppRowBcast31, 0xc>(v, Op::kIdentity));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), kWave - 1));
+}
+
+// Reductions over aligned segments of WIDTH lanes (16 or 64); every lane of
+// a segment receives the segment's result.
 template <int WIDTH>
 __device__ __forceinline__ float segment_max(float v) {
-#pragma unroll
-  for (int offset = WIDTH / 2; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset));
-  return v;
+  static_assert(WIDTH == 16 || WIDTH == kWave, "segments of 16 or 64 lanes");
+  if constexpr (WIDTH == 16) return __uint_as_float(row_reduce<MaxF32>(__float_as_uint(v)));
+  return __uint_as_float(wave_reduce<MaxF32>(__float_as_uint(v)));
 }
 
 template <int WIDTH>
 __device__ __forceinline__ float segment_sum(float v) {
-#pragma unroll
-  for (int offset = WIDTH / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset);
-  return v;
+  static_assert(WIDTH == 16 || WIDTH == kWave, "segments of 16 or 64 lanes");
+  if constexpr (WIDTH == 16) return __uint_as_float(row_reduce<SumF32>(__float_as_uint(v)));
+  return __uint_as_float(wave_reduce<SumF32>(__float_as_uint(v)));
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    const uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), offset));
-    v = v > other ? v : other;
-  }
-  return v;
-}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return wave_reduce<MaxU32>(v); }
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 

@@ -431,7 +431,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 }
 
 // ---------------------------------------------------------------------------
-// SwiGLU + per-128 requantisation: one wave per FC1 row, 8 elements per lane.
+// SwiGLU + per-128 requantisation: one thread per 8 columns, so a 16-lane
+// DPP row is exactly one 128-column group (I / 8 threads per FC1 row, a
+// multiple of 16).  The gate/up loads are issued together with the loads
+// of the row count and sorted id (every row below `rows` is inside the
+// buffer, live or not), so a row costs one memory latency.
 // ---------------------------------------------------------------------------
 constexpr int kRowThreads = 256;
 
@@ -440,55 +444,77 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(
     const int32_t* __restrict__ row_count, const int32_t* __restrict__ sorted_ids,
     const int32_t* __restrict__ pairs_dev, int pairs_host, uint8_t* __restrict__ act,
     float* __restrict__ act_scales) {
-  const int row = (blockIdx.x * kRowThreads + threadIdx.x) / kWave;
-  const int lane = lane_id();
+  const int per_row = intermediate / 8;
+  const int64_t thread = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x;
+  const int row = static_cast<int>(thread / per_row);
+  const int column = static_cast<int>(thread % per_row) * 8;
+  if (row >= rows) return;  // whole 16-lane groups agree
+  const uint16_t* gate = gate_up + static_cast<size_t>(row) * 2 * intermediate + column;
+  const uint4 graw = *reinterpret_cast<const uint4*>(gate);
+  const uint4 uraw = *reinterpret_cast<const uint4*>(gate + intermediate);
   if (row >= live_rows(row_count, rows)) return;
   if (sorted_ids != nullptr) {
     const int pairs = pairs_dev != nullptr ? *pairs_dev : pairs_host;
     if (sorted_ids[row] >= pairs) return;  // padding slot of the sorted layout
   }
-  const uint16_t* gate = gate_up + static_cast<size_t>(row) * 2 * intermediate;
-  const uint16_t* up = gate + intermediate;
-  uint8_t* out = act + static_cast<size_t>(row) * intermediate;
-  const int groups = intermediate / kGroup;
-  for (int base = 0; base < intermediate; base += 8 * kWave) {
-    const int column = base + lane * 8;
-    const bool inside = column < intermediate;
-    uint4 graw = make_uint4(0u, 0u, 0u, 0u), uraw = make_uint4(0u, 0u, 0u, 0u);
-    if (inside) {
-      graw = *reinterpret_cast<const uint4*>(gate + column);
-      uraw = *reinterpret_cast<const uint4*>(up + column);
-    }
-    uint2 codes;
-    const float scale = swiglu_quant_group(graw, uraw, &codes);
-    if (inside) {
-      *reinterpret_cast<uint2*>(out + column) = codes;
-      if ((lane & 15) == 0) act_scales[static_cast<size_t>(row) * groups + column / kGroup] = scale;
-    }
-  }
+  uint2 codes;
+  const float scale = swiglu_quant_group(graw, uraw, &codes);
+  *reinterpret_cast<uint2*>(act + static_cast<size_t>(row) * intermediate + column) = codes;
+  if ((lane_id() & 15) == 0)
+    act_scales[static_cast<size_t>(row) * (intermediate / kGroup) + column / kGroup] = scale;
 }
 
 // ---------------------------------------------------------------------------
 // Weighted combine: out[t] = bf16(sum_r w[t,r] * down[t*K + r]) in rank order.
 // ---------------------------------------------------------------------------
+// One workgroup per (row, 1024-column slice).  With top_k = 8 every load of
+// the slice (8 route rows + 8 weights + the row count) is issued before the
+// first FMA.
+template <int kTopK>
+__device__ __forceinline__ float4 combine4_fixed(const float* down, const void* weights,
+                                                 int weights_f32, int token, int hidden,
+                                                 int column) {
+  float w[kTopK];
+  float4 y[kTopK];
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    w[r] = route_weight(weights, weights_f32, static_cast<size_t>(token) * kTopK + r);
+    y[r] = *reinterpret_cast<const float4*>(down + (static_cast<size_t>(token) * kTopK + r) * hidden +
+                                            column);
+  }
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    acc.x = fmaf(w[r], y[r].x, acc.x);
+    acc.y = fmaf(w[r], y[r].y, acc.y);
+    acc.z = fmaf(w[r], y[r].z, acc.z);
+    acc.w = fmaf(w[r], y[r].w, acc.w);
+  }
+  return acc;
+}
+
+constexpr int kCombineColumns = kRowThreads * 4;
+
 __global__ __launch_bounds__(kRowThreads) void weighted_combine_kernel(
     const float* __restrict__ down, const void* __restrict__ weights, int weights_f32, int rows,
     int top_k, int hidden, const int32_t* __restrict__ row_count,
     const float* __restrict__ shared, uint16_t* __restrict__ out) {
-  const int row = blockIdx.x;
+  const int slices = (hidden + kCombineColumns - 1) / kCombineColumns;
+  const int row = blockIdx.x / slices;
+  const int column = (blockIdx.x % slices) * kCombineColumns + threadIdx.x * 4;
+  if (column >= hidden) return;
+  float4 acc = top_k == 8 ? combine4_fixed<8>(down, weights, weights_f32, row, hidden, column)
+                          : combine4(down, weights, weights_f32, row, top_k, hidden, column);
   if (row >= live_rows(row_count, rows)) return;
-  for (int column = threadIdx.x * 4; column < hidden; column += kRowThreads * 4) {
-    float4 acc = combine4(down, weights, weights_f32, row, top_k, hidden, column);
-    if (shared != nullptr) {
-      // Dense shared expert added to the routed output, each rounded to bf16.
-      const float4 s = *reinterpret_cast<const float4*>(shared + static_cast<size_t>(row) * hidden + column);
-      acc.x = bf16_to_f32(f32_to_bf16(acc.x)) + bf16_to_f32(f32_to_bf16(s.x));
-      acc.y = bf16_to_f32(f32_to_bf16(acc.y)) + bf16_to_f32(f32_to_bf16(s.y));
-      acc.z = bf16_to_f32(f32_to_bf16(acc.z)) + bf16_to_f32(f32_to_bf16(s.z));
-      acc.w = bf16_to_f32(f32_to_bf16(acc.w)) + bf16_to_f32(f32_to_bf16(s.w));
-    }
-    *reinterpret_cast<uint2*>(out + static_cast<size_t>(row) * hidden + column) = pack_bf16x4(acc);
+  if (shared != nullptr) {
+    // Dense shared expert added to the routed output, each rounded to bf16.
+    const float4 s = *reinterpret_cast<const float4*>(shared + static_cast<size_t>(row) * hidden + column);
+    acc.x = bf16_to_f32(f32_to_bf16(acc.x)) + bf16_to_f32(f32_to_bf16(s.x));
+    acc.y = bf16_to_f32(f32_to_bf16(acc.y)) + bf16_to_f32(f32_to_bf16(s.y));
+    acc.z = bf16_to_f32(f32_to_bf16(acc.z)) + bf16_to_f32(f32_to_bf16(s.z));
+    acc.w = bf16_to_f32(f32_to_bf16(acc.w)) + bf16_to_f32(f32_to_bf16(s.w));
   }
+  *reinterpret_cast<uint2*>(out + static_cast<size_t>(row) * hidden + column) = pack_bf16x4(acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -720,7 +746,8 @@ extern "C" int d3_silu_mul_quant(const uint16_t* gate_up, int32_t rows, int32_t 
     clear_error();
     return D3_OK;
   }
-  const int blocks = (rows + kRowThreads / kWave - 1) / (kRowThreads / kWave);
+  const int64_t threads = static_cast<int64_t>(rows) * (intermediate / 8);
+  const int blocks = static_cast<int>((threads + kRowThreads - 1) / kRowThreads);
   hipLaunchKernelGGL(silu_mul_quant_kernel, dim3(blocks), dim3(kRowThreads), 0, as_stream(stream),
                      gate_up, rows, intermediate, row_count, sorted_ids, pairs_dev, pairs, act,
                      act_scales);
@@ -742,7 +769,9 @@ extern "C" int d3_weighted_combine(const float* down, const void* weights, int32
     clear_error();
     return D3_OK;
   }
-  hipLaunchKernelGGL(weighted_combine_kernel, dim3(rows), dim3(kRowThreads), 0, as_stream(stream),
+  const int slices = (hidden + kCombineColumns - 1) / kCombineColumns;
+  hipLaunchKernelGGL(weighted_combine_kernel, dim3(rows * slices), dim3(kRowThreads), 0,
+                     as_stream(stream),
                      down, weights, weights_dtype == D3_DTYPE_F32 ? 1 : 0, rows, top_k, hidden,
                      row_count, shared, out);
   D3_LAUNCHED("weighted_combine");

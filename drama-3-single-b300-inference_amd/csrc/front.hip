@@ -1,9 +1,9 @@
 // Front end of the MoE step: active-slot compaction, top-k routing and
 // per-128 FP8 activation quantisation.
 //
-// All three are row-parallel integer / byte work: one wavefront per row (or
-// one workgroup for the compaction), coalesced 16-byte loads, wave64 ballots
-// and shuffles instead of LDS round trips.
+// All three are row-parallel integer / byte work: one wavefront per routed
+// row, one workgroup per quantised row (or for the compaction), coalesced
+// 16-byte loads, wave64 ballots and DPP reductions instead of LDS round trips.
 #include <math.h>
 
 #include "common.h"
@@ -94,19 +94,30 @@ __device__ __forceinline__ void route_row(const char* base, int num_experts, int
   for (int j = 0; j < NPL; ++j) denominator += expf(values[j] - row_max);
   denominator = segment_sum<kWave>(denominator);
 
-  // Top-k by repeated wave arg-max over unique keys; lane k keeps rank k.
+  // Top-k by repeated wave arg-max over unique keys; lane k keeps rank k and
+  // the winner's logit (read from the owning lane, not reloaded).
   int selected = -1;
+  float selected_value = 0.0f;
   for (int k = 0; k < top_k; ++k) {
     uint32_t best = 0u;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) best = keys[j] > best ? keys[j] : best;
     best = wave_max_u32(best);
+    const int column = 65535 - static_cast<int>(best & 0xffffu);  // uniform
+    float mine = values[0];
+#pragma unroll
+    for (int j = 1; j < NPL; ++j) mine = column / kWave == j ? values[j] : mine;
+    const float value =
+        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), column % kWave));
 #pragma unroll
     for (int j = 0; j < NPL; ++j) keys[j] = keys[j] == best ? 0u : keys[j];
-    if (lane == k) selected = 65535 - static_cast<int>(best & 0xffffu);
+    if (lane == k) {
+      selected = column;
+      selected_value = value;
+    }
   }
   float probability = 0.0f;
-  if (lane < top_k) probability = expf(load_logit<kF32>(base, selected) - row_max) / denominator;
+  if (lane < top_k) probability = expf(selected_value - row_max) / denominator;
   const float total = segment_sum<kWave>(probability);
   if (lane < top_k) {
     const int64_t out = out_row * top_k + lane;
@@ -140,29 +151,44 @@ __global__ __launch_bounds__(kFrontThreads) void route_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Quantisation: one wave per row; 8 elements per lane, 16 lanes per group.
+// Quantisation: one workgroup per row, its 4 waves splitting the row into
+// 512-element chunks (8 elements per lane, 16 lanes per 128-group).
 // ---------------------------------------------------------------------------
+constexpr int kRowWaves = kFrontThreads / kWave;
 constexpr int kMaxRowChunks = 8;  // rows up to 8 * 512 = 4096 elements
+constexpr int kPartChunks = kMaxRowChunks / kRowWaves;
+constexpr int kChunk = 8 * kWave;
 
-// Quantises one row (one wave) of `width` bf16 values: q row + per-128 scales
-// at scales[group * scale_stride].  All loads of the row are issued before
-// any arithmetic so the row costs one memory latency.
-__device__ __forceinline__ void quantize_row(const uint16_t* in, int width, uint8_t* out,
-                                             float* scales, int64_t scale_stride) {
+// Chunks part, part + 4, ... of one row, loaded before any arithmetic so the
+// row costs one memory latency.
+struct RowPart {
+  uint4 raw[kPartChunks];
+};
+
+__device__ __forceinline__ void load_row_part(const uint16_t* in, int width, int part,
+                                              RowPart& row) {
   const int lane = lane_id();
-  uint4 raw[kMaxRowChunks];
 #pragma unroll
-  for (int c = 0; c < kMaxRowChunks; ++c) {
-    const int column = c * 8 * kWave + lane * 8;
-    raw[c] = make_uint4(0u, 0u, 0u, 0u);
-    if (column < width) raw[c] = *reinterpret_cast<const uint4*>(in + column);
+  for (int i = 0; i < kPartChunks; ++i) {
+    const int column = (part + i * kRowWaves) * kChunk + lane * 8;
+    row.raw[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (column < width) row.raw[i] = *reinterpret_cast<const uint4*>(in + column);
   }
+}
+
+// Quantises the chunks loaded by load_row_part: q bytes and per-128 scales
+// at scales[group * scale_stride].
+__device__ __forceinline__ void quantize_row_part(const RowPart& row, int width, int part,
+                                                  uint8_t* out, float* scales,
+                                                  int64_t scale_stride) {
+  const int lane = lane_id();
+  const uint4* raw = row.raw;
 #pragma unroll
-  for (int c = 0; c < kMaxRowChunks; ++c) {
-    const int column = c * 8 * kWave + lane * 8;
-    if (c * 8 * kWave >= width) break;  // uniform
+  for (int i = 0; i < kPartChunks; ++i) {
+    const int column = (part + i * kRowWaves) * kChunk + lane * 8;
+    if ((part + i * kRowWaves) * kChunk >= width) break;  // uniform
     const bool inside = column < width;  // whole 16-lane groups agree
-    const uint32_t words[4] = {raw[c].x, raw[c].y, raw[c].z, raw[c].w};
+    const uint32_t words[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
     float v[8];
     float amax = 0.0f;
 #pragma unroll
@@ -186,6 +212,7 @@ __device__ __forceinline__ void quantize_row(const uint16_t* in, int width, uint
   }
 }
 
+
 template <bool kPrepare>
 __global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
     const uint16_t* __restrict__ x, int64_t stride, int rows, int width,
@@ -195,17 +222,20 @@ __global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
     const void* __restrict__ router, int router_f32, int64_t router_stride, int num_experts,
     const void* __restrict__ row_slots, int row_slots_i64, int64_t padding_start,
     float* __restrict__ logits_out) {
-  const int row = (blockIdx.x * kFrontThreads + threadIdx.x) / kWave;
+  const int row = blockIdx.x;
+  const int part = threadIdx.x / kWave;
   const int lane = lane_id();
   const int live = live_rows(row_count, rows);
   if (row >= live) return;
   const int source = row_index != nullptr ? row_index[row] : row;
   const int groups = width / kGroup;
-  quantize_row(x + static_cast<int64_t>(source) * stride, width,
-               q + static_cast<int64_t>(row) * width,
-               transposed ? scales + row : scales + static_cast<int64_t>(row) * groups,
-               transposed ? rows : 1);
+  RowPart xrow;
+  load_row_part(x + static_cast<int64_t>(source) * stride, width, part, xrow);
+  quantize_row_part(xrow, width, part, q + static_cast<int64_t>(row) * width,
+                    transposed ? scales + row : scales + static_cast<int64_t>(row) * groups,
+                    transposed ? rows : 1);
   if constexpr (kPrepare) {
+    if (part != 0) return;
     // Reserved padding rows reuse row 0's routing (moe_input.py:31-37).
     int router_row = row;
     if (row_slots != nullptr) {
@@ -225,9 +255,10 @@ __global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
 
 // ---------------------------------------------------------------------------
 // Fused front end of one MoE step: slot compaction + routing + quantisation
-// (4 rows per workgroup, one per wave) and, in the last workgroup to finish,
-// the route sort.  The last workgroup is found with an atomic ticket after a
-// release fence; nobody waits, so the launch cannot deadlock, and the last
+// (one row per workgroup: wave 0 routes it, the 4 waves quantise a quarter
+// each) and, in the last workgroup to finish, the route sort.  The last
+// workgroup is found with an atomic ticket after the ids were published with
+// coherent stores; nobody waits, so the launch cannot deadlock, and the last
 // workgroup resets the ticket so the next launch (or graph replay) starts at 0.
 // ---------------------------------------------------------------------------
 constexpr int kMaxFrontExperts = 512;
@@ -265,7 +296,7 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
   __shared__ int ticket_shared;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
-  const int row = blockIdx.x * (kFrontThreads / kWave) + wave;
+  const int row = blockIdx.x;  // one row per workgroup; wave = part of the row
 
   int live;
   int source = -1;
@@ -298,13 +329,18 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
   }
 
   if (row < live) {
-    const char* lbase = static_cast<const char*>(a.logits) +
-                        static_cast<int64_t>(source) * a.logits_stride * (kF32 ? 4 : 2);
-    route_row<NPL, kF32, kSort>(lbase, a.num_experts, a.top_k, row, a.ids, nullptr, a.weights,
-                                a.weights_f32);
-    quantize_row(a.x + static_cast<int64_t>(source) * a.x_stride, a.hidden,
-                 a.q + static_cast<int64_t>(row) * a.hidden,
-                 a.scales + static_cast<int64_t>(row) * (a.hidden / kGroup), 1);
+    // Each wave loads its part of the x row first, so the transfer overlaps
+    // the routing (wave 0).
+    RowPart xrow;
+    load_row_part(a.x + static_cast<int64_t>(source) * a.x_stride, a.hidden, wave, xrow);
+    if (wave == 0) {
+      const char* lbase = static_cast<const char*>(a.logits) +
+                          static_cast<int64_t>(source) * a.logits_stride * (kF32 ? 4 : 2);
+      route_row<NPL, kF32, kSort>(lbase, a.num_experts, a.top_k, row, a.ids, nullptr, a.weights,
+                                  a.weights_f32);
+    }
+    quantize_row_part(xrow, a.hidden, wave, a.q + static_cast<int64_t>(row) * a.hidden,
+                      a.scales + static_cast<int64_t>(row) * (a.hidden / kGroup), 1);
   }
 
   if constexpr (kSort) {
@@ -397,7 +433,7 @@ extern "C" int d3_quantize_rows(const uint16_t* x, int64_t x_row_stride, int32_t
     clear_error();
     return D3_OK;
   }
-  hipLaunchKernelGGL(quantize_kernel<false>, dim3(wave_blocks(rows)), dim3(kFrontThreads), 0,
+  hipLaunchKernelGGL(quantize_kernel<false>, dim3(rows), dim3(kFrontThreads), 0,
                      as_stream(stream), x, x_row_stride, rows, width, row_index, row_count, q,
                      scales, scales_transposed ? 1 : 0, nullptr, 0, 0, 0, nullptr, 0, 0,
                      nullptr);
@@ -429,7 +465,7 @@ extern "C" int d3_prepare_moe_input(const uint16_t* x, int64_t x_row_stride, con
     clear_error();
     return D3_OK;
   }
-  hipLaunchKernelGGL(quantize_kernel<true>, dim3(wave_blocks(rows)), dim3(kFrontThreads), 0,
+  hipLaunchKernelGGL(quantize_kernel<true>, dim3(rows), dim3(kFrontThreads), 0,
                      as_stream(stream), x, x_row_stride, rows, hidden, nullptr, nullptr, q,
                      scales, 1, router, router_dtype == D3_DTYPE_F32 ? 1 : 0, router_row_stride,
                      num_experts, row_slots, row_slots_dtype == D3_DTYPE_I64 ? 1 : 0,
@@ -501,7 +537,7 @@ extern "C" int d3_moe_front(const uint8_t* occupancy, int32_t num_slots, int32_t
                        logits_row_stride, rows, row_index, row_count, hidden, num_experts, top_k,
                        ids, weights, weights_dtype == D3_DTYPE_F32 ? 1 : 0, q, scales, tile,
                        item_rows, out, ticket};
-  const dim3 grid(rows > 0 ? wave_blocks(rows) : 1), block(kFrontThreads);
+  const dim3 grid(rows > 0 ? rows : 1), block(kFrontThreads);
   hipStream_t s = as_stream(stream);
   const bool f32 = logits_dtype == D3_DTYPE_F32;
 #define D3_FRONT_LAUNCH(NPL)                                                                  \

@@ -42,11 +42,16 @@ __device__ __forceinline__ int block_inclusive_scan(int value, int* wave_totals,
   constexpr int kWaves = THREADS / kWave;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
-#pragma unroll
-  for (int offset = 1; offset < kWave; offset <<= 1) {
-    const int other = __shfl_up(value, offset);
-    if (lane >= offset) value += other;
-  }
+  // Wave inclusive scan on DPP moves: row_shr 1, 2, 4, 8 inside each 16-lane
+  // row, then row_bcast 15 / 31 carry the row totals into the later rows.
+  uint32_t v = static_cast<uint32_t>(value);
+  v += dpp_move<0x111>(v, 0u);
+  v += dpp_move<0x112>(v, 0u);
+  v += dpp_move<0x114>(v, 0u);
+  v += dpp_move<0x118>(v, 0u);
+  v += dpp_move<kDppRowBcast15, 0xa>(v, 0u);
+  v += dpp_move<kDppRowBcast31, 0xc>(v, 0u);
+  value = static_cast<int>(v);
   if (lane == kWave - 1) wave_totals[wave] = value;
   __syncthreads();
   int prefix = 0;
@@ -91,6 +96,17 @@ __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int n
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
 
+  // Small batches (decode) read the ids once into registers and reuse them
+  // for the scatter; larger ones read them again per chunk.
+  constexpr int kCached = 4;
+  const bool cache = pairs <= THREADS * kCached;
+  int cached[kCached];
+#pragma unroll
+  for (int c = 0; c < kCached; ++c) {
+    const int p = c * THREADS + tid;
+    cached[c] = cache && p < pairs ? load_route_id<kI64, kCollect>(ids, p) : -1;
+  }
+
   for (int e = tid; e < num_experts; e += THREADS) {
     counts[e] = 0;
     running[e] = 0;
@@ -98,9 +114,15 @@ __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int n
   for (int i = tid; i < kWaves * num_experts; i += THREADS) wave_counts[i] = 0;
   __syncthreads();
 
-  for (int p = tid; p < pairs; p += THREADS) {
-    const int e = load_route_id<kI64, kCollect>(ids, p);
-    if (e >= 0 && e < num_experts) atomicAdd(&counts[e], 1);
+  if (cache) {
+#pragma unroll
+    for (int c = 0; c < kCached; ++c)
+      if (cached[c] >= 0 && cached[c] < num_experts) atomicAdd(&counts[cached[c]], 1);
+  } else {
+    for (int p = tid; p < pairs; p += THREADS) {
+      const int e = load_route_id<kI64, kCollect>(ids, p);
+      if (e >= 0 && e < num_experts) atomicAdd(&counts[e], 1);
+    }
   }
   __syncthreads();
 
@@ -121,10 +143,10 @@ __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int n
   int bits = 0;
   while ((1 << bits) < num_experts) ++bits;
   const uint64_t below = lanemask_lt();
-  for (int chunk = 0; chunk < pairs; chunk += THREADS) {
+  // One chunk of THREADS pairs (all threads call it: it synchronises).
+  auto scatter = [&](int chunk, int e) {
     const int p = chunk + tid;
-    const int e = p < pairs ? load_route_id<kI64, kCollect>(ids, p) : -1;
-    const bool valid = e >= 0 && e < num_experts;
+    const bool valid = p < pairs && e >= 0 && e < num_experts;
     uint64_t peers = __ballot(valid);
     for (int b = 0; b < bits; ++b) {
       const bool bit = valid && ((e >> b) & 1);
@@ -149,6 +171,16 @@ __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int n
       wave_counts[wave * num_experts + e] = 0;
     }
     __syncthreads();
+  };
+  if (cache) {
+#pragma unroll
+    for (int c = 0; c < kCached; ++c)
+      if (c * THREADS < pairs) scatter(c * THREADS, cached[c]);  // uniform condition
+  } else {
+    for (int chunk = 0; chunk < pairs; chunk += THREADS) {
+      const int p = chunk + tid;
+      scatter(chunk, p < pairs ? load_route_id<kI64, kCollect>(ids, p) : -1);
+    }
   }
 
   for (int e = tid; e < num_experts; e += THREADS) {
