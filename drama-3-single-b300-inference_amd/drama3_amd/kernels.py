@@ -228,3 +228,48 @@ def add_norm(x, residual, weight, epsilon):
     call("d3_add_norm", ptr(x), ptr(residual), ptr(weight), float(epsilon),
          x.shape[0], x.shape[1], ptr(out), _lib.stream(x.device))
     return out
+
+
+def routed_moe(x, router, experts, decode=True, *, row_slots=None, padding_start=None):
+    """``DramaModel.routed_moe`` (``model.py:520-583``) as a function of the
+    layer's inputs: top-8 routing of ``router`` [T, E], the routed FP8 SwiGLU
+    experts and the weighted combine -> bf16 [T, H].
+
+    The reference dispatches three numerically different backends (Triton
+    GEMV for <= 8 rows, Fish's sorted GEMM for native prefill, FlashInfer for
+    decode batches above 8 rows); here every batch runs the same MI355X path
+    with ``route_kernel``'s ranking rule (``kernels.py:364-368``).  ``decode``
+    is accepted for the signature.  With ``row_slots`` / ``padding_start``
+    (both or neither), rows whose slot is >= ``padding_start`` take row 0's
+    routing, the reserved-padding router of ``moe_input.py:31-37``.
+    """
+    _check_rows(x)
+    require_cuda(router)
+    if router.dim() != 2 or len(router) != len(x) or router.stride(1) != 1:
+        raise ValueError("router must be [T, E] with unit column stride, one row per x row")
+    if router.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("router must be bfloat16 or float32")
+    if (row_slots is None) != (padding_start is None):
+        raise ValueError("Reserved padding routing requires both row_slots and padding_start")
+    e, h, i = check_experts(experts, x.shape[1])
+    if router.shape[1] != e:
+        raise ValueError(f"router has {router.shape[1]} experts, weights have {e}")
+    rows = len(x)
+    out = torch.empty((rows, h), dtype=torch.bfloat16, device=x.device)
+    if rows == 0:
+        return out
+    logits = router
+    if row_slots is not None:
+        if (row_slots.shape != (rows,) or row_slots.device != x.device
+                or row_slots.dtype not in (torch.int32, torch.int64)):
+            raise ValueError("Expected one integer slot per MoE row on the same device")
+        if not isinstance(padding_start, int) or padding_start <= 0:
+            raise ValueError("padding_start must be a positive reserved-slot boundary")
+        source = torch.arange(rows, device=x.device)
+        source = torch.where(row_slots >= padding_start, torch.zeros_like(source), source)
+        logits = router.index_select(0, source)
+    if x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    ws = MoEWorkspace(Shape(rows, e, h, i, TOP_K), x.device,
+                      item_rows=128 if rows > 128 else None)
+    return ws.forward(x, logits, experts, out=out)

@@ -199,3 +199,31 @@ def test_reference_api_small_and_native(device):
     expected = om.expert_ffn(np_bf16(x), oids, ow, oracle_weights(w.experts))
     assert_bf16_close(np_bf16(a), expected, **EXACT)
     assert rrms(bf16_to_f32(np_bf16(a)), bf16_to_f32(expected)) < RRMS_REFERENCE
+
+
+def test_routed_moe_dispatch_and_padding_router(device):
+    """routed_moe (model.py:520-583): same result as the reference-API chain,
+    and rows in reserved padding slots route exactly like row 0."""
+    from drama3_amd import workloads
+    from drama3_amd.kernels import routed_moe
+
+    w = workloads.config1()
+    x, logits = w.steps[0].packed()
+    experts = w.experts.to(device)
+    xd, ld = x.to(device), logits.to(device)
+    out = routed_moe(xd, ld, experts, True)
+    torch.cuda.synchronize()
+    ow, oids = om.route(np_f32(logits))
+    expected = om.expert_ffn(np_bf16(x), oids, ow, oracle_weights(w.experts))
+    assert_bf16_close(np_bf16(out), expected, **EXACT)
+    # slots >= 32 are reserved padding: rows 1 and 3 take row 0's routing
+    slots = torch.tensor([3, 40, 17, 62], dtype=torch.int64, device=device)
+    padded = routed_moe(xd, ld, experts, True, row_slots=slots, padding_start=32)
+    forced = ld.clone()
+    forced[1] = ld[0]
+    forced[3] = ld[0]
+    ref = routed_moe(xd, forced, experts, True)
+    torch.cuda.synchronize()
+    assert torch.equal(padded, ref)
+    with pytest.raises(ValueError):
+        routed_moe(xd, ld, experts, True, row_slots=slots)
