@@ -2,8 +2,9 @@
 one MI355X.
 
 One step = device-side slot compaction + routing + FP8 quantisation + route
-sort + FC1 + SwiGLU requant + FC2 + weighted combine over the live rows of 64
-persistent slots (H=2048, 128 experts, I=768, top-8), captured in a HIP graph.
+sort + FC1 + FC2 (SwiGLU requant in its prologue) + weighted combine over the
+live rows of 64 persistent slots (H=2048, 128 experts, I=768, top-8), captured
+in a HIP graph.
 Inputs are resident in HBM before timing.  ``value`` is the cold-cache rate:
 the timed replays rotate over several copies of the expert weights whose
 total far exceeds the 256 MB MALL, so every step streams its weights from HBM.
@@ -31,7 +32,7 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 # this script (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors read off
 # the 1 GiB device copy in the same runs); profiles/expert_gemm_c2_hbm_traffic.md.
 # Re-measure whenever the FC1 kernel or its tiling changes.
-FC1_TRAFFIC_BYTES = {"kernel": "expert_gemm_kernel<16,1,0,0,true>", "bytes": 399256914}
+FC1_TRAFFIC_BYTES = {"kernel": "expert_gemm_kernel<16,1,0,0,true>", "bytes": 399241830}
 
 
 def parse():
@@ -172,7 +173,7 @@ def main():
         return g
 
     fc1_graph = kernel_graph(ws.fc1)
-    fc2_graph = kernel_graph(ws.fc2)
+    fc2_graph = kernel_graph(ws.fc2_swiglu if ws.swiglu_in_fc2 else ws.fc2)
     launches = args.kernel_reps * len(copies)
     time_graphs(torch, [fc1_graph, fc2_graph], 2)  # warm-up
     fc1_us = time_graphs(torch, [fc1_graph], 5) / launches
@@ -181,8 +182,10 @@ def main():
     routes = rows * workloads.TOP_K
     fc1_bytes = used * (2 * i * h + 4 * (2 * i // 128) * (h // 128)) + rows * h + rows * (h // 128) * 4 \
         + routes * 2 * i * 2
-    fc2_bytes = used * (h * i + 4 * (h // 128) * (i // 128)) + routes * i + routes * (i // 128) * 4 \
-        + routes * h * 4
+    # FC2 reads its activations as fp8 codes + scales, or (SwiGLU in its
+    # prologue) as FC1's bf16 gate|up rows.
+    act_bytes = routes * 2 * i * 2 if ws.swiglu_in_fc2 else routes * i + routes * (i // 128) * 4
+    fc2_bytes = used * (h * i + 4 * (h // 128) * (i // 128)) + act_bytes + routes * h * 4
     # Practical streaming rate of this GPU for context: a large device copy
     # (torch), counting bytes read plus bytes written.
     src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
@@ -245,7 +248,8 @@ def main():
                      "traffic": FC1_TRAFFIC_BYTES["bytes"],
                      "traffic_kernel": FC1_TRAFFIC_BYTES["kernel"], "us_per_launch": round(fc1_us, 2),
                      "algorithmic_bytes_per_launch": fc1_bytes},
-        "fc2": {"us_per_launch": round(fc2_us, 2), "GB_s": round(fc2_gbs, 1),
+        "fc2": {"kernel": "expert_fc2_swiglu" if ws.swiglu_in_fc2 else "expert_gemm FC2",
+                "us_per_launch": round(fc2_us, 2), "GB_s": round(fc2_gbs, 1),
                 "algorithmic_bytes_per_launch": fc2_bytes},
         "device_copy_GB_s": round(copy_gbs, 1),
         "cpu_baseline": cpu,

@@ -239,13 +239,20 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   // order): the first half of the weights, then the route ids (scalar loads,
   // counted apart from the vector stream) and the activation rows they name,
   // then the second half of the weights.  The staging wait then covers only
-  // the first half, whose MFMAs overlap the second half's transfer.
+  // the first half, whose MFMAs overlap the second half's transfer (MODE 2
+  // also computes the SwiGLU requantisation of the staged rows meanwhile).
   const int stage_col = threadIdx.x >> 4;   // route column staged by this thread
   const int stage_part = threadIdx.x & 15;  // 16 threads per route row
   constexpr int kChunks = K / 256;          // 16-byte chunks per thread and row
   int4 b_stage[kChunks];
   float b_stage_scale = 0.0f;
   int b_stage_target = -1;
+  // MODE 2: the live (route column, K group) units of the tile, packed
+  // densely: unit u = 16 p + stage_col is column u / KB, group u % KB, and
+  // its 16-thread row holds 8 gate and 8 up bf16 values per thread.  Dead
+  // columns are not computed (their output columns are never stored).
+  uint4 g_stage[MODE == 2 ? KB : 1], u_stage[MODE == 2 ? KB : 1];
+  int live_units = 0;
   auto fetch_tile = [&](int m0) {
     int pair = 0;
 #pragma unroll
@@ -256,6 +263,23 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     const int r = m0 + stage_col;
     const bool live = r < routes;
     const int position = first + r;
+    b_stage_target = live ? (MODE == 0 ? position : pair) : -1;
+    if constexpr (MODE == 2) {
+      live_units = min(16, routes - m0) * KB;
+      const uint16_t* rows = reinterpret_cast<const uint16_t*>(act) +
+                             static_cast<size_t>(first + m0) * (2 * K) + stage_part * 8;
+#pragma unroll
+      for (int p = 0; p < KB; ++p) {
+        const int u = p * 16 + stage_col;
+        if (p * 16 < live_units && u < live_units) {
+          const int col = u / KB;
+          const uint16_t* src = rows + static_cast<size_t>(col) * (2 * K) + (u - col * KB) * kGroup;
+          g_stage[p] = *reinterpret_cast<const uint4*>(src);
+          u_stage[p] = *reinterpret_cast<const uint4*>(src + K);
+        }
+      }
+      return;
+    }
     const size_t a_row = MODE == 0 ? static_cast<size_t>(pair / top_k) : static_cast<size_t>(position);
     const uint8_t* src = act + a_row * K;
 #pragma unroll
@@ -264,13 +288,30 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       if (live) b_stage[j] = *reinterpret_cast<const int4*>(src + j * 256 + stage_part * 16);
     }
     b_stage_scale = (live && stage_part < KB) ? act_scales[a_row * KB + stage_part] : 0.0f;
-    b_stage_target = live ? (MODE == 0 ? position : pair) : -1;
   };
   auto store_tile = [&]() {
+    if constexpr (MODE == 2) {
+      // SwiGLU + e4m3 requantisation of the staged units, the same function
+      // as silu_mul_quant_kernel, so the tile holds the bytes that kernel
+      // would have written.  A unit's 16 threads are one DPP row.
 #pragma unroll
-    for (int j = 0; j < kChunks; ++j)
-      *reinterpret_cast<int4*>(b_tile + stage_col * kStride + j * 256 + stage_part * 16) = b_stage[j];
-    if (stage_part < KB) b_scales[stage_col * KB + stage_part] = b_stage_scale;
+      for (int p = 0; p < KB; ++p) {
+        const int u = p * 16 + stage_col;
+        if (p * 16 < live_units && u < live_units) {
+          const int col = u / KB;
+          const int kb = u - col * KB;
+          uint2 codes;
+          const float scale = swiglu_quant_group(g_stage[p], u_stage[p], &codes);
+          *reinterpret_cast<uint2*>(b_tile + col * kStride + kb * kGroup + stage_part * 8) = codes;
+          if (stage_part == 0) b_scales[col * KB + kb] = scale;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kChunks; ++j)
+        *reinterpret_cast<int4*>(b_tile + stage_col * kStride + j * 256 + stage_part * 16) = b_stage[j];
+      if (stage_part < KB) b_scales[stage_col * KB + stage_part] = b_stage_scale;
+    }
     if (stage_part == 0) b_target[stage_col] = b_stage_target;
   };
 
@@ -281,13 +322,16 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     if constexpr (kPacked) return load_packed_fragment(tile, kb, lane);
     return load_fragment(tile + row16 * K, kb, group);
   };
-  constexpr int kFirstHalf = KB > 1 ? KB / 2 : KB;
+  constexpr int kFirstHalf = MODE == 2 ? 0 : (KB > 1 ? KB / 2 : KB);
   int32x8 a_frag[RT][KB];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int kb = 0; kb < kFirstHalf; ++kb) a_frag[rt][kb] = weight_fragment(rt, kb);
   __builtin_amdgcn_sched_barrier(0);
+  // MODE 2 issues the gate / up rows before any weight (they are addressed
+  // by sorted position, no route id needed), so the SwiGLU arithmetic runs
+  // while the whole weight tile is in flight.
   fetch_tile(0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -301,11 +345,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) w_scale[rt][kb] = wsexp[((n0 + rt * 16) / kGroup) * KB + kb];
 
-  for (int m0 = 0; m0 < routes; m0 += 16) {
-    if (m0 > 0) {
-      __syncthreads();  // previous tile fully consumed
-      fetch_tile(m0);
-    }
+  // One route tile against the register-resident weights.  The first tile
+  // runs outside the loop: staged registers carried around a loop back edge
+  // make the compiler wait for every outstanding load (the weights
+  // included) before staging.
+  auto run_tile = [&]() {
     store_tile();
     __syncthreads();
 
@@ -427,6 +471,12 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
         }
       }
     }
+  };
+  run_tile();
+  for (int m0 = 16; m0 < routes; m0 += 16) {
+    __syncthreads();  // previous tile fully consumed
+    fetch_tile(m0);
+    run_tile();
   }
 }
 
@@ -571,6 +621,10 @@ void launch_gemm(dim3 grid, hipStream_t s, const GemmLaunch& g) {
                        g.exact_routes, g.out_bf16, g.out_f32, g.epi);
 }
 
+// FC2 with the SwiGLU prologue stages 2 x 16 bytes of gate / up per K block
+// and thread next to the weights; beyond 8 K blocks that spills.
+constexpr int kMaxSwigluKB = 8;
+
 // Row tiles per wave: keep each wave's register-resident weights near 32 KiB.
 constexpr int rt_for(int kb) { return kb >= 8 ? 1 : (kb >= 4 ? 2 : 4); }
 constexpr int tile_rows_for(int kb) { return kGemmWaves * rt_for(kb) * 16; }
@@ -594,8 +648,13 @@ int dispatch_gemm(const GemmLaunch& g, hipStream_t s) {
     launch_gemm<KB, RT, 1, kFuseCombine>(grid, s, g);
   else if (g.mode == 0)
     launch_gemm<KB, RT, 0, kFuseNone>(grid, s, g);
-  else
+  else if (g.mode == 1)
     launch_gemm<KB, RT, 1, kFuseNone>(grid, s, g);
+  else if constexpr (KB <= kMaxSwigluKB)
+    launch_gemm<KB, RT, 2, kFuseNone>(grid, s, g);
+  else
+    return set_error(D3_ERR_UNSUPPORTED, "expert_fc2_swiglu: intermediate %d > %d", KB * kGroup,
+                     kMaxSwigluKB * kGroup);
   return D3_OK;
 }
 
@@ -626,7 +685,7 @@ int tile_rows(int k) {
 bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
 int check_gemm(const GemmLaunch& g, int num_experts, int k, const char* name) {
-  D3_REQUIRE(g.w && g.ws && g.a && g.as && g.sorted_ids && g.items && g.num_items,
+  D3_REQUIRE(g.w && g.ws && g.a && (g.as || g.mode == 2) && g.sorted_ids && g.items && g.num_items,
              "%s: null pointer", name);
   D3_REQUIRE(g.packed == D3_LAYOUT_REFERENCE || g.packed == D3_LAYOUT_FRAGMENT,
              "%s: weight_layout must be D3_LAYOUT_REFERENCE or D3_LAYOUT_FRAGMENT", name);
@@ -732,6 +791,29 @@ extern "C" int d3_expert_fc2_combine(const uint8_t* w2, const float* s2, int32_t
   status = run_gemm(g, intermediate, as_stream(stream));
   if (status != D3_OK) return status;
   D3_LAUNCHED("expert_fc2_combine");
+}
+
+extern "C" int d3_expert_fc2_swiglu(const uint8_t* w2, const float* s2, int32_t weight_layout,
+                                    int32_t num_experts, int32_t hidden, int32_t intermediate,
+                                    const uint16_t* gate_up, const int32_t* sorted_ids,
+                                    int32_t top_k, const int32_t* items, const int32_t* num_items,
+                                    int32_t max_items, int32_t exact_routes, float* down,
+                                    void* stream) {
+  D3_REQUIRE(gate_up && down, "expert_fc2_swiglu: null pointer");
+  D3_REQUIRE(aligned(gate_up, 16) && aligned(down, 16), "expert_fc2_swiglu: alignment");
+  const GemmLaunch g{2, kFuseNone, weight_layout, w2, s2, hidden,
+                     reinterpret_cast<const uint8_t*>(gate_up), nullptr, sorted_ids, top_k,
+                     reinterpret_cast<const int4*>(items), num_items, max_items, exact_routes,
+                     nullptr, down, EpilogueArgs{}};
+  int status = check_gemm(g, num_experts, intermediate, "expert_fc2_swiglu");
+  if (status != D3_OK) return status;
+  if (max_items == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  status = run_gemm(g, intermediate, as_stream(stream));
+  if (status != D3_OK) return status;
+  D3_LAUNCHED("expert_fc2_swiglu");
 }
 
 extern "C" int d3_silu_mul_quant(const uint16_t* gate_up, int32_t rows, int32_t intermediate,

@@ -15,6 +15,8 @@ Step (one kernel each, all on the current stream):
                                                        (kernels.py:290-301)
     silu_mul_quant   SwiGLU + e4m3 requant             (kernels.py:344,748)
     expert_gemm FC2  W2, fp32 per pair (unpermute)     (kernels.py:304-318)
+    (decode-sized items: FC2 computes the SwiGLU requant in its prologue,
+    d3_expert_fc2_swiglu, and silu_mul_quant is not launched)
     weighted_combine sum_r w[t,r] y[t*K+r] -> bf16     (kernels.py:319-322,779)
 """
 
@@ -78,7 +80,8 @@ class MoEWorkspace:
 
     def __init__(self, shape: Shape, device: torch.device | str = "cuda", tile: int = SORT_TILE,
                  item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
-                 exact_routes: int = EXACT_ROUTES, fused_epilogues: bool = False):
+                 exact_routes: int = EXACT_ROUTES, fused_epilogues: bool = False,
+                 swiglu_in_fc2: bool | None = None):
         lib = _lib.load()
         self.shape = shape
         self.device = torch.device(device)
@@ -121,6 +124,12 @@ class MoEWorkspace:
         fc1_tile, fc2_tile = lib.d3_expert_tile_rows(h), lib.d3_expert_tile_rows(i)
         self.fuse_fc1 = fused_epilogues and 0 < fc1_tile <= 128
         self.fuse_fc2 = fused_epilogues and fc2_tile > 0
+        # SwiGLU requant in FC2's prologue: every FC2 workgroup of an item
+        # recomputes the item's activations, which is free while its weights
+        # stream in as long as items are a few route tiles (decode).
+        if swiglu_in_fc2 is None:
+            swiglu_in_fc2 = self.item_rows <= EXACT_ROUTES and i <= 1024
+        self.swiglu_in_fc2 = swiglu_in_fc2 and not self.fuse_fc1 and not self.fuse_fc2
         self.fc1_tickets = torch.zeros(self.max_rows * (i // 128) if self.fuse_fc1 else 1, **i32)
         self.fc2_tickets = torch.zeros(t * (h // fc2_tile) if self.fuse_fc2 else 1, **i32)
 
@@ -193,6 +202,15 @@ class MoEWorkspace:
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
              self.exact_routes, None, ptr(self.down), stream)
 
+    def fc2_swiglu(self, experts, stream=None) -> None:
+        """FC2 whose workgroups compute the SwiGLU requant of their routes
+        from gate_up themselves (same bytes as activation() + fc2())."""
+        s, stream = self.shape, self._stream(stream)
+        w, ws, layout = fc2_operands(experts)
+        call("d3_expert_fc2_swiglu", ptr(w), ptr(ws), layout, s.num_experts, s.hidden,
+             s.intermediate, ptr(self.gate_up), ptr(self.sorted_ids), s.top_k, ptr(self.items),
+             ptr(self.num_items), self.max_items, self.exact_routes, ptr(self.down), stream)
+
     def combine(self, weights: torch.Tensor | None = None, row_count=None, shared=None,
                 out=None, stream=None) -> torch.Tensor:
         s, stream = self.shape, self._stream(stream)
@@ -210,9 +228,15 @@ class MoEWorkspace:
         self.quantize(x, row_index, row_count, stream)
         self.sort(ids, row_count, stream)
         self.fc1(experts, stream)
-        self.activation(stream)
-        self.fc2(experts, stream)
+        self._fc2_stage(experts, stream)
         return self.combine(weights, row_count, shared, out, stream)
+
+    def _fc2_stage(self, experts, stream) -> None:
+        if self.swiglu_in_fc2:
+            self.fc2_swiglu(experts, stream)
+        else:
+            self.activation(stream)
+            self.fc2(experts, stream)
 
     def forward(self, x, logits, experts, row_index=None, row_count=None, shared=None,
                 out=None, stream=None) -> torch.Tensor:
@@ -249,10 +273,14 @@ class MoEWorkspace:
             self.fc1_swiglu(experts, stream)
         else:
             self.fc1(experts, stream)
-            self.activation(stream)
         if self.fuse_fc2 and shared is None:
+            if not self.fuse_fc1:
+                self.activation(stream)
             return self.fc2_combine(experts, out, stream)
-        self.fc2(experts, stream)
+        if self.fuse_fc1:
+            self.fc2(experts, stream)
+        else:
+            self._fc2_stage(experts, stream)
         return self.combine(None, row_count, shared, out, stream)
 
 

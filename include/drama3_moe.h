@@ -241,6 +241,24 @@ int d3_expert_fc2_combine(const uint8_t *w2, const float *s2, int32_t weight_lay
                           int32_t *tickets, void *stream);
 
 /*
+ * A10 + A11  FC2 with the SwiGLU requantisation done in its prologue.
+ * Replaces Fish silu_mul_quant (src/drama3/kernels.py:344) followed by the
+ * FC2 GEMM (kernels.py:304-318).  d3_expert_gemm mode 1 (down fp32 by pair,
+ * n = hidden, k = intermediate), except that each workgroup computes the
+ * activation tile itself from gate_up bf16 [sorted rows, 2I] ([gate | up])
+ * exactly as d3_silu_mul_quant would (same fp8 codes and scales), while its
+ * weight loads are in flight; no act / act_scales buffers are read or
+ * written.  Every workgroup of an item recomputes the item's activations,
+ * so this suits decode-sized items (a few route tiles).
+ * Supported: intermediate in {256, 512, 768, 1024}.
+ */
+int d3_expert_fc2_swiglu(const uint8_t *w2, const float *s2, int32_t weight_layout,
+                         int32_t num_experts, int32_t hidden, int32_t intermediate,
+                         const uint16_t *gate_up, const int32_t *sorted_ids, int32_t top_k,
+                         const int32_t *items, const int32_t *num_items, int32_t max_items,
+                         int32_t exact_routes, float *down, void *stream);
+
+/*
  * A10  SwiGLU + per-128 FP8 requantisation of FC1 rows.
  * Replaces Fish quantize_groups(silu_mul_quant_kernel, gate_up, I)
  * (src/drama3/kernels.py:344,748).  gate_up bf16 [rows, 2I] ([gate | up]) ->

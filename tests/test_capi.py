@@ -103,6 +103,9 @@ def test_contract_violations_raise_value_error(lib):
     with pytest.raises(ValueError, match="weight_layout"):
         _lib.call("d3_expert_gemm", 0, 16, 16, 7, 4, 512, 512, 16, 16, 16, 8, 16, 16, 4, 64, 16,
                   None, None)
+    with pytest.raises(ValueError, match="intermediate 2048"):
+        _lib.call("d3_expert_fc2_swiglu", 16, 16, 0, 4, 1024, 2048, 16, 16, 8, 16, 16, 4, 64, 16,
+                  None)
     with pytest.raises(ValueError, match="multiple of 16"):
         _lib.call("d3_pack_expert_weights", 16, 4, 24, 128, 32, None)
     assert "K=" in lib.d3_last_error().decode()

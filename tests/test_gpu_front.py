@@ -98,7 +98,8 @@ def test_fused_front_row_mode_with_index(device):
 @pytest.mark.parametrize("config", [1, 2, 3])
 def test_fused_epilogues_match_unfused_chain(device, config):
     """FC1 + fused SwiGLU requant and FC2 + fused combine give exactly the
-    bytes of the four-kernel chain, and leave every ticket at 0."""
+    bytes of the four-kernel chain, and leave every ticket at 0; FC2 with the
+    SwiGLU requant in its prologue (three kernels) gives the same output."""
     from drama3_amd import workloads
     from drama3_amd.pipeline import MoEWorkspace, Shape
 
@@ -107,10 +108,11 @@ def test_fused_epilogues_match_unfused_chain(device, config):
     experts = w.experts.to(device)
     occ = step.occupancy.to(device)
     xs, ls = step.x_slots.to(device), step.logits_slots.to(device)
+    variants = {"chain": dict(swiglu_in_fc2=False), "fused": dict(fused_epilogues=True),
+                "prologue": dict(swiglu_in_fc2=True)}
     outs = {}
-    for fused in (False, True):
-        ws = MoEWorkspace(Shape(64, w.num_experts, w.hidden, w.intermediate), device,
-                         fused_epilogues=fused)
+    for name, options in variants.items():
+        ws = MoEWorkspace(Shape(64, w.num_experts, w.hidden, w.intermediate), device, **options)
         active = torch.empty(64, dtype=torch.int32, device=device)
         count = torch.empty(1, dtype=torch.int32, device=device)
         for _ in range(2):  # second launch proves the tickets were reset
@@ -120,10 +122,12 @@ def test_fused_epilogues_match_unfused_chain(device, config):
         n = int(count.item())
         total = int(ws.total.item())
         valid = ws.sorted_ids.cpu().numpy()[:total] < n * 8
-        outs[fused] = (out[:n].cpu(), np_u8(ws.act)[:total][valid], np_f32(ws.act_scales)[:total][valid])
-        if fused:
-            assert ws.fuse_fc1 and ws.fuse_fc2
+        outs[name] = (out[:n].cpu(), np_u8(ws.act)[:total][valid], np_f32(ws.act_scales)[:total][valid])
+        if name == "fused":
+            assert ws.fuse_fc1 and ws.fuse_fc2 and not ws.swiglu_in_fc2
             assert int(ws.fc1_tickets.abs().sum()) == 0 and int(ws.fc2_tickets.abs().sum()) == 0
-    assert torch.equal(outs[True][0], outs[False][0])
-    assert np.array_equal(outs[True][1], outs[False][1])
-    assert np.array_equal(outs[True][2], outs[False][2])
+        assert ws.swiglu_in_fc2 == (name == "prologue")
+    for name in ("fused", "prologue"):
+        assert torch.equal(outs[name][0], outs["chain"][0]), name
+    assert np.array_equal(outs["fused"][1], outs["chain"][1])
+    assert np.array_equal(outs["fused"][2], outs["chain"][2])

@@ -285,6 +285,33 @@ def test_activation_and_fc2_stages(device, path):
     assert np.all(np.abs(got - expected) <= rel * scale + 1e-6 * np.abs(expected))
 
 
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("path", ["exact", "fp8"])
+@pytest.mark.parametrize("hidden,inter,experts,tokens", [(1024, 256, 16, 4), (2048, 768, 128, 52),
+                                                         (512, 512, 8, 200), (1024, 1024, 16, 24)])
+def test_fc2_swiglu_prologue_matches_separate_stages(device, hidden, inter, experts, tokens, path,
+                                                     packed):
+    """d3_expert_fc2_swiglu (SwiGLU requant inside FC2) gives the bytes of
+    silu_mul_quant followed by FC2, for single- and multi-tile items (200
+    tokens over 8 experts: items of 128 routes, eight route tiles)."""
+    from drama3_amd.expert_weights import prepare_experts
+
+    ws, dev_ex, _, _, _ = _stage_setup(
+        device, tokens, experts, hidden, inter, seed=tokens + inter,
+        exact_routes=EXACT_ALWAYS if path == "exact" else FP8_ALWAYS)
+    if packed:
+        prepare_experts(dev_ex)
+    ws.fc1(dev_ex)
+    ws.activation()
+    ws.down.fill_(float("nan"))
+    ws.fc2(dev_ex)
+    separate = ws.down.clone()
+    ws.down.fill_(float("nan"))
+    ws.fc2_swiglu(dev_ex)
+    torch.cuda.synchronize()
+    assert torch.equal(ws.down.view(torch.int32), separate.view(torch.int32))
+
+
 # --------------------------------------------------------------------------- A12
 def test_combine_kernels(device):
     from drama3_amd.kernels import (add_norm, combine_experts, combine_experts_add_norm,
