@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--copies", type=int, default=6, help="rotated weight copies (cold cache)")
     p.add_argument("--kernel-reps", type=int, default=8, help="FC1/FC2 graph repetitions per copy")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--fused", action="store_true",
+                   help="time the one-launch step (d3_moe_decode_step) instead of the kernel chain")
     p.add_argument("--cpu-sample-steps", type=int, default=3,
                    help="oracle steps timed for cpu_baseline (about 5 s each on 8 cores)")
     return p.parse_args()
@@ -116,7 +118,8 @@ def main():
         prepare_experts(c)
     occ = step.occupancy.to(device)
     x_slots, logits_slots = step.x_slots.to(device), step.logits_slots.to(device)
-    ds = DecodeStep(workloads.SLOTS, w.num_experts, w.hidden, w.intermediate, device=device)
+    ds = DecodeStep(workloads.SLOTS, w.num_experts, w.hidden, w.intermediate, device=device,
+                    fused=args.fused)
 
     # eager warm-up run, then one graph per weight copy
     side = torch.cuda.Stream()
@@ -159,7 +162,7 @@ def main():
     time_steps(copies, args.warmup)
     step_us, out = time_steps(copies, args.steps)
     hot_us, _ = time_steps([copies[0]] * len(copies), args.steps)
-    used = int((ws.counts > 0).sum().item())
+    used = int(torch.unique(ws.ids[:rows]).numel())  # experts with at least one route
     step_bytes = workloads.algorithmic_bytes(w, step, used)
 
     # Dominant kernel (FC1, 2/3 of the weight bytes) and FC2, timed alone:
@@ -239,6 +242,7 @@ def main():
                    "experts": e, "hidden": h, "intermediate": i, "top_k": workloads.TOP_K,
                    "used_experts": used, "algorithmic_bytes_per_step": step_bytes,
                    "weight_copies": len(copies),
+                   "step": "one launch (d3_moe_decode_step)" if args.fused else "kernel chain",
                    "timing": "hipGraph of one step per weight copy (the copies act as consecutive "
                              "layers), replayed; cold: every step streams its copy from HBM"},
         "hot": {"us_per_step": round(hot_us, 2),

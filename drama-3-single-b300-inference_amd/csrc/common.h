@@ -180,6 +180,9 @@ __device__ __forceinline__ void publish_u64(void* p, uint64_t v) {
 __device__ __forceinline__ void publish_u32(void* p, uint32_t v) {
   __hip_atomic_store(static_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void publish_u16(void* p, uint16_t v) {
+  __hip_atomic_store(static_cast<uint16_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ uint64_t collect_u64(const void* p) {
   return __hip_atomic_load(static_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);

@@ -1,0 +1,156 @@
+// Expert-GEMM building blocks shared by the standalone expert kernels
+// (expert.hip) and the one-launch decode step (step.hip): MFMA operand
+// fragments of the two weight layouts, the exact (bf16-widened) and FP8 MFMA
+// blocks, the SwiGLU + e4m3 requantisation of one 128-column group and the
+// rank-order combine.
+//
+// Operand layout of the 16x16x128 MFMA block (both operands): lane l holds
+// row / column l % 16 and 32 contraction bytes of group g = l / 16, bytes
+// 0-15 = k in [16g, 16g+16) and bytes 16-31 = k in [64+16g, 64+16g+16).
+// The product is invariant under any k permutation applied to both.
+#pragma once
+
+#include "common.h"
+
+namespace d3 {
+
+typedef int int32x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef int int32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kGemmWaves = 4;
+constexpr int kGemmThreads = kGemmWaves * kWave;
+
+// Row tiles per wave: keep each wave's register-resident weights near 32 KiB.
+constexpr int rt_for(int kb) { return kb >= 8 ? 1 : (kb >= 4 ? 2 : 4); }
+constexpr int tile_rows_for(int kb) { return kGemmWaves * rt_for(kb) * 16; }
+
+// Fragment of one row in the reference layout [N, K] (row = this lane's row).
+__device__ __forceinline__ int32x8 load_fragment(const uint8_t* row, int kb, int group) {
+  const uint8_t* p = row + kb * kGroup + group * 16;
+  const int4 lo = *reinterpret_cast<const int4*>(p);
+  const int4 hi = *reinterpret_cast<const int4*>(p + 64);
+  int32x8 v;
+  v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+  v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+  return v;
+}
+
+// Fragment of a 16-row tile in the fragment-major layout: the tile is
+// stored as [K block][half][lane][16 bytes], so each of the two loads is
+// 1 KiB of contiguous memory per wave, read non-temporally (every weight
+// byte is used once).
+__device__ __forceinline__ int32x8 load_packed_fragment(const uint8_t* tile, int kb, int lane) {
+  const int32x4* p = reinterpret_cast<const int32x4*>(tile + kb * 2048) + lane;
+  const int32x4 lo = __builtin_nontemporal_load(p);
+  const int32x4 hi = __builtin_nontemporal_load(p + kWave);
+  int32x8 v;
+  v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
+  v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
+  return v;
+}
+
+__device__ __forceinline__ floatx4 mfma_fp8(const int32x8& a, const int32x8& b) {
+  const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  // cbsz = blgp = 0 selects OCP E4M3 for both operands; zero scale operands
+  // select the unscaled instruction.
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
+}
+
+// 32 e4m3 bytes -> 4 x 8 bf16, exactly (scale 1.0).  Element i of part j is
+// byte 8j + i, for both operands alike.
+__device__ __forceinline__ void widen_fp8(const int32x8& v, bf16x8 out[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[2 * j], 1.0f, false);
+    const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[2 * j], 1.0f, true);
+    const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[2 * j + 1], 1.0f, false);
+    const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[2 * j + 1], 1.0f, true);
+    out[j] = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+  }
+}
+
+// One K128 block on the exact path: four chained bf16 MFMAs.  The weight
+// fragment is passed through an empty asm so the widening cannot be hoisted
+// out of the route-tile loop (that would hold every K block in bf16 at once).
+__device__ __forceinline__ floatx4 mfma_block_bf16(int32x8 a, const bf16x8 b[4]) {
+  asm volatile("" : "+v"(a));
+  bf16x8 wide[4];
+  widen_fp8(a, wide);
+  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wide[j], b[j], acc, 0, 0, 0);
+  return acc;
+}
+
+// SwiGLU + e4m3 requantisation of one 128-column group held by 16 lanes
+// (8 gate and 8 up bf16 values per lane): a = (g * sigmoid(g)) * u in fp32,
+// scale = max(amax, 1e-10) / 448, codes of clamp(a / scale).  Shared by the
+// standalone kernel and the fused FC1 epilogue, so both give the same bytes.
+__device__ __forceinline__ float swiglu_quant_group(uint4 graw, uint4 uraw, uint2* codes) {
+  const uint32_t gw[4] = {graw.x, graw.y, graw.z, graw.w};
+  const uint32_t uw[4] = {uraw.x, uraw.y, uraw.z, uraw.w};
+  float v[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t gbits = (i & 1) ? (gw[i / 2] & 0xffff0000u) : (gw[i / 2] << 16);
+    const uint32_t ubits = (i & 1) ? (uw[i / 2] & 0xffff0000u) : (uw[i / 2] << 16);
+    const float g = __uint_as_float(gbits);
+    const float u = __uint_as_float(ubits);
+    const float sig = 1.0f / (1.0f + expf(-g));
+    v[i] = (g * sig) * u;
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  amax = segment_max<16>(amax);
+  const float scale = group_scale(amax);
+  uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo |= quantize_one(v[i], scale) << (8 * i);
+    hi |= quantize_one(v[i + 4], scale) << (8 * i);
+  }
+  *codes = make_uint2(lo, hi);
+  return scale;
+}
+
+__device__ __forceinline__ float route_weight(const void* weights, int weights_f32, size_t index) {
+  return weights_f32 ? static_cast<const float*>(weights)[index]
+                     : bf16_to_f32(static_cast<const uint16_t*>(weights)[index]);
+}
+
+// out[token, column .. column+3] = sum_r w[token, r] * down[token*top_k + r, ...]
+// with one fused multiply-add per rank in rank order (fp32), before rounding.
+// kCollect: `down` was published by other workgroups (coherent loads).
+template <bool kCollect = false>
+__device__ __forceinline__ float4 combine4(const float* down, const void* weights, int weights_f32,
+                                           int token, int top_k, int hidden, int column) {
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int r = 0; r < top_k; ++r) {
+    const float w = route_weight(weights, weights_f32, static_cast<size_t>(token) * top_k + r);
+    const float* src = down + (static_cast<size_t>(token) * top_k + r) * hidden + column;
+    float4 y;
+    if constexpr (kCollect) {
+      const uint64_t lo = collect_u64(src), hi = collect_u64(src + 2);
+      y = make_float4(__uint_as_float(static_cast<uint32_t>(lo)), __uint_as_float(static_cast<uint32_t>(lo >> 32)),
+                      __uint_as_float(static_cast<uint32_t>(hi)), __uint_as_float(static_cast<uint32_t>(hi >> 32)));
+    } else {
+      y = *reinterpret_cast<const float4*>(src);
+    }
+    acc.x = fmaf(w, y.x, acc.x);
+    acc.y = fmaf(w, y.y, acc.y);
+    acc.z = fmaf(w, y.z, acc.z);
+    acc.w = fmaf(w, y.w, acc.w);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ uint2 pack_bf16x4(float4 v) {
+  const uint32_t lo = f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
+  const uint32_t hi = f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+  return make_uint2(lo, hi);
+}
+
+}  // namespace d3

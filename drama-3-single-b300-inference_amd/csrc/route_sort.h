@@ -67,22 +67,29 @@ __device__ __forceinline__ int block_inclusive_scan(int value, int* wave_totals,
 }
 
 struct SortOutputs {
-  int32_t* counts;
-  int32_t* starts;
-  int32_t* total;
+  int32_t* counts;      // optional
+  int32_t* starts;      // optional
+  int32_t* total;       // optional
   int32_t* sorted_ids;
-  int32_t* expert_ids;
+  int32_t* expert_ids;  // optional
   int max_rows;
   int32_t* inverse;  // optional
   int4* items;       // optional
   int max_items;
   int32_t* num_items;  // optional
   int32_t* pairs_out;  // optional
+  // optional: per expert {count + 1, start} as one 64-bit word at the start
+  // of a 16-byte record, written last (see kPublishOut)
+  int4* expert_state;
 };
 
 // All THREADS threads of the workgroup must call this (it synchronises).
 // num_experts <= THREADS; `smem` holds sort_shared_ints(THREADS, E) ints.
-template <int THREADS, bool kI64, bool kCollect = false>
+// kPublishOut: the outputs are read by other workgroups of the same launch:
+// sorted ids go out with coherent stores, and each expert's state word is
+// published only after every sorted id is visible, so a reader that sees
+// count + 1 > 0 may read the expert's sorted ids.
+template <int THREADS, bool kI64, bool kCollect = false, bool kPublishOut = false>
 __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int num_experts,
                                   int tile, int item_rows, int* smem, const SortOutputs& out) {
   constexpr int kWaves = THREADS / kWave;
@@ -160,7 +167,10 @@ __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int n
     if (valid) {
       int position = starts[e] + running[e] + rank;
       for (int w = 0; w < wave; ++w) position += wave_counts[w * num_experts + e];
-      out.sorted_ids[position] = p;
+      if constexpr (kPublishOut)
+        publish_u32(out.sorted_ids + position, static_cast<uint32_t>(p));
+      else
+        out.sorted_ids[position] = p;
       if (out.inverse != nullptr) out.inverse[p] = position;
     } else if (p < pairs && out.inverse != nullptr) {
       out.inverse[p] = -1;
@@ -188,9 +198,10 @@ __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int n
     const int s = starts[e];
     const int pad = (c + tile - 1) / tile * tile;
     for (int i = c; i < pad; ++i) out.sorted_ids[s + i] = pairs;
-    for (int b = 0; b < pad / tile; ++b) out.expert_ids[s / tile + b] = e;
-    out.counts[e] = c;
-    out.starts[e] = s;
+    if (out.expert_ids != nullptr)
+      for (int b = 0; b < pad / tile; ++b) out.expert_ids[s / tile + b] = e;
+    if (out.counts != nullptr) out.counts[e] = c;
+    if (out.starts != nullptr) out.starts[e] = s;
     if (out.items != nullptr) {
       const int n = (c + item_rows - 1) / item_rows;
       for (int j = 0; j < n; ++j) {
@@ -200,14 +211,24 @@ __device__ void sort_routes_block(const void* __restrict__ ids, int pairs, int n
     }
   }
   for (int i = total + tid; i < out.max_rows; i += THREADS) out.sorted_ids[i] = pairs;
-  for (int i = total / tile + tid; i < out.max_rows / tile; i += THREADS) out.expert_ids[i] = -1;
+  if (out.expert_ids != nullptr)
+    for (int i = total / tile + tid; i < out.max_rows / tile; i += THREADS) out.expert_ids[i] = -1;
   if (out.items != nullptr)
     for (int i = total_items + tid; i < out.max_items; i += THREADS)
       out.items[i] = make_int4(-1, 0, 0, 0);
   if (tid == 0) {
-    *out.total = total;
+    if (out.total != nullptr) *out.total = total;
     if (out.num_items != nullptr) *out.num_items = total_items;
     if (out.pairs_out != nullptr) *out.pairs_out = pairs;
+  }
+  if (out.expert_state != nullptr) {
+    if constexpr (kPublishOut) {
+      wait_stores();  // every sorted id of this thread is visible device-wide
+      __syncthreads();
+    }
+    for (int e = tid; e < num_experts; e += THREADS)
+      publish_u64(&out.expert_state[e], (static_cast<uint64_t>(static_cast<uint32_t>(starts[e])) << 32) |
+                                            static_cast<uint32_t>(counts[e] + 1));
   }
 }
 

@@ -63,6 +63,10 @@ SIGNATURES = {
                _p, _p]),
     "d3_expert_fc2_swiglu": (
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p]),
+    "d3_moe_step_sync_ints": (_i32, [_i32, _i32, _i32, _i32]),
+    "d3_moe_decode_step": (
+        _i32, [_p, _i32, _p, _p, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32,
+               _p, _p, _i32, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p]),
     "d3_silu_mul_quant": (_i32, [_p, _i32, _i32, _p, _p, _p, _i32, _p, _p, _p]),
     "d3_weighted_combine": (_i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
     "d3_combine_experts": (_i32, [_p, _p, _p, _i64, _i32, _i32, _p, _p]),

@@ -28,7 +28,7 @@ import torch
 
 from . import _lib
 from ._lib import DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64, call, ptr
-from .expert_weights import fc1_operands, fc2_operands
+from .expert_weights import LAYOUT_FRAGMENT, fc1_operands, fc2_operands
 
 SORT_TILE = 16  # MFMA route tile; also the padding granularity of the sorted layout
 # Work items with at most this many routes take the exact (bf16-MFMA) path of
@@ -336,20 +336,62 @@ class DecodeStep:
     driven by the device count (graph-capturable, no host sync).
 
     Output row r belongs to slot ``active[r]`` for r < ``count``.
+
+    ``fused=True`` runs the whole step as one launch (``d3_moe_decode_step``)
+    on fragment-major weights (``prepare_experts``) and bf16 logits, with the
+    same buffers and results as the multi-kernel chain; other calls (and the
+    default) use the chain, which is currently the faster of the two.
     """
 
     def __init__(self, slots: int, num_experts: int, hidden: int, intermediate: int,
-                 top_k: int = 8, device="cuda", item_rows: int | None = None):
+                 top_k: int = 8, device="cuda", item_rows: int | None = None,
+                 fused: bool | None = None):
         dev = torch.device(device)
         self.slots = slots
         self.active = torch.empty(slots, dtype=torch.int32, device=dev)
         self.count = torch.empty(1, dtype=torch.int32, device=dev)
         self.workspace = MoEWorkspace(Shape(slots, num_experts, hidden, intermediate, top_k), dev,
                                       item_rows=item_rows)
+        lib = _lib.load()
+        sync_ints = lib.d3_moe_step_sync_ints(slots, num_experts, hidden, intermediate)
+        supported = sync_ints > 0 and slots <= 256 and num_experts <= 256
+        if fused and not supported:
+            raise ValueError(f"the one-launch step does not cover slots={slots}, "
+                             f"E={num_experts}, H={hidden}, I={intermediate}")
+        self.fused = bool(fused)
+        # Hand-off counters of the one-launch step: zero between launches.
+        self.sync = torch.zeros(max(sync_ints, 4), dtype=torch.int32, device=dev)
+
+    def uses_fused(self, logits_slots, experts) -> bool:
+        return (self.fused and logits_slots.dtype == torch.bfloat16
+                and fc1_operands(experts)[2] == LAYOUT_FRAGMENT
+                and fc2_operands(experts)[2] == LAYOUT_FRAGMENT)
 
     def __call__(self, occupancy, x_slots, logits_slots, experts, stream=None) -> torch.Tensor:
         stream = _lib.stream(x_slots.device) if stream is None else stream
         ws = self.workspace
+        if self.uses_fused(logits_slots, experts):
+            return self._fused(occupancy, x_slots, logits_slots, experts, stream)
         ws.front(x_slots, logits_slots, occupancy=occupancy, active=self.active,
                  count=self.count, stream=stream)
         return ws.experts(experts, self.count, stream=stream)
+
+    def _fused(self, occupancy, x_slots, logits_slots, experts, stream) -> torch.Tensor:
+        ws, s = self.workspace, self.workspace.shape
+        require_cuda(occupancy, x_slots, logits_slots)
+        if occupancy.numel() != self.slots or x_slots.shape[0] < self.slots:
+            raise ValueError("occupancy / x_slots must cover every slot")
+        w13, s13, _ = fc1_operands(experts)
+        w2, s2, _ = fc2_operands(experts)
+        call("d3_moe_decode_step", ptr(occupancy), self.slots, ptr(self.active), ptr(self.count),
+             ptr(x_slots), x_slots.stride(0), ptr(logits_slots), logits_slots.stride(0), s.hidden,
+             s.num_experts, s.intermediate, s.top_k, ptr(w13), ptr(s13), ptr(w2), ptr(s2),
+             ws.exact_routes, ptr(ws.ids), ptr(ws.weights), dtype_code(ws.weights.dtype),
+             ptr(ws.q), ptr(ws.x_scales), ptr(ws.sorted_ids), ws.max_rows, ptr(ws.gate_up),
+             ptr(ws.act), ptr(ws.act_scales), ptr(ws.down), ptr(ws.out), ptr(self.sync), stream)
+        return ws.out
+
+    def wait_failed(self) -> bool:
+        """True if a wait inside a one-launch step gave up (output invalid);
+        synchronises with the device."""
+        return int(self.sync[0].item()) != 0

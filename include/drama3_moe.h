@@ -259,6 +259,49 @@ int d3_expert_fc2_swiglu(const uint8_t *w2, const float *s2, int32_t weight_layo
                          int32_t exact_routes, float *down, void *stream);
 
 /*
+ * A1-A12  The whole decode MoE step in one launch.
+ * Replaces DramaModel.routed_moe's decode path (src/drama3/model.py:520-583:
+ * slot filter engine.py:637-647, route kernels.py:360-383, quantise
+ * moe_input.py:24-27, small_batch_moe kernels.py:325-357 with the route sort
+ * kernels.py:658-731, FC1 / silu_mul_quant / FC2 / combine kernels.py:290-322,
+ * 344).  Same results as d3_moe_front + d3_expert_gemm (FC1) +
+ * d3_silu_mul_quant + d3_expert_gemm (FC2) + d3_weighted_combine on the same
+ * buffers (bit for bit, every intermediate included), in one kernel whose
+ * expert-GEMM workgroups start streaming their weights before routing is
+ * known; the route sort, the SwiGLU requant of an expert and the combine of
+ * a token are done by the workgroup that completes their inputs.
+ *   occupancy u8 [num_slots] -> active_slots int32 [num_slots] (ascending,
+ *   -1 padded), *count = live rows; output row r (r < *count) of out
+ *   bf16 [num_slots, hidden] belongs to slot active_slots[r].
+ *   x bf16 [num_slots rows, x_row_stride], logits bf16 [num_slots rows,
+ *   logits_row_stride] (slot-indexed); w13 / w2 in the fragment-major layout
+ *   (d3_pack_expert_weights) with their block scales s13 / s2.
+ *   ids, weights (route weights, bf16 or f32), q, x_scales, sorted_ids
+ *   (max_rows >= d3_max_sorted_rows(num_slots * top_k, num_experts, 16)),
+ *   gate_up, act, act_scales, down: the same buffers as the multi-kernel
+ *   step, written with the same contents.
+ *   sync: int32 [d3_moe_step_sync_ints(...)], 16-byte aligned, all zero
+ *   before the first launch; every launch leaves it zero except sync[0],
+ *   which becomes nonzero if a wait inside the kernel gave up (a launch that
+ *   was not given the GPU to itself for ~1 s); the output is then invalid.
+ * Launches on one sync buffer must not overlap.  Items of at most
+ * exact_routes routes use the exact bf16-MFMA path (as d3_expert_gemm).
+ * Supported: (hidden, intermediate) in {(1024, 256), (1024, 512),
+ * (2048, 512), (2048, 768)}, num_experts <= 256, num_slots <= 256, bf16 logits.
+ */
+int32_t d3_moe_step_sync_ints(int32_t num_slots, int32_t num_experts, int32_t hidden,
+                              int32_t intermediate);
+int d3_moe_decode_step(const uint8_t *occupancy, int32_t num_slots, int32_t *active_slots,
+                       int32_t *count, const uint16_t *x, int64_t x_row_stride,
+                       const uint16_t *logits, int64_t logits_row_stride, int32_t hidden,
+                       int32_t num_experts, int32_t intermediate, int32_t top_k,
+                       const uint8_t *w13, const float *s13, const uint8_t *w2, const float *s2,
+                       int32_t exact_routes, int32_t *ids, void *weights, int32_t weights_dtype,
+                       uint8_t *q, float *x_scales, int32_t *sorted_ids, int32_t max_rows,
+                       uint16_t *gate_up, uint8_t *act, float *act_scales, float *down,
+                       uint16_t *out, int32_t *sync, void *stream);
+
+/*
  * A10  SwiGLU + per-128 FP8 requantisation of FC1 rows.
  * Replaces Fish quantize_groups(silu_mul_quant_kernel, gate_up, I)
  * (src/drama3/kernels.py:344,748).  gate_up bf16 [rows, 2I] ([gate | up]) ->
