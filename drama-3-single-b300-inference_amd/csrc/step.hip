@@ -246,8 +246,8 @@ __device__ void act_finish(const StepArgs& a, int4* state, int routes, int first
 // (FC2) or between the halves of (FC1) the weight loads, so the staging
 // latency hides under the weight stream as in the multi-kernel GEMM.
 // ---------------------------------------------------------------------------
-template <int KB, int RT, bool kFC1, int KB2>
-__device__ void expert_task(const StepArgs& a, int expert, int tile, uint8_t* smem, int* bcast) {
+template <int KB, int RT, bool kFC1, int KB2, int TILES>
+__device__ void expert_task(const StepArgs& a, int expert, int tile_group, uint8_t* smem, int* bcast) {
   constexpr int K = KB * kGroup;
   constexpr int kRowsPerWave = RT * 16;
   constexpr int kRowsPerGroup = kGemmWaves * kRowsPerWave;
@@ -257,19 +257,24 @@ __device__ void expert_task(const StepArgs& a, int expert, int tile, uint8_t* sm
   uint8_t* b_tile = smem;
   float* b_scales = reinterpret_cast<float*>(smem + 16 * kStride);
   int* b_target = reinterpret_cast<int*>(b_scales + 16 * KB);
-  int* finish = b_target + 16;
+  int* finish = b_target + 16;  // [16 * TILES]
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int row16 = lane & 15;
   const int group = lane >> 4;
   const int n_rows = kFC1 ? 2 * a.intermediate : a.hidden;
-  const int n0 = tile * kRowsPerGroup + wave * kRowsPerWave;
+  const int first_tile = tile_group * TILES;
   int4* state = a.expert_state + expert;
 
+  // Weight tiles of this workgroup: TILES consecutive row tiles of the
+  // expert, each held in registers in turn.
   const uint8_t* wexp = (kFC1 ? a.w13 : a.w2) + static_cast<size_t>(expert) * n_rows * K;
+  const float* wsexp = (kFC1 ? a.s13 : a.s2) + static_cast<size_t>(expert) * (n_rows / kGroup) * KB;
   int32x8 a_frag[RT][KB];
-  auto load_weights = [&](int kb0, int kb1) {
+  float w_scale[RT][KB];
+  auto load_weights = [&](int tile, int kb0, int kb1) {
+    const int n0 = tile * kRowsPerGroup + wave * kRowsPerWave;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -277,19 +282,19 @@ __device__ void expert_task(const StepArgs& a, int expert, int tile, uint8_t* sm
         if (kb >= kb0 && kb < kb1)
           a_frag[rt][kb] = load_packed_fragment(wexp + static_cast<size_t>(n0 + rt * 16) * K, kb, lane);
   };
-  float w_scale[RT][KB];
-  const float* wsexp = (kFC1 ? a.s13 : a.s2) + static_cast<size_t>(expert) * (n_rows / kGroup) * KB;
+  auto load_scales = [&](int tile) {
+    const int n0 = tile * kRowsPerGroup + wave * kRowsPerWave;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) w_scale[rt][kb] = wsexp[((n0 + rt * 16) / kGroup) * KB + kb];
+      for (int kb = 0; kb < KB; ++kb) w_scale[rt][kb] = wsexp[((n0 + rt * 16) / kGroup) * KB + kb];
+  };
 
-  // Staging of one route tile: 16 threads per route column.
+  // Staging of one route tile: 16 threads per route column.  The loads are
+  // unconditional (dead columns read past the buffer and get zeros): no
+  // branch, so no register copy of a loaded value forces an early wait.
   const int stage_col = threadIdx.x >> 4;
   const int stage_part = threadIdx.x & 15;
-  // Staging loads are unconditional (dead columns read past the buffer and
-  // get zeros): no branch, so no register copy of a loaded value forces an
-  // early wait.
   const uint32_t a_rows = static_cast<uint32_t>(kFC1 ? a.num_slots : a.max_rows);
   const CoherentBuffer act_rows(kFC1 ? static_cast<const void*>(a.q) : a.act, a_rows * K);
   const CoherentBuffer act_scales(kFC1 ? static_cast<const void*>(a.x_scales) : a.act_scales,
@@ -299,7 +304,6 @@ __device__ void expert_task(const StepArgs& a, int expert, int tile, uint8_t* sm
   int first = 0;
   int4 b_stage[kChunks];
   float b_stage_scale = 0.0f;
-  int b_stage_target = -1;
   int stage_pair = 0;
   auto fetch_ids = [&](int m0) {  // pair of this thread's route column
     const int r = m0 + stage_col;
@@ -317,12 +321,11 @@ __device__ void expert_task(const StepArgs& a, int expert, int tile, uint8_t* sm
   };
   auto store_tile = [&](int m0) {
     const bool live = m0 + stage_col < routes;
-    b_stage_target = live ? (kFC1 ? first + m0 + stage_col : stage_pair) : -1;
 #pragma unroll
     for (int j = 0; j < kChunks; ++j)
       *reinterpret_cast<int4*>(b_tile + stage_col * kStride + j * 256 + stage_part * 16) = b_stage[j];
     if (stage_part < KB) b_scales[stage_col * KB + stage_part] = b_stage_scale;
-    if (stage_part == 0) b_target[stage_col] = b_stage_target;
+    if (stage_part == 0) b_target[stage_col] = live ? (kFC1 ? first + m0 + stage_col : stage_pair) : -1;
   };
 
   // Expert state: {count + 1, start} (0 = routing not done), act_done.
@@ -350,22 +353,24 @@ __device__ void expert_task(const StepArgs& a, int expert, int tile, uint8_t* sm
   }
   if (fast) {
     if (routes == 0) return;
+    load_scales(first_tile);
     if constexpr (kFC1) {
       fetch_ids(0);  // before any weight: its wait does not include them
-      load_weights(0, kFirstHalf);
+      load_weights(first_tile, 0, kFirstHalf);
       __builtin_amdgcn_sched_barrier(0);
       fetch_rows(0);
       __builtin_amdgcn_sched_barrier(0);
-      load_weights(kFirstHalf, KB);
+      load_weights(first_tile, kFirstHalf, KB);
     } else {
       fetch_ids(0);
       fetch_rows(0);
       __builtin_amdgcn_sched_barrier(0);
-      load_weights(0, KB);
+      load_weights(first_tile, 0, KB);
     }
     store_tile(0);
   } else {
-    load_weights(0, KB);
+    load_weights(first_tile, 0, KB);
+    load_scales(first_tile);
     if (threadIdx.x == 0) {
       int count = 0, start = 0;
       for (int spins = 0;; ++spins) {
@@ -394,11 +399,8 @@ __device__ void expert_task(const StepArgs& a, int expert, int tile, uint8_t* sm
   }
   const bool exact = routes <= a.exact_routes;
 
-  // Route tiles of 16 against the register-resident weights; tile m0's
-  // activations are in LDS when compute_tile runs.
-  auto compute_tile = [&]() {
-    __syncthreads();
-    floatx4 acc[RT];
+  // One weight tile against the route tile in LDS.
+  auto mma = [&](floatx4 (&acc)[RT]) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint8_t* brow = b_tile + row16 * kStride;
@@ -427,74 +429,111 @@ __device__ void expert_task(const StepArgs& a, int expert, int tile, uint8_t* sm
         }
       }
     }
+  };
+  auto epilogue = [&](const floatx4 (&acc)[RT], int tile) {
     const int target = b_target[row16];
-    if (target >= 0) {
+    if (target < 0) return;
+    const int n0 = tile * kRowsPerGroup + wave * kRowsPerWave;
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int n = n0 + rt * 16 + group * 4;  // rows n..n+3 of this column
-        if constexpr (kFC1) {
-          const uint32_t lo = f32_to_bf16(acc[rt][0]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][1])) << 16);
-          const uint32_t hi = f32_to_bf16(acc[rt][2]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][3])) << 16);
-          publish_u64(a.gate_up + static_cast<size_t>(target) * n_rows + n, (static_cast<uint64_t>(hi) << 32) | lo);
-        } else {
-          float* dst = a.down + static_cast<size_t>(target) * n_rows + n;
-          publish_u64(dst, (static_cast<uint64_t>(__float_as_uint(acc[rt][1])) << 32) | __float_as_uint(acc[rt][0]));
-          publish_u64(dst + 2, (static_cast<uint64_t>(__float_as_uint(acc[rt][3])) << 32) | __float_as_uint(acc[rt][2]));
-        }
-      }
-    }
-    if constexpr (!kFC1) {
-      // Weighted combine of each token whose last contribution to this
-      // column tile this was (rank order, one rounding to bf16).
-      wait_stores();
-      __syncthreads();
-      if (threadIdx.x < 16) {
-        const int t = b_target[threadIdx.x];
-        int done = -1;
-        if (t >= 0) {
-          const int token = t / a.top_k;
-          if (take_ticket(&a.combine_tickets[token * a.fc2_tiles + tile]) == a.top_k - 1) done = token;
-        }
-        finish[threadIdx.x] = done;
-      }
-      __syncthreads();
-      const int seg = threadIdx.x >> 4;
-      const int part = threadIdx.x & 15;
-      const int token = finish[seg];
-      if (token >= 0) {
-        const int tile_n0 = tile * kRowsPerGroup;
-        for (int column = tile_n0 + part * 4; column < tile_n0 + kRowsPerGroup; column += 64) {
-          float4 acc4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          for (int r = 0; r < a.top_k; ++r) {
-            const int index = token * a.top_k + r;
-            const float w = collect_route_weight(a.weights, a.weights_f32, index);
-            const float* src = a.down + static_cast<size_t>(index) * n_rows + column;
-            const uint64_t lo = collect_u64(src), hi = collect_u64(src + 2);
-            acc4.x = fmaf(w, __uint_as_float(static_cast<uint32_t>(lo)), acc4.x);
-            acc4.y = fmaf(w, __uint_as_float(static_cast<uint32_t>(lo >> 32)), acc4.y);
-            acc4.z = fmaf(w, __uint_as_float(static_cast<uint32_t>(hi)), acc4.z);
-            acc4.w = fmaf(w, __uint_as_float(static_cast<uint32_t>(hi >> 32)), acc4.w);
-          }
-          *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(token) * n_rows + column) = pack_bf16x4(acc4);
-        }
-        if (part == 0) reset_ticket(&a.combine_tickets[token * a.fc2_tiles + tile]);
+    for (int rt = 0; rt < RT; ++rt) {
+      const int n = n0 + rt * 16 + group * 4;  // rows n..n+3 of this column
+      if constexpr (kFC1) {
+        const uint32_t lo = f32_to_bf16(acc[rt][0]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][1])) << 16);
+        const uint32_t hi = f32_to_bf16(acc[rt][2]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][3])) << 16);
+        publish_u64(a.gate_up + static_cast<size_t>(target) * n_rows + n, (static_cast<uint64_t>(hi) << 32) | lo);
+      } else {
+        float* dst = a.down + static_cast<size_t>(target) * n_rows + n;
+        publish_u64(dst, (static_cast<uint64_t>(__float_as_uint(acc[rt][1])) << 32) | __float_as_uint(acc[rt][0]));
+        publish_u64(dst + 2, (static_cast<uint64_t>(__float_as_uint(acc[rt][3])) << 32) | __float_as_uint(acc[rt][2]));
       }
     }
   };
-  compute_tile();
-  for (int m0 = 16; m0 < routes; m0 += 16) {
-    __syncthreads();  // previous tile fully consumed
-    fetch_ids(m0);
-    fetch_rows(m0);
-    store_tile(m0);
-    compute_tile();
+  // FC2: for the route tile in LDS and column tiles [tile0, tile0 + count),
+  // the weighted combine of each token whose last contribution this was
+  // (rank order, one rounding to bf16).
+  auto combine_handoff = [&](int tile0, int count) {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x < 16 * count) {
+      const int t = b_target[threadIdx.x & 15];
+      int done = -1;
+      if (t >= 0) {
+        const int token = t / a.top_k;
+        const int index = token * a.fc2_tiles + tile0 + (threadIdx.x >> 4);
+        if (take_ticket(&a.combine_tickets[index]) == a.top_k - 1) done = token;
+      }
+      finish[threadIdx.x] = done;
+    }
+    __syncthreads();
+    const int seg = threadIdx.x >> 4;
+    const int part = threadIdx.x & 15;
+    for (int f = seg; f < 16 * count; f += 16) {
+      const int token = finish[f];
+      if (token < 0) continue;  // whole 16-thread segment
+      const int tile = tile0 + (f >> 4);
+      const int tile_n0 = tile * kRowsPerGroup;
+      for (int column = tile_n0 + part * 4; column < tile_n0 + kRowsPerGroup; column += 64) {
+        float4 acc4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int r = 0; r < a.top_k; ++r) {
+          const int index = token * a.top_k + r;
+          const float w = collect_route_weight(a.weights, a.weights_f32, index);
+          const float* src = a.down + static_cast<size_t>(index) * n_rows + column;
+          const uint64_t lo = collect_u64(src), hi = collect_u64(src + 2);
+          acc4.x = fmaf(w, __uint_as_float(static_cast<uint32_t>(lo)), acc4.x);
+          acc4.y = fmaf(w, __uint_as_float(static_cast<uint32_t>(lo >> 32)), acc4.y);
+          acc4.z = fmaf(w, __uint_as_float(static_cast<uint32_t>(hi)), acc4.z);
+          acc4.w = fmaf(w, __uint_as_float(static_cast<uint32_t>(hi >> 32)), acc4.w);
+        }
+        *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(token) * n_rows + column) = pack_bf16x4(acc4);
+      }
+      if (part == 0) reset_ticket(&a.combine_tickets[token * a.fc2_tiles + tile]);
+    }
+  };
+
+  if (routes <= 16) {
+    // One route tile: the weight tiles follow each other through the same
+    // registers; tile tt + 1 streams in while tile tt's outputs are stored.
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < TILES; ++tt) {
+      floatx4 acc[RT];
+      mma(acc);
+      if (tt + 1 < TILES) {
+        load_weights(first_tile + tt + 1, 0, KB);
+        load_scales(first_tile + tt + 1);
+      }
+      epilogue(acc, first_tile + tt);
+    }
+    if constexpr (!kFC1) combine_handoff(first_tile, TILES);
+  } else {
+    // Several route tiles: each weight tile walks them, restaging each.
+#pragma unroll
+    for (int tt = 0; tt < TILES; ++tt) {
+      if (tt > 0) {
+        load_weights(first_tile + tt, 0, KB);
+        load_scales(first_tile + tt);
+      }
+      for (int m0 = 0; m0 < routes; m0 += 16) {
+        if (tt > 0 || m0 > 0) {
+          __syncthreads();  // previous route tile fully consumed
+          fetch_ids(m0);
+          fetch_rows(m0);
+          store_tile(m0);
+        }
+        __syncthreads();
+        floatx4 acc[RT];
+        mma(acc);
+        epilogue(acc, first_tile + tt);
+        if constexpr (!kFC1) combine_handoff(first_tile + tt, 1);
+      }
+    }
   }
 
   if constexpr (kFC1) {
-    // The expert's last FC1 tile computes its SwiGLU requant.
+    // The expert's last FC1 workgroup computes its SwiGLU requant.
     wait_stores();
     __syncthreads();
-    if (threadIdx.x == 0) bcast[2] = take_ticket(&state->w) == a.fc1_tiles - 1 ? 1 : 0;
+    if (threadIdx.x == 0) bcast[2] = take_ticket(&state->w) == a.fc1_tiles / TILES - 1 ? 1 : 0;
     __syncthreads();
     if (bcast[2]) act_finish<KB2>(a, state, routes, first);
   }
@@ -521,10 +560,11 @@ __device__ void janitor(const StepArgs& a) {
   if (threadIdx.x == 0) reset_ticket(a.exit_count);
 }
 
-constexpr int gemm_smem_bytes(int kb) { return 16 * (kb * kGroup + 16) + 16 * kb * 4 + 2 * 16 * 4; }
+constexpr int kMaxTiles = 4;  // weight tiles per expert workgroup
+constexpr int gemm_smem_bytes(int kb) { return 16 * (kb * kGroup + 16) + 16 * kb * 4 + 16 * 4 + 16 * kMaxTiles * 4; }
 constexpr int max3(int x, int y, int z) { return x > y ? (x > z ? x : z) : (y > z ? y : z); }
 
-template <int NPL, int KB1, int KB2>
+template <int NPL, int KB1, int KB2, int TILES1, int TILES2>
 __global__ __launch_bounds__(kStepThreads) __attribute__((amdgpu_waves_per_eu(2))) void moe_step_kernel(
     StepArgs a) {
   constexpr int kSmem = max3(gemm_smem_bytes(KB1), gemm_smem_bytes(KB2),
@@ -536,15 +576,17 @@ __global__ __launch_bounds__(kStepThreads) __attribute__((amdgpu_waves_per_eu(2)
     janitor(a);
     return;
   }
-  const int fc1_end = a.num_slots + a.num_experts * a.fc1_tiles;
+  const int fc1_groups = a.fc1_tiles / TILES1;
+  const int fc2_groups = a.fc2_tiles / TILES2;
+  const int fc1_end = a.num_slots + a.num_experts * fc1_groups;
   if (b < a.num_slots) {
     front_task<NPL>(a, b, reinterpret_cast<int*>(smem), bcast);
   } else if (b < fc1_end) {
     const int t = b - a.num_slots;
-    expert_task<KB1, rt_for(KB1), true, KB2>(a, t / a.fc1_tiles, t % a.fc1_tiles, smem, bcast);
+    expert_task<KB1, rt_for(KB1), true, KB2, TILES1>(a, t / fc1_groups, t % fc1_groups, smem, bcast);
   } else {
     const int t = b - fc1_end;
-    expert_task<KB2, rt_for(KB2), false, KB2>(a, t / a.fc2_tiles, t % a.fc2_tiles, smem, bcast);
+    expert_task<KB2, rt_for(KB2), false, KB2, TILES2>(a, t / fc2_groups, t % fc2_groups, smem, bcast);
   }
   // Leave: every access of this workgroup to the expert state has completed
   // (loads consumed, tickets returned, act_done stores waited for), so a
@@ -647,19 +689,21 @@ extern "C" int d3_moe_decode_step(const uint8_t* occupancy, int32_t num_slots,
   args.combine_tickets = sync + kSyncHeader + 4 * num_experts;
   args.fc1_tiles = 2 * intermediate / tile_rows_for(hidden / kGroup);
   args.fc2_tiles = fc2_tiles_of(hidden, intermediate);
-  const dim3 grid(num_slots + num_experts * (args.fc1_tiles + args.fc2_tiles) + 1);  // + janitor
+  // Weight tiles per expert workgroup (each divides the expert's tile count).
+  constexpr int kTiles1 = 2, kTiles2 = 2;
+  const dim3 grid(num_slots + num_experts * (args.fc1_tiles / kTiles1 + args.fc2_tiles / kTiles2) + 1);  // + janitor
   const dim3 block(kStepThreads);
   hipStream_t s = as_stream(stream);
   const int kb1 = hidden / kGroup, kb2 = intermediate / kGroup;
 #define D3_STEP_LAUNCH(NPL)                                                                     \
   if (kb1 == 8 && kb2 == 2)                                                                     \
-    hipLaunchKernelGGL((moe_step_kernel<NPL, 8, 2>), grid, block, 0, s, args);                  \
+    hipLaunchKernelGGL((moe_step_kernel<NPL, 8, 2, kTiles1, kTiles2>), grid, block, 0, s, args);                  \
   else if (kb1 == 8 && kb2 == 4)                                                                \
-    hipLaunchKernelGGL((moe_step_kernel<NPL, 8, 4>), grid, block, 0, s, args);                  \
+    hipLaunchKernelGGL((moe_step_kernel<NPL, 8, 4, kTiles1, kTiles2>), grid, block, 0, s, args);                  \
   else if (kb1 == 16 && kb2 == 4)                                                               \
-    hipLaunchKernelGGL((moe_step_kernel<NPL, 16, 4>), grid, block, 0, s, args);                 \
+    hipLaunchKernelGGL((moe_step_kernel<NPL, 16, 4, kTiles1, kTiles2>), grid, block, 0, s, args);                 \
   else                                                                                          \
-    hipLaunchKernelGGL((moe_step_kernel<NPL, 16, 6>), grid, block, 0, s, args);
+    hipLaunchKernelGGL((moe_step_kernel<NPL, 16, 6, kTiles1, kTiles2>), grid, block, 0, s, args);
   if (num_experts <= 64) {
     D3_STEP_LAUNCH(1)
   } else if (num_experts <= 128) {
