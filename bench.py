@@ -1,10 +1,11 @@
 """Benchmark of the 64-slot FP8 top-8 MoE decode step on
 one MI355X.
 
-One step = device-side slot compaction + routing + FP8 quantisation + route
-sort + FC1 + FC2 (SwiGLU requant in its prologue) + weighted combine over the
-live rows of 64 persistent slots (H=2048, 128 experts, I=768, top-8), captured
-in a HIP graph.
+One step = device-side slot compaction + routing + FP8 quantisation (one
+launch), FC1 and FC2 (SwiGLU requant in FC2's prologue) as expert GEMMs that
+find their own routes (no route sort), and the weighted combine, over the
+live rows of 64 persistent slots (H=2048, 128 experts, I=768, top-8),
+captured in a HIP graph.
 Inputs are resident in HBM before timing.  ``value`` is the cold-cache rate:
 the timed replays rotate over several copies of the expert weights whose
 total far exceeds the 256 MB MALL, so every step streams its weights from HBM.
@@ -32,7 +33,7 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 # this script (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors read off
 # the 1 GiB device copy in the same runs); profiles/expert_gemm_c2_hbm_traffic.md.
 # Re-measure whenever the FC1 kernel or its tiling changes.
-FC1_TRAFFIC_BYTES = {"kernel": "expert_gemm_kernel<16,1,0,0,true>", "bytes": 399241830}
+FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,0,1>", "bytes": 402288538}
 
 
 def parse():
@@ -175,8 +176,12 @@ def main():
                     fn(c)
         return g
 
-    fc1_graph = kernel_graph(ws.fc1)
-    fc2_graph = kernel_graph(ws.fc2_swiglu if ws.swiglu_in_fc2 else ws.fc2)
+    if ws.sortless:  # the step's own expert kernels: sortless decode GEMMs
+        fc1_graph = kernel_graph(lambda c: ws.decode_fc1(c, ds.count))
+        fc2_graph = kernel_graph(lambda c: ws.decode_fc2(c, ds.count))
+    else:
+        fc1_graph = kernel_graph(ws.fc1)
+        fc2_graph = kernel_graph(ws.fc2_swiglu if ws.swiglu_in_fc2 else ws.fc2)
     launches = args.kernel_reps * len(copies)
     time_graphs(torch, [fc1_graph, fc2_graph], 2)  # warm-up
     fc1_us = time_graphs(torch, [fc1_graph], 5) / launches
@@ -187,7 +192,8 @@ def main():
         + routes * 2 * i * 2
     # FC2 reads its activations as fp8 codes + scales, or (SwiGLU in its
     # prologue) as FC1's bf16 gate|up rows.
-    act_bytes = routes * 2 * i * 2 if ws.swiglu_in_fc2 else routes * i + routes * (i // 128) * 4
+    prologue = ws.sortless or ws.swiglu_in_fc2
+    act_bytes = routes * 2 * i * 2 if prologue else routes * i + routes * (i // 128) * 4
     fc2_bytes = used * (h * i + 4 * (h // 128) * (i // 128)) + act_bytes + routes * h * 4
     # Practical streaming rate of this GPU for context: a large device copy
     # (torch), counting bytes read plus bytes written.
@@ -242,17 +248,22 @@ def main():
                    "experts": e, "hidden": h, "intermediate": i, "top_k": workloads.TOP_K,
                    "used_experts": used, "algorithmic_bytes_per_step": step_bytes,
                    "weight_copies": len(copies),
-                   "step": "one launch (d3_moe_decode_step)" if args.fused else "kernel chain",
+                   "step": ("one launch (d3_moe_decode_step)" if args.fused else
+                            "front + sortless decode GEMMs + combine" if ws.sortless else
+                            "front + sorted expert GEMMs + combine"),
                    "timing": "hipGraph of one step per weight copy (the copies act as consecutive "
                              "layers), replayed; cold: every step streams its copy from HBM"},
         "hot": {"us_per_step": round(hot_us, 2),
                 "GB_s": round(step_bytes / hot_us / 1e3, 1)},
-        "roofline": {"bound": "hbm", "kernel": "expert_gemm FC1", "achieved": round(fc1_gbs, 1),
+        "roofline": {"bound": "hbm",
+                     "kernel": "decode_expert_gemm FC1" if ws.sortless else "expert_gemm FC1",
+                     "achieved": round(fc1_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(fc1_gbs / HBM_PEAK_GBS, 4),
                      "traffic": FC1_TRAFFIC_BYTES["bytes"],
                      "traffic_kernel": FC1_TRAFFIC_BYTES["kernel"], "us_per_launch": round(fc1_us, 2),
                      "algorithmic_bytes_per_launch": fc1_bytes},
-        "fc2": {"kernel": "expert_fc2_swiglu" if ws.swiglu_in_fc2 else "expert_gemm FC2",
+        "fc2": {"kernel": ("decode_expert_gemm FC2 (SwiGLU prologue)" if ws.sortless else
+                           "expert_fc2_swiglu" if ws.swiglu_in_fc2 else "expert_gemm FC2"),
                 "us_per_launch": round(fc2_us, 2), "GB_s": round(fc2_gbs, 1),
                 "algorithmic_bytes_per_launch": fc2_bytes},
         "device_copy_GB_s": round(copy_gbs, 1),

@@ -71,7 +71,7 @@ struct EpilogueArgs {
   uint16_t* combined;
 };
 
-template <int KB, int RT, int MODE, int FUSE, bool kPacked>
+template <int KB, int RT, int MODE, int FUSE, bool kPacked, int TILES>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void expert_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows,
     const uint8_t* __restrict__ act, const float* __restrict__ act_scales,
@@ -89,8 +89,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   __shared__ int b_target[16];  // FC1: sorted position, FC2: pair id; -1 = no route
   __shared__ int finish[16];    // fused epilogue: group this workgroup finishes, or -1
 
+  static_assert(TILES == 1 || FUSE == kFuseNone, "fused epilogues take one weight tile per workgroup");
   const int tiles = n_rows / kRowsPerGroup;
-  const int item_index = blockIdx.x / tiles;
+  const int groups = tiles / TILES;  // workgroups per item
+  const int item_index = blockIdx.x / groups;
+  const int first_tile = (blockIdx.x % groups) * TILES;
   if (item_index >= *num_items) return;
   const int4 item = items[item_index];
   const int expert = item.x;
@@ -102,7 +105,8 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int row16 = lane & 15;
   const int group = lane >> 4;
-  const int n0 = (blockIdx.x % tiles) * kRowsPerGroup + wave * kRowsPerWave;
+  // Rows of weight tile `tile` held by this wave: n0_of(tile) + [0, RT * 16).
+  auto n0_of = [&](int tile) { return tile * kRowsPerGroup + wave * kRowsPerWave; };
 
   // Issue order of the first tile (memory returns are counted in issue
   // order): the first half of the weights, then the route ids (scalar loads,
@@ -186,43 +190,41 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 
   // A 16-row tile starts at the same offset in both weight layouts.
   const uint8_t* wexp = w + static_cast<size_t>(expert) * n_rows * K;
-  auto weight_fragment = [&](int rt, int kb) {
-    const uint8_t* tile = wexp + static_cast<size_t>(n0 + rt * 16) * K;
-    if constexpr (kPacked) return load_packed_fragment(tile, kb, lane);
-    return load_fragment(tile + row16 * K, kb, group);
+  int32x8 a_frag[RT][KB];
+  auto load_weights = [&](int tile, int kb0, int kb1) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        if (kb < kb0 || kb >= kb1) continue;
+        const uint8_t* rows = wexp + static_cast<size_t>(n0_of(tile) + rt * 16) * K;
+        if constexpr (kPacked)
+          a_frag[rt][kb] = load_packed_fragment(rows, kb, lane);
+        else
+          a_frag[rt][kb] = load_fragment(rows + row16 * K, kb, group);
+      }
+  };
+  float w_scale[RT][KB];
+  const float* wsexp = ws + static_cast<size_t>(expert) * (n_rows / kGroup) * KB;
+  auto load_scales = [&](int tile) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) w_scale[rt][kb] = wsexp[((n0_of(tile) + rt * 16) / kGroup) * KB + kb];
   };
   constexpr int kFirstHalf = MODE == 2 ? 0 : (KB > 1 ? KB / 2 : KB);
-  int32x8 a_frag[RT][KB];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int kb = 0; kb < kFirstHalf; ++kb) a_frag[rt][kb] = weight_fragment(rt, kb);
+  load_weights(first_tile, 0, kFirstHalf);
   __builtin_amdgcn_sched_barrier(0);
   // MODE 2 issues the gate / up rows before any weight (they are addressed
   // by sorted position, no route id needed), so the SwiGLU arithmetic runs
   // while the whole weight tile is in flight.
   fetch_tile(0);
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int kb = kFirstHalf; kb < KB; ++kb) a_frag[rt][kb] = weight_fragment(rt, kb);
-  float w_scale[RT][KB];
-  const float* wsexp = ws + static_cast<size_t>(expert) * (n_rows / kGroup) * KB;
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) w_scale[rt][kb] = wsexp[((n0 + rt * 16) / kGroup) * KB + kb];
+  load_weights(first_tile, kFirstHalf, KB);
+  load_scales(first_tile);
 
-  // One route tile against the register-resident weights.  The first tile
-  // runs outside the loop: staged registers carried around a loop back edge
-  // make the compiler wait for every outstanding load (the weights
-  // included) before staging.
-  auto run_tile = [&]() {
-    store_tile();
-    __syncthreads();
-
-    floatx4 acc[RT];
+  // One weight tile against the route tile in LDS.
+  auto mma = [&](floatx4 (&acc)[RT]) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint8_t* brow = b_tile + row16 * kStride;
@@ -253,11 +255,13 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
         }
       }
     }
+  };
+  auto epilogue = [&](const floatx4 (&acc)[RT], int tile) {
     const int target = b_target[row16];
     if (target >= 0) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        const int n = n0 + rt * 16 + group * 4;  // rows n..n+3 of this column
+        const int n = n0_of(tile) + rt * 16 + group * 4;  // rows n..n+3 of this column
         if constexpr (MODE == 0) {
           const uint32_t lo = f32_to_bf16(acc[rt][0]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][1])) << 16);
           const uint32_t hi = f32_to_bf16(acc[rt][2]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][3])) << 16);
@@ -280,7 +284,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       }
     }
     if constexpr (FUSE != kFuseNone) {
-      const int tile_n0 = (blockIdx.x % tiles) * kRowsPerGroup;
+      const int tile_n0 = tile * kRowsPerGroup;
       wait_stores();  // this tile's published outputs are visible device-wide
       __syncthreads();
       if (threadIdx.x < 16) {
@@ -297,7 +301,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
             if (take_ticket(&epi.tickets[index]) == contributors - 1) done = index;
           } else {
             // (token, column tile): one contribution per routed expert
-            const int index = (t / top_k) * tiles + (blockIdx.x % tiles);
+            const int index = (t / top_k) * tiles + tile;
             if (take_ticket(&epi.tickets[index]) == top_k - 1) done = index;
           }
         }
@@ -341,11 +345,40 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       }
     }
   };
-  run_tile();
-  for (int m0 = 16; m0 < routes; m0 += 16) {
-    __syncthreads();  // previous tile fully consumed
-    fetch_tile(m0);
-    run_tile();
+  // The first route tile is staged outside any loop: staged registers
+  // carried around a loop back edge make the compiler wait for every
+  // outstanding load (the weights included) before staging.
+  store_tile();
+  if constexpr (TILES > 1) {
+    // Items of at most 16 routes (one route tile, a launch contract): the
+    // TILES weight tiles pass through the same registers, tile tt + 1
+    // streaming in while tile tt's outputs are stored.
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < TILES; ++tt) {
+      floatx4 acc[RT];
+      mma(acc);
+      if (tt + 1 < TILES) {
+        // Not above the MFMAs: the next tile reuses this tile's registers.
+        __builtin_amdgcn_sched_barrier(0);
+        load_weights(first_tile + tt + 1, 0, KB);
+        load_scales(first_tile + tt + 1);
+      }
+      epilogue(acc, first_tile + tt);
+    }
+  } else {
+    // Route tiles of 16 against the one weight tile.
+    for (int m0 = 0; m0 < routes; m0 += 16) {
+      if (m0 > 0) {
+        __syncthreads();  // previous route tile fully consumed
+        fetch_tile(m0);
+        store_tile();
+      }
+      __syncthreads();
+      floatx4 acc[RT];
+      mma(acc);
+      epilogue(acc, first_tile);
+    }
   }
 }
 
@@ -472,22 +505,41 @@ struct GemmLaunch {
   const int4* items;
   const int32_t* num_items;
   int max_items;
+  int item_rows;  // upper bound on the routes of one item
   int exact_routes;
   uint16_t* out_bf16;
   float* out_f32;
   EpilogueArgs epi;
 };
 
+// Weight tiles per workgroup: FC2 takes two when every item is one route
+// tile and the tile count is even (the second tile streams in while the
+// first one's outputs are stored, the activation staging - and for MODE 2
+// the SwiGLU requant - is done once, and the two-tile kernel fits three
+// workgroups per CU).  FC1 keeps one: its tiles are 128 KiB, and longer
+// workgroups leave a longer partial last round (measured on c2: 65.5 us
+// with two tiles against 62.5 us with one).  Fused epilogues take one.
 template <int KB, int RT, int MODE, int FUSE>
-void launch_gemm(dim3 grid, hipStream_t s, const GemmLaunch& g) {
+void launch_gemm(int tiles, hipStream_t s, const GemmLaunch& g) {
+  const bool pair = FUSE == kFuseNone && MODE != 0 && tiles % 2 == 0 && g.item_rows <= 16;
+  const dim3 grid(g.max_items * (pair ? tiles / 2 : tiles));
+#define D3_GEMM_ARGS                                                                          \
+  grid, dim3(kGemmThreads), 0, s, g.w, g.ws, g.n, g.a, g.as, g.sorted_ids, g.top_k, g.items, \
+      g.num_items, g.exact_routes, g.out_bf16, g.out_f32, g.epi
+  if constexpr (FUSE == kFuseNone) {
+    if (pair) {
+      if (g.packed)
+        hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, true, 2>), D3_GEMM_ARGS);
+      else
+        hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, false, 2>), D3_GEMM_ARGS);
+      return;
+    }
+  }
   if (g.packed)
-    hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, true>), grid, dim3(kGemmThreads), 0,
-                       s, g.w, g.ws, g.n, g.a, g.as, g.sorted_ids, g.top_k, g.items, g.num_items,
-                       g.exact_routes, g.out_bf16, g.out_f32, g.epi);
+    hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, true, 1>), D3_GEMM_ARGS);
   else
-    hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, false>), grid, dim3(kGemmThreads), 0,
-                       s, g.w, g.ws, g.n, g.a, g.as, g.sorted_ids, g.top_k, g.items, g.num_items,
-                       g.exact_routes, g.out_bf16, g.out_f32, g.epi);
+    hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, false, 1>), D3_GEMM_ARGS);
+#undef D3_GEMM_ARGS
 }
 
 // FC2 with the SwiGLU prologue stages 2 x 16 bytes of gate / up per K block
@@ -501,23 +553,23 @@ int dispatch_gemm(const GemmLaunch& g, hipStream_t s) {
   constexpr int rows_per_group = tile_rows_for(KB);
   D3_SUPPORTED(g.n % rows_per_group == 0, "expert_gemm: N=%d must be a multiple of %d for K=%d",
                g.n, rows_per_group, KB * kGroup);
-  const dim3 grid(g.max_items * (g.n / rows_per_group));
+  const int tiles = g.n / rows_per_group;
   if (g.fuse == kFuseSwiglu) {
     if constexpr (rows_per_group <= kGroup) {
-      launch_gemm<KB, RT, 0, kFuseSwiglu>(grid, s, g);
+      launch_gemm<KB, RT, 0, kFuseSwiglu>(tiles, s, g);
       return D3_OK;
     }
     return set_error(D3_ERR_UNSUPPORTED, "expert_fc1_swiglu: K=%d tiles %d rows (> 128)",
                      KB * kGroup, rows_per_group);
   }
   if (g.fuse == kFuseCombine)
-    launch_gemm<KB, RT, 1, kFuseCombine>(grid, s, g);
+    launch_gemm<KB, RT, 1, kFuseCombine>(tiles, s, g);
   else if (g.mode == 0)
-    launch_gemm<KB, RT, 0, kFuseNone>(grid, s, g);
+    launch_gemm<KB, RT, 0, kFuseNone>(tiles, s, g);
   else if (g.mode == 1)
-    launch_gemm<KB, RT, 1, kFuseNone>(grid, s, g);
+    launch_gemm<KB, RT, 1, kFuseNone>(tiles, s, g);
   else if constexpr (KB <= kMaxSwigluKB)
-    launch_gemm<KB, RT, 2, kFuseNone>(grid, s, g);
+    launch_gemm<KB, RT, 2, kFuseNone>(tiles, s, g);
   else
     return set_error(D3_ERR_UNSUPPORTED, "expert_fc2_swiglu: intermediate %d > %d", KB * kGroup,
                      kMaxSwigluKB * kGroup);
@@ -574,15 +626,17 @@ extern "C" int d3_expert_gemm(int32_t mode, const uint8_t* w, const float* ws,
                               int32_t weight_layout, int32_t num_experts, int32_t n, int32_t k,
                               const uint8_t* a, const float* a_scales,
                               const int32_t* sorted_ids, int32_t top_k, const int32_t* items,
-                              const int32_t* num_items, int32_t max_items, int32_t exact_routes,
-                              uint16_t* out_bf16, float* out_f32, void* stream) {
+                              const int32_t* num_items, int32_t max_items, int32_t item_rows,
+                              int32_t exact_routes, uint16_t* out_bf16, float* out_f32,
+                              void* stream) {
   D3_REQUIRE(mode == 0 || mode == 1, "expert_gemm: mode must be 0 (FC1) or 1 (FC2)");
   D3_REQUIRE(mode == 0 ? out_bf16 != nullptr : out_f32 != nullptr, "expert_gemm: null output");
   D3_REQUIRE(mode == 0 ? aligned(out_bf16, 8) : aligned(out_f32, 16),
              "expert_gemm: output alignment");
+  D3_REQUIRE(item_rows >= 1, "expert_gemm: item_rows must be positive");
   const GemmLaunch g{mode, kFuseNone, weight_layout, w, ws, n, a, a_scales, sorted_ids, top_k,
-                     reinterpret_cast<const int4*>(items), num_items, max_items, exact_routes,
-                     out_bf16, out_f32, EpilogueArgs{}};
+                     reinterpret_cast<const int4*>(items), num_items, max_items, item_rows,
+                     exact_routes, out_bf16, out_f32, EpilogueArgs{}};
   int status = check_gemm(g, num_experts, k, "expert_gemm");
   if (status != D3_OK) return status;
   if (max_items == 0) {
@@ -613,8 +667,8 @@ extern "C" int d3_expert_fc1_swiglu(const uint8_t* w13, const float* s13, int32_
   epi.act_scales_out = act_scales;
   const GemmLaunch g{0, kFuseSwiglu, weight_layout, w13, s13, 2 * intermediate, q, x_scales,
                      sorted_ids, top_k,
-                     reinterpret_cast<const int4*>(items), num_items, max_items, exact_routes,
-                     gate_up, nullptr, epi};
+                     reinterpret_cast<const int4*>(items), num_items, max_items, 1 << 30,
+                     exact_routes, gate_up, nullptr, epi};
   int status = check_gemm(g, num_experts, hidden, "expert_fc1_swiglu");
   if (status != D3_OK) return status;
   if (max_items == 0) {
@@ -646,8 +700,8 @@ extern "C" int d3_expert_fc2_combine(const uint8_t* w2, const float* s2, int32_t
   epi.combined = out;
   const GemmLaunch g{1, kFuseCombine, weight_layout, w2, s2, hidden, act, act_scales, sorted_ids,
                      top_k,
-                     reinterpret_cast<const int4*>(items), num_items, max_items, exact_routes,
-                     nullptr, down, epi};
+                     reinterpret_cast<const int4*>(items), num_items, max_items, 1 << 30,
+                     exact_routes, nullptr, down, epi};
   int status = check_gemm(g, num_experts, intermediate, "expert_fc2_combine");
   if (status != D3_OK) return status;
   if (max_items == 0) {
@@ -663,14 +717,15 @@ extern "C" int d3_expert_fc2_swiglu(const uint8_t* w2, const float* s2, int32_t 
                                     int32_t num_experts, int32_t hidden, int32_t intermediate,
                                     const uint16_t* gate_up, const int32_t* sorted_ids,
                                     int32_t top_k, const int32_t* items, const int32_t* num_items,
-                                    int32_t max_items, int32_t exact_routes, float* down,
-                                    void* stream) {
+                                    int32_t max_items, int32_t item_rows, int32_t exact_routes,
+                                    float* down, void* stream) {
   D3_REQUIRE(gate_up && down, "expert_fc2_swiglu: null pointer");
+  D3_REQUIRE(item_rows >= 1, "expert_fc2_swiglu: item_rows must be positive");
   D3_REQUIRE(aligned(gate_up, 16) && aligned(down, 16), "expert_fc2_swiglu: alignment");
   const GemmLaunch g{2, kFuseNone, weight_layout, w2, s2, hidden,
                      reinterpret_cast<const uint8_t*>(gate_up), nullptr, sorted_ids, top_k,
-                     reinterpret_cast<const int4*>(items), num_items, max_items, exact_routes,
-                     nullptr, down, EpilogueArgs{}};
+                     reinterpret_cast<const int4*>(items), num_items, max_items, item_rows,
+                     exact_routes, nullptr, down, EpilogueArgs{}};
   int status = check_gemm(g, num_experts, intermediate, "expert_fc2_swiglu");
   if (status != D3_OK) return status;
   if (max_items == 0) {

@@ -27,6 +27,27 @@ constexpr int kGemmThreads = kGemmWaves * kWave;
 constexpr int rt_for(int kb) { return kb >= 8 ? 1 : (kb >= 4 ? 2 : 4); }
 constexpr int tile_rows_for(int kb) { return kGemmWaves * rt_for(kb) * 16; }
 
+// Raw (untyped) buffer view: loads at or past `bytes` return zeros, so lanes
+// with nothing to load take an out-of-range offset instead of a branch (a
+// branch around a load leaves register copies that force an early wait on
+// every outstanding load).  kPolicy: cache policy bits (16 = sc1, coherent
+// across the XCDs' L2s).
+constexpr uint32_t kNoRow = 0x80000000u;  // past every buffer used here
+struct BufferView {
+  __amdgpu_buffer_rsrc_t rsrc;
+  __device__ BufferView(const void* base, uint32_t bytes)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000)) {}
+  template <int kPolicy = 0>
+  __device__ int4 load16(uint32_t offset) const {
+    const int32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, kPolicy);
+    return make_int4(v[0], v[1], v[2], v[3]);
+  }
+  template <int kPolicy = 0>
+  __device__ uint32_t load4(uint32_t offset) const {
+    return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rsrc, offset, 0, kPolicy));
+  }
+};
+
 // Fragment of one row in the reference layout [N, K] (row = this lane's row).
 __device__ __forceinline__ int32x8 load_fragment(const uint8_t* row, int kb, int group) {
   const uint8_t* p = row + kb * kGroup + group * 16;

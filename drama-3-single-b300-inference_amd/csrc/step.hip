@@ -60,26 +60,15 @@ constexpr int kActBatch = 4;      // requant units per thread loaded before arit
 // expect to find the route sort done.
 constexpr int kFirstWave = 512;
 
-// Raw (untyped) buffer resource: 32-bit data format, no swizzle; bytes past
-// num_records read as zero and are not written.
-constexpr int kRawBufferFormat = 0x00020000;
 constexpr int kCoherent = 16;  // cache policy sc1: device-coherent access
 
+// Buffer view whose loads are coherent across the XCDs' L2s.
 struct CoherentBuffer {
-  __amdgpu_buffer_rsrc_t rsrc;
-  __device__ CoherentBuffer(const void* base, uint32_t bytes)
-      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes,
-                                               kRawBufferFormat)) {}
-  __device__ int4 load16(uint32_t offset) const {
-    const int32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, kCoherent);
-    return make_int4(v[0], v[1], v[2], v[3]);
-  }
-  __device__ uint32_t load4(uint32_t offset) const {
-    return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rsrc, offset, 0, kCoherent));
-  }
+  BufferView view;
+  __device__ CoherentBuffer(const void* base, uint32_t bytes) : view(base, bytes) {}
+  __device__ int4 load16(uint32_t offset) const { return view.load16<kCoherent>(offset); }
+  __device__ uint32_t load4(uint32_t offset) const { return view.load4<kCoherent>(offset); }
 };
-// Offset past every buffer here: the load returns zeros without a branch.
-constexpr uint32_t kNoRow = 0x80000000u;
 
 struct StepArgs {
   const uint8_t* occupancy;
@@ -499,6 +488,8 @@ __device__ void expert_task(const StepArgs& a, int expert, int tile_group, uint8
       floatx4 acc[RT];
       mma(acc);
       if (tt + 1 < TILES) {
+        // Not above the MFMAs: the next tile reuses this tile's registers.
+        __builtin_amdgcn_sched_barrier(0);
         load_weights(first_tile + tt + 1, 0, KB);
         load_scales(first_tile + tt + 1);
       }
@@ -510,6 +501,7 @@ __device__ void expert_task(const StepArgs& a, int expert, int tile_group, uint8
 #pragma unroll
     for (int tt = 0; tt < TILES; ++tt) {
       if (tt > 0) {
+        __builtin_amdgcn_sched_barrier(0);
         load_weights(first_tile + tt, 0, KB);
         load_scales(first_tile + tt);
       }

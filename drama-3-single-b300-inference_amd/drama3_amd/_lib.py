@@ -51,8 +51,8 @@ SIGNATURES = {
     "d3_max_sorted_rows": (_i32, [_i32, _i32, _i32]),
     "d3_max_items": (_i32, [_i32, _i32, _i32]),
     "d3_expert_gemm": (
-        _i32, [_i32, _p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p,
-               _p]),
+        _i32, [_i32, _p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32,
+               _p, _p, _p]),
     "d3_expert_tile_rows": (_i32, [_i32]),
     "d3_pack_expert_weights": (_i32, [_p, _i32, _i32, _i32, _p, _p]),
     "d3_expert_fc1_swiglu": (
@@ -62,7 +62,9 @@ SIGNATURES = {
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _i32, _p,
                _p, _p]),
     "d3_expert_fc2_swiglu": (
-        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p]),
+        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _p, _p]),
+    "d3_decode_expert_gemm": (
+        _i32, [_i32, _p, _p, _i32, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _i32, _p, _p, _p]),
     "d3_moe_step_sync_ints": (_i32, [_i32, _i32, _i32, _i32]),
     "d3_moe_decode_step": (
         _i32, [_p, _i32, _p, _p, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32,

@@ -53,11 +53,17 @@ def require_cuda(*tensors: torch.Tensor | None) -> None:
             raise ValueError("MI355X MoE operators need device tensors (no CPU fallback)")
 
 
-def default_item_rows(rows: int, tile: int = SORT_TILE) -> int:
+def default_item_rows(rows: int, tile: int = SORT_TILE, num_experts: int | None = None,
+                      top_k: int = 8) -> int:
     """Routes per work item (a multiple of ``tile``).  Up to 128 rows an
     expert cannot receive more routes than rows, so one item covers all of an
     expert's routes (one weight read per expert); larger batches cap items at
-    128 routes so busy experts spread over several workgroups."""
+    128 routes so busy experts spread over several workgroups.  When experts
+    are sparse (at most 8 routes each on average at full capacity) items are
+    one 16-route tile: the expert GEMM then pipelines two weight tiles per
+    workgroup, and the rare expert with more routes is read once per item."""
+    if num_experts is not None and rows <= 128 and rows * top_k <= 8 * num_experts:
+        return tile
     rows = min(rows, 128) if rows > 128 else rows
     return max(tile, -(-rows // tile) * tile)
 
@@ -81,13 +87,14 @@ class MoEWorkspace:
     def __init__(self, shape: Shape, device: torch.device | str = "cuda", tile: int = SORT_TILE,
                  item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
                  exact_routes: int = EXACT_ROUTES, fused_epilogues: bool = False,
-                 swiglu_in_fc2: bool | None = None):
+                 swiglu_in_fc2: bool | None = None, sortless: bool = False):
         lib = _lib.load()
         self.shape = shape
         self.device = torch.device(device)
         self.tile = tile
         self.exact_routes = exact_routes
-        self.item_rows = item_rows or default_item_rows(shape.rows, tile)
+        self.item_rows = item_rows or default_item_rows(shape.rows, tile, shape.num_experts,
+                                                        shape.top_k)
         if self.item_rows % tile:
             raise ValueError("item_rows must be a multiple of the sort tile")
         pairs = shape.pairs
@@ -130,6 +137,12 @@ class MoEWorkspace:
         if swiglu_in_fc2 is None:
             swiglu_in_fc2 = self.item_rows <= EXACT_ROUTES and i <= 1024
         self.swiglu_in_fc2 = swiglu_in_fc2 and not self.fuse_fc1 and not self.fuse_fc2
+        # Sortless decode: the front skips the route sort and the expert GEMMs
+        # (d3_decode_expert_gemm, fragment-major weights) find each expert's
+        # routes themselves; gate_up / down rows are indexed by pair.
+        self.sortless = sortless
+        if sortless and (t > 256 or shape.top_k > 8):
+            raise ValueError("sortless decode covers up to 256 rows and top_k <= 8")
         self.fc1_tickets = torch.zeros(self.max_rows * (i // 128) if self.fuse_fc1 else 1, **i32)
         self.fc2_tickets = torch.zeros(t * (h // fc2_tile) if self.fuse_fc2 else 1, **i32)
 
@@ -163,7 +176,7 @@ class MoEWorkspace:
         (two when the batch exceeds the fused sort).  With ``occupancy`` the
         rows are the live slots (``active`` / ``count`` receive the list)."""
         s, stream = self.shape, self._stream(stream)
-        fused = s.pairs <= FUSED_SORT_PAIRS
+        fused = s.pairs <= FUSED_SORT_PAIRS and not self.sortless
         slots = occupancy.numel() if occupancy is not None else 0
         if occupancy is not None and slots != s.rows:
             raise ValueError("slot mode needs a workspace with one row per slot")
@@ -177,7 +190,7 @@ class MoEWorkspace:
              ptr(row_count), s.hidden, s.num_experts, s.top_k, ptr(self.ids), ptr(self.weights),
              dtype_code(self.weights.dtype), ptr(self.q), ptr(self.x_scales), self.tile,
              self.item_rows, *sort_args, stream)
-        if not fused:
+        if not fused and not self.sortless:
             self.sort(None, count if occupancy is not None else row_count, stream)
 
     def fc1(self, experts, stream=None) -> None:
@@ -186,7 +199,7 @@ class MoEWorkspace:
         call("d3_expert_gemm", 0, ptr(w), ptr(ws), layout,
              s.num_experts, 2 * s.intermediate, s.hidden, ptr(self.q), ptr(self.x_scales),
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
-             self.exact_routes, ptr(self.gate_up), None, stream)
+             self.item_rows, self.exact_routes, ptr(self.gate_up), None, stream)
 
     def activation(self, stream=None) -> None:
         s, stream = self.shape, self._stream(stream)
@@ -200,7 +213,7 @@ class MoEWorkspace:
         call("d3_expert_gemm", 1, ptr(w), ptr(ws), layout,
              s.num_experts, s.hidden, s.intermediate, ptr(self.act), ptr(self.act_scales),
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
-             self.exact_routes, None, ptr(self.down), stream)
+             self.item_rows, self.exact_routes, None, ptr(self.down), stream)
 
     def fc2_swiglu(self, experts, stream=None) -> None:
         """FC2 whose workgroups compute the SwiGLU requant of their routes
@@ -209,7 +222,8 @@ class MoEWorkspace:
         w, ws, layout = fc2_operands(experts)
         call("d3_expert_fc2_swiglu", ptr(w), ptr(ws), layout, s.num_experts, s.hidden,
              s.intermediate, ptr(self.gate_up), ptr(self.sorted_ids), s.top_k, ptr(self.items),
-             ptr(self.num_items), self.max_items, self.exact_routes, ptr(self.down), stream)
+             ptr(self.num_items), self.max_items, self.item_rows, self.exact_routes,
+             ptr(self.down), stream)
 
     def combine(self, weights: torch.Tensor | None = None, row_count=None, shared=None,
                 out=None, stream=None) -> torch.Tensor:
@@ -264,11 +278,35 @@ class MoEWorkspace:
              ptr(out), ptr(self.fc2_tickets), stream)
         return out
 
+    def decode_fc1(self, experts, row_count=None, stream=None) -> None:
+        """Sortless FC1: gate_up[pair] for every live route (fragment-major W13)."""
+        s, stream = self.shape, self._stream(stream)
+        w, ws, layout = fc1_operands(experts)
+        if layout != LAYOUT_FRAGMENT:
+            raise ValueError("sortless decode needs fragment-major weights (prepare_experts)")
+        call("d3_decode_expert_gemm", 0, ptr(w), ptr(ws), s.num_experts, 2 * s.intermediate,
+             s.hidden, ptr(self.ids), ptr(row_count), s.rows, s.top_k, ptr(self.q),
+             ptr(self.x_scales), self.exact_routes, ptr(self.gate_up), None, stream)
+
+    def decode_fc2(self, experts, row_count=None, stream=None) -> None:
+        """Sortless FC2 with the SwiGLU requant in its prologue: down[pair]."""
+        s, stream = self.shape, self._stream(stream)
+        w, ws, layout = fc2_operands(experts)
+        if layout != LAYOUT_FRAGMENT:
+            raise ValueError("sortless decode needs fragment-major weights (prepare_experts)")
+        call("d3_decode_expert_gemm", 2, ptr(w), ptr(ws), s.num_experts, s.hidden,
+             s.intermediate, ptr(self.ids), ptr(row_count), s.rows, s.top_k, ptr(self.gate_up),
+             None, self.exact_routes, None, ptr(self.down), stream)
+
     def experts(self, experts, row_count=None, shared=None, out=None, stream=None):
         """FC1, SwiGLU requant, FC2 and combine over the routes sorted by front().
         With ``fused_epilogues`` two launches replace four; a dense shared
         expert is always added by the separate combine."""
         stream = _lib.stream(self.device) if stream is None else stream
+        if self.sortless:
+            self.decode_fc1(experts, row_count, stream)
+            self.decode_fc2(experts, row_count, stream)
+            return self.combine(None, row_count, shared, out, stream)
         if self.fuse_fc1:
             self.fc1_swiglu(experts, stream)
         else:
@@ -311,14 +349,14 @@ class DenseExpert:
         h, i = self.hidden, self.intermediate
         w13, s13, layout13 = fc1_operands(experts)
         w2, s2, layout2 = fc2_operands(experts)
-        call("d3_expert_gemm", 0, ptr(w13), ptr(s13), layout13, 1, 2 * i, h, ptr(q), ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items),
-             ptr(self.num_items), self.max_items, self.exact_routes, ptr(self.gate_up), None,
-             stream)
+        call("d3_expert_gemm", 0, ptr(w13), ptr(s13), layout13, 1, 2 * i, h, ptr(q),
+             ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items), ptr(self.num_items),
+             self.max_items, self.item_rows, self.exact_routes, ptr(self.gate_up), None, stream)
         call("d3_silu_mul_quant", ptr(self.gate_up), self.rows, i, None, None, None, 0,
              ptr(self.act), ptr(self.act_scales), stream)
-        call("d3_expert_gemm", 1, ptr(w2), ptr(s2), layout2, 1, h, i, ptr(self.act), ptr(self.act_scales), ptr(self.sorted_ids), 1, ptr(self.items),
-             ptr(self.num_items), self.max_items, self.exact_routes, None, ptr(self.down),
-             stream)
+        call("d3_expert_gemm", 1, ptr(w2), ptr(s2), layout2, 1, h, i, ptr(self.act),
+             ptr(self.act_scales), ptr(self.sorted_ids), 1, ptr(self.items), ptr(self.num_items),
+             self.max_items, self.item_rows, self.exact_routes, None, ptr(self.down), stream)
         return self.down
 
 
@@ -345,14 +383,24 @@ class DecodeStep:
 
     def __init__(self, slots: int, num_experts: int, hidden: int, intermediate: int,
                  top_k: int = 8, device="cuda", item_rows: int | None = None,
-                 fused: bool | None = None):
+                 fused: bool | None = None, sortless: bool | None = None):
         dev = torch.device(device)
         self.slots = slots
         self.active = torch.empty(slots, dtype=torch.int32, device=dev)
         self.count = torch.empty(1, dtype=torch.int32, device=dev)
         self.workspace = MoEWorkspace(Shape(slots, num_experts, hidden, intermediate, top_k), dev,
                                       item_rows=item_rows)
+        # Sortless expert GEMMs (default when the slots' routes cover the
+        # experts densely: at least 4 routes per expert at full occupancy,
+        # and the shapes are in the compiled set) on fragment-major weights.
         lib = _lib.load()
+        decode_shapes = (hidden // 128 in (8, 16) and intermediate // 128 in (2, 4, 6, 8)
+                         and hidden % 128 == 0 and intermediate % 128 == 0
+                         and hidden % lib.d3_expert_tile_rows(intermediate) == 0)
+        dense = slots * top_k >= 4 * num_experts
+        if sortless is None:
+            sortless = decode_shapes and dense and slots <= 256 and top_k <= 8
+        self.sortless = bool(sortless)
         sync_ints = lib.d3_moe_step_sync_ints(slots, num_experts, hidden, intermediate)
         supported = sync_ints > 0 and slots <= 256 and num_experts <= 256
         if fused and not supported:
@@ -372,9 +420,18 @@ class DecodeStep:
         ws = self.workspace
         if self.uses_fused(logits_slots, experts):
             return self._fused(occupancy, x_slots, logits_slots, experts, stream)
+        ws.sortless = self.sortless and self.uses_sortless(experts)
         ws.front(x_slots, logits_slots, occupancy=occupancy, active=self.active,
                  count=self.count, stream=stream)
         return ws.experts(experts, self.count, stream=stream)
+
+    @staticmethod
+    def uses_sortless_layout(experts) -> bool:
+        return (fc1_operands(experts)[2] == LAYOUT_FRAGMENT
+                and fc2_operands(experts)[2] == LAYOUT_FRAGMENT)
+
+    def uses_sortless(self, experts) -> bool:
+        return self.sortless and self.uses_sortless_layout(experts)
 
     def _fused(self, occupancy, x_slots, logits_slots, experts, stream) -> torch.Tensor:
         ws, s = self.workspace, self.workspace.shape

@@ -179,15 +179,20 @@ int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);
  * FP8 -> bf16 widening (fp32-accurate sums); larger items use FP8 MFMAs,
  * whose in-instruction product alignment rounds at ~1e-4 of sum|products|.
  * Work items cover live routes only, so padding slots are never read.
- * The grid is max_items x (N / row tile); items at or beyond *num_items exit.
+ * item_rows: upper bound on the routes of one item (the sort's item_rows).
+ * With item_rows <= 16 (every item one 16-route MFMA tile) each FC2
+ * workgroup takes two consecutive weight tiles of its item, the second
+ * streaming in while the first one's outputs are stored; otherwise one.
+ * The grid is max_items x (N / row tile) / tiles per workgroup; items at or
+ * beyond *num_items exit.
  * Supported: K in {256, 512, 768, 1024, 1536, 2048}; N a multiple of the
  * workgroup row tile (64 for K >= 1024, 128 for K = 512/768, 256 for K = 256).
  */
 int d3_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32_t weight_layout,
                    int32_t num_experts, int32_t n, int32_t k, const uint8_t *a, const float *a_scales,
                    const int32_t *sorted_ids, int32_t top_k, const int32_t *items,
-                   const int32_t *num_items, int32_t max_items, int32_t exact_routes,
-                   uint16_t *out_bf16, float *out_f32, void *stream);
+                   const int32_t *num_items, int32_t max_items, int32_t item_rows,
+                   int32_t exact_routes, uint16_t *out_bf16, float *out_f32, void *stream);
 
 /* Weight rows per workgroup tile of d3_expert_gemm for contraction length k. */
 int32_t d3_expert_tile_rows(int32_t k);
@@ -256,7 +261,33 @@ int d3_expert_fc2_swiglu(const uint8_t *w2, const float *s2, int32_t weight_layo
                          int32_t num_experts, int32_t hidden, int32_t intermediate,
                          const uint16_t *gate_up, const int32_t *sorted_ids, int32_t top_k,
                          const int32_t *items, const int32_t *num_items, int32_t max_items,
-                         int32_t exact_routes, float *down, void *stream);
+                         int32_t item_rows, int32_t exact_routes, float *down, void *stream);
+
+/*
+ * A8-A11  Decode expert GEMMs without a route sort.
+ * Replaces expert_up_kernel / expert_down_kernel (src/drama3/kernels.py:290-318)
+ * with the Fish silu_mul_quant between them (kernels.py:344) for decode
+ * batches, where the reference sorts routes first (kernels.py:658-731).
+ * The grid is (expert, weight row tile); each workgroup finds its expert's
+ * routes in ids int32 [capacity, top_k] (rows below *row_count, or all
+ * capacity rows when row_count is NULL), in ascending pair order, while its
+ * weight tile streams in.  Rows are indexed by pair = row * top_k + rank:
+ *   mode 0 (FC1): a = q fp8 [capacity, k], a_scales [capacity, k/128]
+ *                 -> out_bf16 gate_up [capacity * top_k, n], n = 2I, k = H;
+ *   mode 2 (FC2): a = gate_up bf16 [capacity * top_k, 2k]; the SwiGLU
+ *                 requant of each route is computed in the prologue exactly
+ *                 as d3_silu_mul_quant -> out_f32 down [capacity * top_k, n],
+ *                 n = H, k = I.
+ * Values equal d3_expert_gemm's for the same pair.  Weights must be
+ * fragment-major (d3_pack_expert_weights).  A workgroup of an expert with no
+ * route reads half a weight tile before it knows, so this suits batches
+ * whose routes cover most experts.  capacity <= 256, top_k <= 8; k in
+ * {1024, 2048} (mode 0) or {256, 512, 768, 1024} (mode 2).
+ */
+int d3_decode_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32_t num_experts,
+                          int32_t n, int32_t k, const int32_t *ids, const int32_t *row_count,
+                          int32_t capacity, int32_t top_k, const void *a, const float *a_scales,
+                          int32_t exact_routes, uint16_t *out_bf16, float *out_f32, void *stream);
 
 /*
  * A1-A12  The whole decode MoE step in one launch.

@@ -82,7 +82,7 @@ def test_capacity_helpers(lib):
     for pairs, experts, tile in ((32, 16, 16), (384, 128, 16), (33280, 128, 64), (0, 8, 16)):
         assert lib.d3_max_sorted_rows(pairs, experts, tile) == om.max_sorted_rows(pairs, experts, tile)
     assert lib.d3_max_items(384, 128, 64) == (384 + 128 * 63) // 64
-    assert lib.d3_abi_version() == 2
+    assert lib.d3_abi_version() == 3
 
 
 def test_contract_violations_raise_value_error(lib):
@@ -98,14 +98,14 @@ def test_contract_violations_raise_value_error(lib):
         _lib.call("d3_sort_routes", 16, 3, 4, None, 8, 16, 16, 16, 16, 16, 16, 16, 8, None, 16,
                   None, 0, None, None, None)
     with pytest.raises(ValueError, match="K="):
-        _lib.call("d3_expert_gemm", 0, 16, 16, 0, 4, 512, 384, 16, 16, 16, 8, 16, 16, 4, 64, 16,
-                  None, None)
+        _lib.call("d3_expert_gemm", 0, 16, 16, 0, 4, 512, 384, 16, 16, 16, 8, 16, 16, 4, 16, 64,
+                  16, None, None)
     with pytest.raises(ValueError, match="weight_layout"):
-        _lib.call("d3_expert_gemm", 0, 16, 16, 7, 4, 512, 512, 16, 16, 16, 8, 16, 16, 4, 64, 16,
-                  None, None)
+        _lib.call("d3_expert_gemm", 0, 16, 16, 7, 4, 512, 512, 16, 16, 16, 8, 16, 16, 4, 16, 64,
+                  16, None, None)
     with pytest.raises(ValueError, match="intermediate 2048"):
-        _lib.call("d3_expert_fc2_swiglu", 16, 16, 0, 4, 1024, 2048, 16, 16, 8, 16, 16, 4, 64, 16,
-                  None)
+        _lib.call("d3_expert_fc2_swiglu", 16, 16, 0, 4, 1024, 2048, 16, 16, 8, 16, 16, 4, 16, 64,
+                  16, None)
     with pytest.raises(ValueError, match="multiple of 16"):
         _lib.call("d3_pack_expert_weights", 16, 4, 24, 128, 32, None)
     assert "K=" in lib.d3_last_error().decode()

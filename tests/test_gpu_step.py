@@ -19,7 +19,8 @@ def make_steps(w, device):
 
     experts = prepare_experts(w.experts.to(device))
     fused = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device, fused=True)
-    chain = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device, fused=False)
+    chain = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device, fused=False,
+                       sortless=False)
     chain.workspace.swiglu_in_fc2 = False  # the chain writes act / act_scales too
     return experts, fused, chain
 
@@ -144,7 +145,8 @@ def test_fused_step_graph_replays(device):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         out = fused(occ, xs, ls, experts)
-    chain = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device, fused=False)
+    chain = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device, fused=False,
+                       sortless=False)
     rng = np.random.default_rng(1)
     for replay, p in enumerate([0.1, 0.5, 0.9, 1.0, 0.0]):
         occupancy = (rng.uniform(size=64) < p).astype(np.uint8)
