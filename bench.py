@@ -33,7 +33,7 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 # this script (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors read off
 # the 1 GiB device copy in the same runs); profiles/expert_gemm_c2_hbm_traffic.md.
 # Re-measure whenever the FC1 kernel or its tiling changes.
-FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,0,1>", "bytes": 402288538}
+FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,0,6>", "bytes": 400085606}
 
 
 def parse():

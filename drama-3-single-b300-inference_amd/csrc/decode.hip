@@ -33,8 +33,8 @@ constexpr int kIdsPerThread = kMaxIds / kGemmThreads;  // 8
 // MODE 0: FC1, q rows of the routes' tokens x W13 -> bf16 gate|up by pair.
 // MODE 2: FC2 with the SwiGLU requant in the prologue, gate|up by pair x W2
 //         -> fp32 down by pair.
-// TILES weight tiles per workgroup (TILES > 1: routes beyond the first 16
-// reload the weight tiles).
+// TILES weight tiles per workgroup, streamed through the registers in halves
+// (TILES > 1: routes beyond the first 16 reload the weight tiles).
 template <int KB, int RT, int MODE, int TILES>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows,
@@ -192,13 +192,13 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     if (stage_part == 0) b_target[stage_col] = stage_pair;
   };
 
-  auto mma = [&](floatx4 (&acc)[RT]) {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) acc[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  // K blocks [kb0, kb1) of one weight tile against the route tile in LDS.
+  auto mma_range = [&](floatx4 (&acc)[RT], int kb0, int kb1) {
     const uint8_t* brow = b_tile + row16 * kStride;
     if (exact) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
+        if (kb < kb0 || kb >= kb1) continue;
         bf16x8 b_wide[4];
         widen_fp8(load_fragment(brow, kb, group), b_wide);
         const float b_scale = b_scales[row16 * KB + kb];
@@ -212,6 +212,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     } else {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
+        if (kb < kb0 || kb >= kb1) continue;
         const int32x8 b_frag = load_fragment(brow, kb, group);
         const float b_scale = b_scales[row16 * KB + kb];
 #pragma unroll
@@ -221,6 +222,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
         }
       }
     }
+  };
+  auto mma = [&](floatx4 (&acc)[RT]) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    mma_range(acc, 0, KB);
   };
   auto epilogue = [&](const floatx4 (&acc)[RT], int tile) {
     const int target = b_target[row16];
@@ -247,15 +253,26 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   store_tile();
   __syncthreads();
   if constexpr (TILES > 1) {
-    // Weight tiles pass through the same registers: tile tt + 1 streams in
-    // while tile tt's outputs are stored.
+    // Weight tiles stream through the same registers in halves: once the
+    // first half of tile tt has been multiplied, the first half of tile
+    // tt + 1 is loaded into its registers while the second half of tile tt
+    // is multiplied, and so on, so every wave keeps at least half a tile of
+    // loads in flight until its last tile (memory returns are counted in
+    // issue order, so each wait covers only the half it needs).
 #pragma unroll
     for (int tt = 0; tt < TILES; ++tt) {
       floatx4 acc[RT];
-      mma(acc);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) acc[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      mma_range(acc, 0, kFirstHalf);
       if (tt + 1 < TILES) {
-        __builtin_amdgcn_sched_barrier(0);  // the next tile reuses these registers
-        load_weights(first_tile + tt + 1, 0, KB);
+        __builtin_amdgcn_sched_barrier(0);  // the next half reuses these registers
+        load_weights(first_tile + tt + 1, 0, kFirstHalf);
+      }
+      mma_range(acc, kFirstHalf, KB);
+      if (tt + 1 < TILES) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_weights(first_tile + tt + 1, kFirstHalf, KB);
         load_scales(first_tile + tt + 1);
       }
       epilogue(acc, first_tile + tt);
@@ -293,20 +310,52 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 
 bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
-template <int KB, int MODE>
-void launch_decode(int num_experts, int n, bool pair, hipStream_t s, const uint8_t* w,
-                   const float* ws, const int32_t* ids, const int32_t* row_count, int capacity,
-                   int top_k, const void* a, const float* as, int exact_routes,
-                   uint16_t* out_bf16, float* out_f32) {
-  constexpr int RT = rt_for(KB);
+template <int KB, int MODE, int TILES>
+void launch_tiles(int num_experts, int n, hipStream_t s, const uint8_t* w, const float* ws,
+                  const int32_t* ids, const int32_t* row_count, int capacity, int top_k,
+                  const void* a, const float* as, int exact_routes, uint16_t* out_bf16,
+                  float* out_f32) {
   const int tiles = n / tile_rows_for(KB);
-  const dim3 block(kGemmThreads);
-  if (pair)
-    hipLaunchKernelGGL((decode_gemm_kernel<KB, RT, MODE, 2>), dim3(num_experts * (tiles / 2)), block, 0, s,
-                       w, ws, n, ids, row_count, capacity, top_k, a, as, exact_routes, out_bf16, out_f32);
-  else
-    hipLaunchKernelGGL((decode_gemm_kernel<KB, RT, MODE, 1>), dim3(num_experts * tiles), block, 0, s,
-                       w, ws, n, ids, row_count, capacity, top_k, a, as, exact_routes, out_bf16, out_f32);
+  hipLaunchKernelGGL((decode_gemm_kernel<KB, rt_for(KB), MODE, TILES>),
+                     dim3(num_experts * (tiles / TILES)), dim3(kGemmThreads), 0, s, w, ws, n, ids,
+                     row_count, capacity, top_k, a, as, exact_routes, out_bf16, out_f32);
+}
+
+// Weight tiles per workgroup: enough that the whole grid is about one round
+// of resident workgroups (two per CU), so each workgroup streams its tiles
+// back to back instead of the GPU turning workgroups over; a divisor of the
+// expert's tile count.  Experts averaging more than 8 routes at full
+// capacity take one tile per workgroup (each further route tile would walk
+// all of a workgroup's tiles again).
+constexpr int kResidentGroups = 512;
+int tiles_per_group(int num_experts, int tiles, int capacity, int top_k, int mode) {
+  if (capacity * top_k > 8 * num_experts) return 1;
+  const int options[] = {1, 2, 4, 6};
+  const int limit = mode == 0 ? 6 : 4;
+  for (int t : options)
+    if (t <= limit && tiles % t == 0 && num_experts * (tiles / t) <= kResidentGroups) return t;
+  for (int i = 3; i >= 0; --i)
+    if (options[i] <= limit && tiles % options[i] == 0) return options[i];
+  return 1;
+}
+
+template <int KB, int MODE>
+void launch_decode(int num_experts, int n, hipStream_t s, const uint8_t* w, const float* ws,
+                   const int32_t* ids, const int32_t* row_count, int capacity, int top_k,
+                   const void* a, const float* as, int exact_routes, uint16_t* out_bf16,
+                   float* out_f32) {
+  const int tiles = n / tile_rows_for(KB);
+  const int t = tiles_per_group(num_experts, tiles, capacity, top_k, MODE);
+#define D3_TILES(T)                                                                             \
+  launch_tiles<KB, MODE, T>(num_experts, n, s, w, ws, ids, row_count, capacity, top_k, a, as, \
+                            exact_routes, out_bf16, out_f32)
+  if constexpr (MODE == 0) {
+    if (t == 6) { D3_TILES(6); return; }
+  }
+  if (t == 4) D3_TILES(4);
+  else if (t == 2) D3_TILES(2);
+  else D3_TILES(1);
+#undef D3_TILES
 }
 
 }  // namespace
@@ -336,13 +385,9 @@ extern "C" int d3_decode_expert_gemm(int32_t mode, const uint8_t* w, const float
                "decode_expert_gemm: K=%d not in the compiled set", k);
   D3_SUPPORTED(n % tile_rows_for(kb) == 0, "decode_expert_gemm: N=%d must be a multiple of %d", n,
                tile_rows_for(kb));
-  // FC2 pairs weight tiles when experts average at most 8 routes at full
-  // capacity (beyond 16 routes an expert reloads its tiles).
-  const int tiles = n / tile_rows_for(kb);
-  const bool pair = mode == 2 && tiles % 2 == 0 && capacity * top_k <= 8 * num_experts;
   hipStream_t s = as_stream(stream);
-#define D3_DECODE(KB_, MODE_)                                                                   \
-  launch_decode<KB_, MODE_>(num_experts, n, pair, s, w, ws, ids, row_count, capacity, top_k, a, \
+#define D3_DECODE(KB_, MODE_)                                                                 \
+  launch_decode<KB_, MODE_>(num_experts, n, s, w, ws, ids, row_count, capacity, top_k, a,    \
                             a_scales, exact_routes, out_bf16, out_f32)
   if (mode == 0) {
     if (kb == 8) D3_DECODE(8, 0); else D3_DECODE(16, 0);

@@ -419,7 +419,7 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(
 // ---------------------------------------------------------------------------
 // Weighted combine: out[t] = bf16(sum_r w[t,r] * down[t*K + r]) in rank order.
 // ---------------------------------------------------------------------------
-// One workgroup per (row, 1024-column slice).  With top_k = 8 every load of
+// One workgroup per (row, 512-column slice).  With top_k = 8 every load of
 // the slice (8 route rows + 8 weights + the row count) is issued before the
 // first FMA.
 template <int kTopK>
@@ -445,9 +445,12 @@ __device__ __forceinline__ float4 combine4_fixed(const float* down, const void* 
   return acc;
 }
 
-constexpr int kCombineColumns = kRowThreads * 4;
+// 128 threads x 4 columns: a c2 decode step (52 rows x 2048 columns) spreads
+// over 208 workgroups, so most CUs have one row slice in flight.
+constexpr int kCombineThreads = 128;
+constexpr int kCombineColumns = kCombineThreads * 4;
 
-__global__ __launch_bounds__(kRowThreads) void weighted_combine_kernel(
+__global__ __launch_bounds__(kCombineThreads) void weighted_combine_kernel(
     const float* __restrict__ down, const void* __restrict__ weights, int weights_f32, int rows,
     int top_k, int hidden, const int32_t* __restrict__ row_count,
     const float* __restrict__ shared, uint16_t* __restrict__ out) {
@@ -773,7 +776,7 @@ extern "C" int d3_weighted_combine(const float* down, const void* weights, int32
     return D3_OK;
   }
   const int slices = (hidden + kCombineColumns - 1) / kCombineColumns;
-  hipLaunchKernelGGL(weighted_combine_kernel, dim3(rows * slices), dim3(kRowThreads), 0,
+  hipLaunchKernelGGL(weighted_combine_kernel, dim3(rows * slices), dim3(kCombineThreads), 0,
                      as_stream(stream),
                      down, weights, weights_dtype == D3_DTYPE_F32 ? 1 : 0, rows, top_k, hidden,
                      row_count, shared, out);

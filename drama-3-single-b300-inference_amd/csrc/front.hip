@@ -104,8 +104,8 @@ __global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
 
 // ---------------------------------------------------------------------------
 // Fused front end of one MoE step: slot compaction + routing + quantisation
-// (one row per workgroup: wave 0 routes it, the 4 waves quantise a quarter
-// each) and, in the last workgroup to finish, the route sort.  The last
+// (one slot / row per workgroup: wave 0 routes it, the 4 waves quantise a
+// quarter each) and, in the last workgroup to finish, the route sort.  The last
 // workgroup is found with an atomic ticket after the ids were published with
 // coherent stores; nobody waits, so the launch cannot deadlock, and the last
 // workgroup resets the ticket so the next launch (or graph replay) starts at 0.
@@ -145,26 +145,36 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
   __shared__ int ticket_shared;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
-  const int row = blockIdx.x;  // one row per workgroup; wave = part of the row
-
   int live;
-  int source = -1;
+  int row;
+  bool on;
+  RowPart xrow;
+  RouteLogits<NPL> logits;
   if (a.occupancy != nullptr) {
-    // Every wave scans the occupancy (a few ballots) to find the count and
-    // the slot of its row; workgroup 0 also writes the ascending slot list.
+    // One workgroup per slot: the slot's x row and logits are loaded first
+    // (wasted when the slot is free), then every wave counts the occupied
+    // slots with ballots: before this slot (= its row) and in total;
+    // workgroup 0 also writes the ascending slot list.
+    const int slot = blockIdx.x;
+    load_row_part(a.x + static_cast<int64_t>(slot) * a.x_stride, a.hidden, wave, xrow);
+    if (wave == 0)
+      load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
+                                       static_cast<int64_t>(slot) * a.logits_stride * (kF32 ? 4 : 2),
+                                   a.num_experts, logits);
     int running = 0;
+    row = 0;
+    on = false;
     for (int base = 0, chunk = 0; base < a.num_slots; base += kWave, ++chunk) {
-      const bool on = base + lane < a.num_slots && a.occupancy[base + lane] != 0;
-      const uint64_t mask = __ballot(on);
+      const bool occupied = base + lane < a.num_slots && a.occupancy[base + lane] != 0;
+      const uint64_t mask = __ballot(occupied);
       const int rank = __popcll(mask & lanemask_lt());
-      const int here = __popcll(mask);
-      if (row >= running && row < running + here) {
-        const uint64_t hit = __ballot(on && rank == row - running);
-        source = base + __ffsll(static_cast<unsigned long long>(hit)) - 1;
+      if (slot >= base && slot < base + kWave) {
+        row = running + __popcll(mask & (slot - base == 0 ? 0ull : (~0ull >> (kWave - (slot - base)))));
+        on = (mask >> (slot - base)) & 1ull;
       }
-      if (blockIdx.x == 0 && (chunk % (kFrontThreads / kWave)) == wave && on)
+      if (blockIdx.x == 0 && (chunk % (kFrontThreads / kWave)) == wave && occupied)
         a.active[running + rank] = base + lane;
-      running += here;
+      running += __popcll(mask);
     }
     live = running;
     if (blockIdx.x == 0) {
@@ -173,21 +183,24 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
       if (threadIdx.x == 0) *a.count = live;
     }
   } else {
+    row = blockIdx.x;  // one row per workgroup
     live = live_rows(a.row_count, a.rows);
-    if (row < live) source = a.row_index != nullptr ? a.row_index[row] : row;
+    on = row < live;
+    if (on) {
+      const int source = a.row_index != nullptr ? a.row_index[row] : row;
+      load_row_part(a.x + static_cast<int64_t>(source) * a.x_stride, a.hidden, wave, xrow);
+      if (wave == 0)
+        load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
+                                         static_cast<int64_t>(source) * a.logits_stride * (kF32 ? 4 : 2),
+                                     a.num_experts, logits);
+    }
   }
 
-  if (row < live) {
-    // Each wave loads its part of the x row first, so the transfer overlaps
-    // the routing (wave 0).
-    RowPart xrow;
-    load_row_part(a.x + static_cast<int64_t>(source) * a.x_stride, a.hidden, wave, xrow);
-    if (wave == 0) {
-      const char* lbase = static_cast<const char*>(a.logits) +
-                          static_cast<int64_t>(source) * a.logits_stride * (kF32 ? 4 : 2);
-      route_row<NPL, kF32, kSort>(lbase, a.num_experts, a.top_k, row, a.ids, nullptr, a.weights,
-                                  a.weights_f32);
-    }
+  if (on) {
+    // wave 0 routes the row while every wave quantises its part
+    if (wave == 0)
+      route_logits<NPL, kSort>(logits, a.num_experts, a.top_k, row, a.ids, nullptr, a.weights,
+                               a.weights_f32);
     quantize_row_part(xrow, a.hidden, wave, a.q + static_cast<int64_t>(row) * a.hidden,
                       a.scales + static_cast<int64_t>(row) * (a.hidden / kGroup), 1);
   }

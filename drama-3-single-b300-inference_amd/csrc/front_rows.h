@@ -30,13 +30,30 @@ __device__ __forceinline__ uint32_t route_key(float value, int column) {
   return (ordered & 0xffff0000u) | (65535u - static_cast<uint32_t>(column));
 }
 
-// Routes one row (one wave): top-k ids of the row at `base` (E <= 64 * NPL)
-// into ids[out_row * top_k + rank], weights likewise.
+// One row's logits, NPL per lane (column lane + 64 j; -inf past E).
+template <int NPL>
+struct RouteLogits {
+  float values[NPL];
+};
+
+template <int NPL, bool kF32>
+__device__ __forceinline__ void load_route_logits(const char* base, int num_experts,
+                                                  RouteLogits<NPL>& logits) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int column = lane + j * kWave;
+    logits.values[j] = column < num_experts ? load_logit<kF32>(base, column) : -INFINITY;
+  }
+}
+
+// Routes one row (one wave) from its loaded logits (E <= 64 * NPL): top-k
+// ids into ids[out_row * top_k + rank], weights likewise.
 // kPublish: ids and weights are read by other workgroups (coherent stores).
-template <int NPL, bool kF32, bool kPublish = false>
-__device__ __forceinline__ void route_row(const char* base, int num_experts, int top_k,
-                                          int64_t out_row, int32_t* ids32, int64_t* ids64,
-                                          void* weights, int weights_f32) {
+template <int NPL, bool kPublish = false>
+__device__ __forceinline__ void route_logits(const RouteLogits<NPL>& logits, int num_experts,
+                                             int top_k, int64_t out_row, int32_t* ids32,
+                                             int64_t* ids64, void* weights, int weights_f32) {
   const int lane = lane_id();
   float values[NPL];
   uint32_t keys[NPL];
@@ -44,12 +61,11 @@ __device__ __forceinline__ void route_row(const char* base, int num_experts, int
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     const int column = lane + j * kWave;
+    values[j] = logits.values[j];
     if (column < num_experts) {
-      values[j] = load_logit<kF32>(base, column);
       keys[j] = route_key(values[j], column);
       row_max = fmaxf(row_max, values[j]);
     } else {
-      values[j] = -INFINITY;
       keys[j] = 0u;  // below every valid key (65535 - column > 0)
     }
   }
@@ -105,6 +121,17 @@ __device__ __forceinline__ void route_row(const char* base, int num_experts, int
       static_cast<uint16_t*>(weights)[out] = f32_to_bf16(weight);
     }
   }
+}
+
+// Routes the row at `base`: load_route_logits + route_logits.
+template <int NPL, bool kF32, bool kPublish = false>
+__device__ __forceinline__ void route_row(const char* base, int num_experts, int top_k,
+                                          int64_t out_row, int32_t* ids32, int64_t* ids64,
+                                          void* weights, int weights_f32) {
+  RouteLogits<NPL> logits;
+  load_route_logits<NPL, kF32>(base, num_experts, logits);
+  route_logits<NPL, kPublish>(logits, num_experts, top_k, out_row, ids32, ids64, weights,
+                              weights_f32);
 }
 
 // ---------------------------------------------------------------------------
