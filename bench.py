@@ -33,7 +33,7 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 # this script (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors read off
 # the 1 GiB device copy in the same runs); profiles/expert_gemm_c2_hbm_traffic.md.
 # Re-measure whenever the FC1 kernel or its tiling changes.
-FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,0,6>", "bytes": 400085606}
+FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,1,6,1>", "bytes": 401299456}
 
 
 def parse():
@@ -176,7 +176,12 @@ def main():
                     fn(c)
         return g
 
-    if ws.sortless:  # the step's own expert kernels: sortless decode GEMMs
+    frontless = ws.sortless and ds.uses_frontless(occ, x_slots, logits_slots)
+    if frontless:  # the step's own expert kernels: FC1 from the slots, sortless FC2
+        fc1_graph = kernel_graph(lambda c: ws.decode_route_fc1(c, occ, x_slots, logits_slots,
+                                                               ds.active, ds.count))
+        fc2_graph = kernel_graph(lambda c: ws.decode_fc2(c, ds.count))
+    elif ws.sortless:  # sortless decode GEMMs after the front
         fc1_graph = kernel_graph(lambda c: ws.decode_fc1(c, ds.count))
         fc2_graph = kernel_graph(lambda c: ws.decode_fc2(c, ds.count))
     else:
@@ -188,8 +193,13 @@ def main():
     fc2_us = time_graphs(torch, [fc2_graph], 5) / launches
     h, i, e = w.hidden, w.intermediate, w.num_experts
     routes = rows * workloads.TOP_K
-    fc1_bytes = used * (2 * i * h + 4 * (2 * i // 128) * (h // 128)) + rows * h + rows * (h // 128) * 4 \
-        + routes * 2 * i * 2
+    fc1_weights = used * (2 * i * h + 4 * (2 * i // 128) * (h // 128))
+    if frontless:  # bf16 x rows, the slots' logits and occupancy in; gate_up, ids, slot list out
+        slots = workloads.SLOTS
+        fc1_bytes = fc1_weights + rows * h * 2 + slots * e * 2 + slots + routes * 2 * i * 2 \
+            + routes * 4 + slots * 4
+    else:  # fp8 q rows + scales in, gate_up out
+        fc1_bytes = fc1_weights + rows * h + rows * (h // 128) * 4 + routes * 2 * i * 2
     # FC2 reads its activations as fp8 codes + scales, or (SwiGLU in its
     # prologue) as FC1's bf16 gate|up rows.
     prologue = ws.sortless or ws.swiglu_in_fc2
@@ -249,6 +259,8 @@ def main():
                    "used_experts": used, "algorithmic_bytes_per_step": step_bytes,
                    "weight_copies": len(copies),
                    "step": ("one launch (d3_moe_decode_step)" if args.fused else
+                            "FC1 routing + quantising the slots itself, sortless FC2, routed "
+                            "combine (3 launches)" if frontless else
                             "front + sortless decode GEMMs + combine" if ws.sortless else
                             "front + sorted expert GEMMs + combine"),
                    "timing": "hipGraph of one step per weight copy (the copies act as consecutive "
@@ -256,7 +268,8 @@ def main():
         "hot": {"us_per_step": round(hot_us, 2),
                 "GB_s": round(step_bytes / hot_us / 1e3, 1)},
         "roofline": {"bound": "hbm",
-                     "kernel": "decode_expert_gemm FC1" if ws.sortless else "expert_gemm FC1",
+                     "kernel": ("decode_route_fc1" if frontless else
+                                "decode_expert_gemm FC1" if ws.sortless else "expert_gemm FC1"),
                      "achieved": round(fc1_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(fc1_gbs / HBM_PEAK_GBS, 4),
                      "traffic": FC1_TRAFFIC_BYTES["bytes"],

@@ -82,6 +82,20 @@ __device__ __forceinline__ uint32_t quantize_one(float x, float scale) {
   return f32_to_e4m3(v);
 }
 
+// quantize_one of four values, packed little-endian (v[0] in the low byte).
+// The conversion is v_cvt_pk_fp8_f32 (round to nearest even into OCP e4m3),
+// which gives f32_to_e4m3's byte for every input in [-448, 448] in every
+// byte position: checked on gfx950 over all 2^32 fp32 bit patterns after
+// the clamp.
+__device__ __forceinline__ uint32_t quantize_four(const float* v, float scale) {
+  float c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = fminf(fmaxf(v[i] / scale, -448.0f), 448.0f);
+  int word = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
+  word = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], word, true);
+  return static_cast<uint32_t>(word);
+}
+
 // ---------------------------------------------------------------------------
 // wave64 reductions on DPP lane moves (VALU operand modifiers, no LDS
 // round trip): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and

@@ -19,8 +19,18 @@
 // A workgroup whose expert receives no route exits after its first weight
 // loads (those bytes are wasted): the layout suits batches whose routes
 // cover most experts; sparse ones are better served by the sorted chain.
+//
+// The FC1 can also start from the slots themselves (MODE 1), which removes
+// the front launch: slot s routes to expert e at rank c when c, the number
+// of experts whose routing key beats e's in that row, is below top_k (the
+// keys are unique, so this is exactly the rank the front's top-k assigns),
+// and the workgroup quantises the x rows of its routes itself with the
+// front's per-128 rule.  The routing weights are then computed by the
+// combine (routed_combine_kernel) from the same logits with the front's
+// function, so every byte matches the chain that runs the front.
 #include "common.h"
 #include "expert_tile.h"
+#include "front_rows.h"
 #include "status.h"
 
 namespace d3 {
@@ -30,17 +40,67 @@ constexpr int kMaxSlots = 256;                        // rows per launch (one ro
 constexpr int kMaxIds = kMaxSlots * 8;                // ids read per workgroup (top_k <= 8)
 constexpr int kIdsPerThread = kMaxIds / kGemmThreads;  // 8
 
+struct DecodeArgs {
+  const uint8_t* w;  // fragment-major weights [E, n_rows, K]
+  const float* ws;   // block scales [E, n_rows / 128, K / 128]
+  int n_rows;
+  int capacity;  // slot rows
+  int top_k;
+  int exact_routes;
+  // MODE 0 / 2: routed ids of every row and the live row count (front output)
+  const int32_t* ids;
+  const int32_t* row_count;
+  // MODE 0: q rows and their scales; MODE 2: bf16 gate|up by pair
+  const void* act;
+  const float* act_scales;
+  // MODE 1: the slots (occupancy bytes, bf16 x rows, logits) and the
+  // front outputs this FC1 writes instead (ids by pair, count, slot list)
+  const uint8_t* occupancy;
+  const uint16_t* x;
+  int64_t x_stride;  // elements
+  const void* logits;
+  int logits_f32;
+  int64_t logits_stride;  // elements
+  int num_experts;
+  int32_t* ids_out;
+  int32_t* count_out;
+  int32_t* active_out;
+  uint16_t* out_bf16;  // MODE 0 / 1: gate|up [pairs, n_rows]
+  float* out_f32;      // MODE 2: down [pairs, n_rows]
+};
+
+constexpr int kPassSlots = kGemmThreads / 4;         // MODE 1: 4 lanes per slot
+constexpr int kMaxPasses = kMaxSlots / kPassSlots;  // 4: capacity 256
+constexpr int kLogitChunks = 8;                      // 16-byte logit loads per lane and pass
+
+// MODE 1 ranking: the logits of one pass of 64 slots (lane q of a slot's quad
+// holds 16-byte chunks q, q + 4, ...) and the slot's own logit of this expert.
+struct LogitPass {
+  int4 chunk[kLogitChunks];
+  uint32_t own;
+};
+
 // MODE 0: FC1, q rows of the routes' tokens x W13 -> bf16 gate|up by pair.
+// MODE 1: FC1 from the slots: routing ranks from the logits, x rows
+//         quantised while staged -> bf16 gate|up by pair, ids, count, slots.
 // MODE 2: FC2 with the SwiGLU requant in the prologue, gate|up by pair x W2
 //         -> fp32 down by pair.
 // TILES weight tiles per workgroup, streamed through the registers in halves
 // (TILES > 1: routes beyond the first 16 reload the weight tiles).
-template <int KB, int RT, int MODE, int TILES>
+// PASSES (MODE 1): ranking passes of 64 slots the kernel is built for.
+template <int KB, int RT, int MODE, int TILES, int PASSES = 1>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_gemm_kernel(
-    const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows,
-    const int32_t* __restrict__ ids, const int32_t* __restrict__ row_count, int capacity,
-    int top_k, const void* __restrict__ act, const float* __restrict__ act_scales,
-    int exact_routes, uint16_t* __restrict__ out_bf16, float* __restrict__ out_f32) {
+    DecodeArgs a) {
+  const uint8_t* __restrict__ w = a.w;
+  const float* __restrict__ ws = a.ws;
+  const int n_rows = a.n_rows;
+  const int capacity = a.capacity;
+  const int top_k = a.top_k;
+  const int exact_routes = a.exact_routes;
+  const void* __restrict__ act = a.act;
+  const float* __restrict__ act_scales = a.act_scales;
+  uint16_t* __restrict__ out_bf16 = a.out_bf16;
+  float* __restrict__ out_f32 = a.out_f32;
   constexpr int K = KB * kGroup;
   constexpr int kRowsPerWave = RT * 16;
   constexpr int kRowsPerGroup = kGemmWaves * kRowsPerWave;
@@ -51,6 +111,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   __shared__ float b_scales[16 * KB];
   __shared__ int b_target[16];  // pair of each route column, -1 = none
   __shared__ int route_pairs[kMaxSlots];
+  __shared__ int route_slots[MODE == 1 ? kMaxSlots : 1];
   __shared__ int chunk_counts[kIdsPerThread * kGemmWaves];
 
   const int tiles = n_rows / kRowsPerGroup;
@@ -82,46 +143,194 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       for (int kb = 0; kb < KB; ++kb) w_scale[rt][kb] = wsexp[((n0_of(tile) + rt * 16) / kGroup) * KB + kb];
   };
 
-  // 1. The routed ids of every slot row (past the capacity: zeros, masked
-  //    below), issued before any weight.
-  const uint32_t id_bytes = static_cast<uint32_t>(capacity * top_k) * 4;
-  const BufferView id_view(ids, id_bytes);
-  uint32_t id[kIdsPerThread];
+  int routes;
+  if constexpr (MODE == 1) {
+    // 1. Occupancy and the first 64 slots' logits, issued before any weight.
+    const int elem = a.logits_f32 ? 4 : 2;
+    const int chunk_columns = 16 / elem;
+    const BufferView logit_view(a.logits, static_cast<uint32_t>(capacity * a.logits_stride * elem));
+    const int q = threadIdx.x & 3;
+    auto load_pass = [&](int p, LogitPass& lp) {
+      const int s = p * kPassSlots + (static_cast<int>(threadIdx.x) >> 2);
+      const bool valid = s < capacity;
+      const uint32_t row_bytes = static_cast<uint32_t>(s * a.logits_stride * elem);
 #pragma unroll
-  for (int j = 0; j < kIdsPerThread; ++j) {
-    const uint32_t p = static_cast<uint32_t>(j * kGemmThreads + threadIdx.x);
-    id[j] = id_view.load4(p * 4 < id_bytes ? p * 4 : kNoRow);
-  }
-  const int rows = live_rows(row_count, capacity);
-  // 2. The first half of the first weight tile streams meanwhile.
-  load_weights(first_tile, 0, kFirstHalf);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 3. This expert's route list, in ascending pair order: pair p = j * 256 +
-  //    thread, so the order is (j, wave, lane).
-  const int pairs = rows * top_k;
-  uint64_t hits[kIdsPerThread];
+      for (int i = 0; i < kLogitChunks; ++i) {
+        const int column = (i * 4 + q) * chunk_columns;
+        lp.chunk[i] = logit_view.load16(valid && column < a.num_experts
+                                            ? row_bytes + static_cast<uint32_t>(column * elem)
+                                            : kNoRow);
+      }
+      // the dword holding this expert's logit (a bf16 logit is one half of it)
+      lp.own = logit_view.load4(valid ? ((row_bytes + static_cast<uint32_t>(expert * elem)) & ~3u) : kNoRow);
+    };
+    const BufferView occupancy_view(a.occupancy, static_cast<uint32_t>(capacity));
+    uint32_t occupied_bits[PASSES];
 #pragma unroll
-  for (int j = 0; j < kIdsPerThread; ++j) {
-    const int p = j * kGemmThreads + static_cast<int>(threadIdx.x);
-    hits[j] = __ballot(p < pairs && static_cast<int>(id[j]) == expert);
-    if (lane == 0) chunk_counts[j * kGemmWaves + wave] = __popcll(hits[j]);
-  }
-  __syncthreads();
-  int chunk_base = 0;  // routes in chunks before chunk j
-#pragma unroll
-  for (int j = 0; j < kIdsPerThread; ++j) {
-    int base = chunk_base;  // + blocks of earlier waves in chunk j
-#pragma unroll
-    for (int w2 = 0; w2 < kGemmWaves; ++w2) {
-      const int c = chunk_counts[j * kGemmWaves + w2];
-      base += w2 < wave ? c : 0;
-      chunk_base += c;
+    for (int p = 0; p < PASSES; ++p) {
+      const int s = p * kWave + lane;
+      occupied_bits[p] = occupancy_view.load1(s < capacity ? static_cast<uint32_t>(s) : kNoRow);
     }
-    if ((hits[j] >> lane) & 1ull)
-      route_pairs[base + __popcll(hits[j] & lanemask_lt())] = j * kGemmThreads + threadIdx.x;
+    LogitPass lp;
+    load_pass(0, lp);
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. The first half of the first weight tile streams meanwhile.
+    load_weights(first_tile, 0, kFirstHalf);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. Occupied slots (every wave holds the masks) and this expert's rank
+    //    in every live slot: the keys above its key, summed over the quad.
+    uint64_t occ_mask[PASSES];
+    int occ_base[PASSES];
+    int live = 0;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      occ_mask[p] = __ballot(occupied_bits[p] != 0u);
+      occ_base[p] = live;
+      live += __popcll(occ_mask[p]);
+    }
+    const uint32_t own_key_column = static_cast<uint32_t>(expert);
+    uint64_t hits[PASSES];
+    int my_pair[PASSES];
+    auto rank_pass = [&](int p, const LogitPass& lp2) {
+      const int bit = static_cast<int>(threadIdx.x) >> 2;  // slot - 64 p
+      const int s = p * kPassSlots + bit;
+      const uint32_t own_bits = elem == 4 ? lp2.own
+                                : (((expert * 2) & 2) ? (lp2.own & 0xffff0000u) : (lp2.own << 16));
+      const uint32_t own_key = route_key(__uint_as_float(own_bits), static_cast<int>(own_key_column));
+      // Keys of columns past E must rank below every valid key: their bits
+      // are set to all ones (ordered value 0; the column is above e, so
+      // the tie-break field is below e's too).  Only the last chunk row can
+      // hold such columns, and only when E is not a multiple of its width.
+      const int row_columns = 4 * chunk_columns;
+      const int chunks = (a.num_experts + row_columns - 1) / row_columns;  // uniform
+      const bool ragged = a.num_experts % row_columns != 0;
+      uint32_t above = 0;
+#pragma unroll
+      for (int i = 0; i < kLogitChunks; ++i) {
+        if (i >= chunks) break;  // uniform
+        uint32_t words[4] = {static_cast<uint32_t>(lp2.chunk[i].x), static_cast<uint32_t>(lp2.chunk[i].y),
+                             static_cast<uint32_t>(lp2.chunk[i].z), static_cast<uint32_t>(lp2.chunk[i].w)};
+        const int column0 = (i * 4 + q) * chunk_columns;
+        if (ragged && i == chunks - 1) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (a.logits_f32) {
+              words[k] |= column0 + k < a.num_experts ? 0u : 0xffffffffu;
+            } else {
+              words[k] |= column0 + 2 * k < a.num_experts ? 0u : 0x0000ffffu;
+              words[k] |= column0 + 2 * k + 1 < a.num_experts ? 0u : 0xffff0000u;
+            }
+          }
+        }
+        const uint32_t tie0 = 65535u - static_cast<uint32_t>(column0);
+        if (a.logits_f32) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) above += key_of_bits(words[c], tie0 - c) > own_key ? 1u : 0u;
+        } else {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const uint32_t bits = (c & 1) ? (words[c >> 1] & 0xffff0000u) : (words[c >> 1] << 16);
+            above += key_of_bits(bits, tie0 - c) > own_key ? 1u : 0u;
+          }
+        }
+      }
+      above += dpp_move<kDppQuad1032>(above, 0u);
+      above += dpp_move<kDppQuad2301>(above, 0u);
+      const uint64_t mask = occ_mask[p];
+      const bool occupied = s < capacity && ((mask >> bit) & 1ull);
+      const int row = occ_base[p] + __popcll(mask & ((1ull << bit) - 1ull));
+      const bool routed = occupied && static_cast<int>(above) < top_k;
+      hits[p] = __ballot(q == 0 && routed);
+      my_pair[p] = row * top_k + static_cast<int>(above);
+      if (q == 0 && routed && first_tile == 0) a.ids_out[my_pair[p]] = expert;
+    };
+    rank_pass(0, lp);
+#pragma unroll
+    for (int p = 1; p < PASSES; ++p) {
+      hits[p] = 0ull;
+      my_pair[p] = 0;
+      if (p * kPassSlots < capacity) {
+        load_pass(p, lp);
+        rank_pass(p, lp);
+      }
+    }
+    // The slot list and the live count (one workgroup writes them).
+    if (blockIdx.x == 0) {
+      if (wave == 0) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+          if ((occ_mask[p] >> lane) & 1ull)
+            a.active_out[occ_base[p] + __popcll(occ_mask[p] & lanemask_lt())] = p * kWave + lane;
+      }
+      for (int i = live + static_cast<int>(threadIdx.x); i < capacity; i += kGemmThreads) a.active_out[i] = -1;
+      if (threadIdx.x == 0) *a.count_out = live;
+    }
+    // 4. The route list in slot order (= ascending pair order).
+    if (lane == 0) {
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) chunk_counts[p * kGemmWaves + wave] = __popcll(hits[p]);
+    }
+    __syncthreads();
+    int chunk_base = 0;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      int base = chunk_base;
+#pragma unroll
+      for (int w2 = 0; w2 < kGemmWaves; ++w2) {
+        const int c = chunk_counts[p * kGemmWaves + w2];
+        base += w2 < wave ? c : 0;
+        chunk_base += c;
+      }
+      if ((hits[p] >> lane) & 1ull) {
+        const int r = base + __popcll(hits[p] & lanemask_lt());
+        route_pairs[r] = my_pair[p];
+        route_slots[r] = p * kPassSlots + (static_cast<int>(threadIdx.x) >> 2);
+      }
+    }
+    routes = chunk_base;
+  } else {
+    // 1. The routed ids of every slot row (past the capacity: zeros, masked
+    //    below), issued before any weight.
+    const uint32_t id_bytes = static_cast<uint32_t>(capacity * top_k) * 4;
+    const BufferView id_view(a.ids, id_bytes);
+    uint32_t id[kIdsPerThread];
+#pragma unroll
+    for (int j = 0; j < kIdsPerThread; ++j) {
+      const uint32_t p = static_cast<uint32_t>(j * kGemmThreads + threadIdx.x);
+      id[j] = id_view.load4(p * 4 < id_bytes ? p * 4 : kNoRow);
+    }
+    const int rows = live_rows(a.row_count, capacity);
+    // 2. The first half of the first weight tile streams meanwhile.
+    load_weights(first_tile, 0, kFirstHalf);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. This expert's route list, in ascending pair order: pair p = j * 256 +
+    //    thread, so the order is (j, wave, lane).
+    const int pairs = rows * top_k;
+    uint64_t hits[kIdsPerThread];
+#pragma unroll
+    for (int j = 0; j < kIdsPerThread; ++j) {
+      const int p = j * kGemmThreads + static_cast<int>(threadIdx.x);
+      hits[j] = __ballot(p < pairs && static_cast<int>(id[j]) == expert);
+      if (lane == 0) chunk_counts[j * kGemmWaves + wave] = __popcll(hits[j]);
+    }
+    __syncthreads();
+    int chunk_base = 0;  // routes in chunks before chunk j
+#pragma unroll
+    for (int j = 0; j < kIdsPerThread; ++j) {
+      int base = chunk_base;  // + blocks of earlier waves in chunk j
+#pragma unroll
+      for (int w2 = 0; w2 < kGemmWaves; ++w2) {
+        const int c = chunk_counts[j * kGemmWaves + w2];
+        base += w2 < wave ? c : 0;
+        chunk_base += c;
+      }
+      if ((hits[j] >> lane) & 1ull)
+        route_pairs[base + __popcll(hits[j] & lanemask_lt())] = j * kGemmThreads + threadIdx.x;
+    }
+    routes = chunk_base;
   }
-  int routes = chunk_base;
   __syncthreads();
   routes = __builtin_amdgcn_readfirstlane(routes);
   if (routes == 0) return;  // no route for this expert: the loads issued so far are dropped
@@ -133,14 +342,84 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   int4 b_stage[MODE == 0 ? kChunks : 1];
   float b_stage_scale = 0.0f;
   int stage_pair = -1;
+  // MODE 1: live (route column, 128-group) units packed densely as in MODE
+  // 2; a unit's 16 threads hold 8 bf16 each (the front's quantisation
+  // layout), so only live units are quantised.
+  constexpr int kStageUnits = MODE == 1 ? (KB < 8 ? KB : 8) : 1;  // unit rows staged at once
+  uint4 x_stage[kStageUnits];
   // MODE 2: live (route column, K group) units packed densely: unit
   // u = 16 p + stage_col is column u / KB, group u % KB.
   uint4 g_stage[MODE == 2 ? KB : 1], u_stage[MODE == 2 ? KB : 1];
   int live_units = 0;
+  // MODE 1: unit rows [base, base + kStageUnits) of route tile stage_m0.
+  int stage_m0 = 0;
+  auto fetch_units = [&](int base) {
+    if constexpr (MODE == 1) {
+      const BufferView x_view(a.x, static_cast<uint32_t>(capacity * a.x_stride * 2));
+#pragma unroll
+      for (int i = 0; i < kStageUnits; ++i) {
+        const int u = (base + i) * 16 + stage_col;
+        const int col = u / KB;
+        const bool live = u < live_units;
+        const int slot = route_slots[min(stage_m0 + col, routes - 1)];
+        const uint32_t offset =
+            live ? static_cast<uint32_t>(slot * a.x_stride * 2 + ((u - col * KB) * kGroup + stage_part * 8) * 2)
+                 : kNoRow;
+        const int4 v = x_view.load16(offset);
+        x_stage[i] = make_uint4(v.x, v.y, v.z, v.w);
+      }
+    }
+  };
+  // Per-128 e4m3 quantisation of the staged units: the arithmetic and lane
+  // layout of quantize_row_part, so the tile holds the front's q bytes and
+  // scales.
+  auto quantize_units = [&](int base) {
+    if constexpr (MODE == 1) {
+#pragma unroll
+      for (int i = 0; i < kStageUnits; ++i) {
+        if ((base + i) * 16 >= live_units) break;  // uniform
+        const int u = (base + i) * 16 + stage_col;
+        const int col = u / KB;
+        const int j = u - col * KB;
+        const uint32_t words[4] = {x_stage[i].x, x_stage[i].y, x_stage[i].z, x_stage[i].w};
+        float v[8];
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[2 * e] = __uint_as_float(words[e] << 16);
+          v[2 * e + 1] = __uint_as_float(words[e] & 0xffff0000u);
+          amax = fmaxf(amax, fmaxf(fabsf(v[2 * e]), fabsf(v[2 * e + 1])));
+        }
+        amax = segment_max<16>(amax);
+        const float scale = group_scale(amax);
+        const uint32_t lo = quantize_four(v, scale);
+        const uint32_t hi = quantize_four(v + 4, scale);
+        if (u < live_units) {
+          *reinterpret_cast<uint2*>(b_tile + col * kStride + j * kGroup + stage_part * 8) = make_uint2(lo, hi);
+          if (stage_part == 0) b_scales[col * KB + j] = scale;
+        }
+      }
+    }
+  };
+  // MODE 1: the unit rows beyond the first kStageUnits (route tiles with
+  // more than 128 / KB routes), staged and quantised after the rest.
+  auto stage_rest = [&]() {
+    if constexpr (MODE == 1 && kStageUnits < KB) {
+      for (int base = kStageUnits; base < KB; base += kStageUnits) {
+        if (base * 16 >= live_units) break;  // uniform
+        fetch_units(base);
+        quantize_units(base);
+      }
+    }
+  };
   auto fetch_tile = [&](int m0) {
     const int r = m0 + stage_col;
     stage_pair = r < routes ? route_pairs[r] : -1;
-    if constexpr (MODE == 0) {
+    if constexpr (MODE == 1) {
+      live_units = min(16, routes - m0) * KB;
+      stage_m0 = m0;
+      fetch_units(0);
+    } else if constexpr (MODE == 0) {
       const BufferView rows_view(act, static_cast<uint32_t>(capacity) * K);
       const BufferView scale_view(act_scales, static_cast<uint32_t>(capacity) * KB * 4);
       const int token = stage_pair / top_k;
@@ -183,6 +462,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
           if (stage_part == 0) b_scales[col * KB + kb] = scale;
         }
       }
+    } else if constexpr (MODE == 1) {
+      quantize_units(0);
+      stage_rest();
     } else {
 #pragma unroll
       for (int j = 0; j < kChunks; ++j)
@@ -234,7 +516,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int n = n0_of(tile) + rt * 16 + group * 4;  // rows n..n+3 of this column
-      if constexpr (MODE == 0) {
+      if constexpr (MODE != 2) {
         const uint32_t lo = f32_to_bf16(acc[rt][0]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][1])) << 16);
         const uint32_t hi = f32_to_bf16(acc[rt][2]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][3])) << 16);
         *reinterpret_cast<uint2*>(out_bf16 + static_cast<size_t>(target) * n_rows + n) = make_uint2(lo, hi);
@@ -311,14 +593,16 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
 template <int KB, int MODE, int TILES>
-void launch_tiles(int num_experts, int n, hipStream_t s, const uint8_t* w, const float* ws,
-                  const int32_t* ids, const int32_t* row_count, int capacity, int top_k,
-                  const void* a, const float* as, int exact_routes, uint16_t* out_bf16,
-                  float* out_f32) {
-  const int tiles = n / tile_rows_for(KB);
-  hipLaunchKernelGGL((decode_gemm_kernel<KB, rt_for(KB), MODE, TILES>),
-                     dim3(num_experts * (tiles / TILES)), dim3(kGemmThreads), 0, s, w, ws, n, ids,
-                     row_count, capacity, top_k, a, as, exact_routes, out_bf16, out_f32);
+void launch_tiles(int num_experts, hipStream_t s, const DecodeArgs& a) {
+  const int tiles = a.n_rows / tile_rows_for(KB);
+  const dim3 grid(num_experts * (tiles / TILES)), block(kGemmThreads);
+  if constexpr (MODE == 1) {
+    if (a.capacity > kPassSlots) {
+      hipLaunchKernelGGL((decode_gemm_kernel<KB, rt_for(KB), MODE, TILES, kMaxPasses>), grid, block, 0, s, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((decode_gemm_kernel<KB, rt_for(KB), MODE, TILES, 1>), grid, block, 0, s, a);
 }
 
 // Weight tiles per workgroup: enough that the whole grid is about one round
@@ -331,7 +615,7 @@ constexpr int kResidentGroups = 512;
 int tiles_per_group(int num_experts, int tiles, int capacity, int top_k, int mode) {
   if (capacity * top_k > 8 * num_experts) return 1;
   const int options[] = {1, 2, 4, 6};
-  const int limit = mode == 0 ? 6 : 4;
+  const int limit = mode != 2 ? 6 : 4;
   for (int t : options)
     if (t <= limit && tiles % t == 0 && num_experts * (tiles / t) <= kResidentGroups) return t;
   for (int i = 3; i >= 0; --i)
@@ -340,22 +624,112 @@ int tiles_per_group(int num_experts, int tiles, int capacity, int top_k, int mod
 }
 
 template <int KB, int MODE>
-void launch_decode(int num_experts, int n, hipStream_t s, const uint8_t* w, const float* ws,
-                   const int32_t* ids, const int32_t* row_count, int capacity, int top_k,
-                   const void* a, const float* as, int exact_routes, uint16_t* out_bf16,
-                   float* out_f32) {
-  const int tiles = n / tile_rows_for(KB);
-  const int t = tiles_per_group(num_experts, tiles, capacity, top_k, MODE);
-#define D3_TILES(T)                                                                             \
-  launch_tiles<KB, MODE, T>(num_experts, n, s, w, ws, ids, row_count, capacity, top_k, a, as, \
-                            exact_routes, out_bf16, out_f32)
-  if constexpr (MODE == 0) {
-    if (t == 6) { D3_TILES(6); return; }
+void launch_decode(int num_experts, hipStream_t s, const DecodeArgs& a) {
+  const int tiles = a.n_rows / tile_rows_for(KB);
+  const int t = tiles_per_group(num_experts, tiles, a.capacity, a.top_k, MODE);
+  if constexpr (MODE != 2) {
+    if (t == 6) {
+      launch_tiles<KB, MODE, 6>(num_experts, s, a);
+      return;
+    }
   }
-  if (t == 4) D3_TILES(4);
-  else if (t == 2) D3_TILES(2);
-  else D3_TILES(1);
-#undef D3_TILES
+  if (t == 4)
+    launch_tiles<KB, MODE, 4>(num_experts, s, a);
+  else if (t == 2)
+    launch_tiles<KB, MODE, 2>(num_experts, s, a);
+  else
+    launch_tiles<KB, MODE, 1>(num_experts, s, a);
+}
+
+// ---------------------------------------------------------------------------
+// Weighted combine of the step whose FC1 routed the slots itself: one
+// workgroup per (slot, 512-column slice).  The down rows of the slot's
+// routes are loaded first; meanwhile wave 0 recomputes the slot's top-k
+// weights from its logits with the front's function (route_top_k) and
+// rounds them to the stored dtype, so the sum is the chain combine's
+// (one fused multiply-add per rank, in rank order).  Slice 0 also stores
+// the weights, as the front would.
+// ---------------------------------------------------------------------------
+constexpr int kRoutedCombineThreads = 128;
+constexpr int kRoutedCombineColumns = kRoutedCombineThreads * 4;
+
+struct RoutedCombineArgs {
+  const uint8_t* occupancy;
+  int capacity;
+  const void* logits;
+  int64_t logits_stride;  // elements
+  int num_experts;
+  int top_k;
+  int hidden;
+  const float* down;  // [pairs, hidden] by pair
+  void* weights;      // [capacity, top_k] by row, bf16 or f32
+  int weights_f32;
+  uint16_t* out;  // [capacity, hidden] by row
+};
+
+template <int NPL, bool kF32>
+__global__ __launch_bounds__(kRoutedCombineThreads) void routed_combine_kernel(RoutedCombineArgs a) {
+  __shared__ float route_w[8];
+  const int slices = (a.hidden + kRoutedCombineColumns - 1) / kRoutedCombineColumns;
+  const int slot = blockIdx.x / slices;
+  const int slice = blockIdx.x % slices;
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  // The slot's row: occupied slots below it (every wave counts them).
+  int row = 0;
+  bool on = false;
+  for (int base = 0; base < a.capacity; base += kWave) {
+    const bool occupied = base + lane < a.capacity && a.occupancy[base + lane] != 0;
+    const uint64_t mask = __ballot(occupied);
+    if (slot >= base && slot < base + kWave) {
+      const int bit = slot - base;
+      row += __popcll(mask & ((1ull << bit) - 1ull));
+      on = (mask >> bit) & 1ull;
+    } else if (slot >= base + kWave) {
+      row += __popcll(mask);
+    }
+  }
+  if (!on) return;  // uniform over the workgroup
+  RouteLogits<NPL> logits;
+  if (wave == 0)
+    load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
+                                     static_cast<int64_t>(slot) * a.logits_stride * (kF32 ? 4 : 2),
+                                 a.num_experts, logits);
+  const int column = slice * kRoutedCombineColumns + static_cast<int>(threadIdx.x) * 4;
+  const bool inside = column < a.hidden;
+  float4 y[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    y[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (inside && r < a.top_k)
+      y[r] = *reinterpret_cast<const float4*>(a.down + (static_cast<size_t>(row) * a.top_k + r) * a.hidden + column);
+  }
+  if (wave == 0) {
+    const RouteChoice choice = route_top_k<NPL>(logits, a.num_experts, a.top_k);
+    if (lane < a.top_k) {
+      route_w[lane] = stored_weight(choice.weight, a.weights_f32);
+      if (slice == 0) {
+        const size_t index = static_cast<size_t>(row) * a.top_k + lane;
+        if (a.weights_f32)
+          static_cast<float*>(a.weights)[index] = choice.weight;
+        else
+          static_cast<uint16_t*>(a.weights)[index] = f32_to_bf16(choice.weight);
+      }
+    }
+  }
+  __syncthreads();
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    if (r < a.top_k) {
+      const float wr = route_w[r];
+      acc.x = fmaf(wr, y[r].x, acc.x);
+      acc.y = fmaf(wr, y[r].y, acc.y);
+      acc.z = fmaf(wr, y[r].z, acc.z);
+      acc.w = fmaf(wr, y[r].w, acc.w);
+    }
+  }
+  if (inside) *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(row) * a.hidden + column) = pack_bf16x4(acc);
 }
 
 }  // namespace
@@ -385,15 +759,123 @@ extern "C" int d3_decode_expert_gemm(int32_t mode, const uint8_t* w, const float
                "decode_expert_gemm: K=%d not in the compiled set", k);
   D3_SUPPORTED(n % tile_rows_for(kb) == 0, "decode_expert_gemm: N=%d must be a multiple of %d", n,
                tile_rows_for(kb));
+  DecodeArgs args{};
+  args.w = w;
+  args.ws = ws;
+  args.n_rows = n;
+  args.capacity = capacity;
+  args.top_k = top_k;
+  args.exact_routes = exact_routes;
+  args.ids = ids;
+  args.row_count = row_count;
+  args.act = a;
+  args.act_scales = a_scales;
+  args.out_bf16 = out_bf16;
+  args.out_f32 = out_f32;
   hipStream_t s = as_stream(stream);
-#define D3_DECODE(KB_, MODE_)                                                                 \
-  launch_decode<KB_, MODE_>(num_experts, n, s, w, ws, ids, row_count, capacity, top_k, a,    \
-                            a_scales, exact_routes, out_bf16, out_f32)
   if (mode == 0) {
-    if (kb == 8) D3_DECODE(8, 0); else D3_DECODE(16, 0);
+    if (kb == 8) launch_decode<8, 0>(num_experts, s, args);
+    else launch_decode<16, 0>(num_experts, s, args);
   } else {
-    if (kb == 2) D3_DECODE(2, 2); else if (kb == 4) D3_DECODE(4, 2); else if (kb == 6) D3_DECODE(6, 2); else D3_DECODE(8, 2);
+    if (kb == 2) launch_decode<2, 2>(num_experts, s, args);
+    else if (kb == 4) launch_decode<4, 2>(num_experts, s, args);
+    else if (kb == 6) launch_decode<6, 2>(num_experts, s, args);
+    else launch_decode<8, 2>(num_experts, s, args);
   }
-#undef D3_DECODE
   D3_LAUNCHED("decode_expert_gemm");
+}
+
+extern "C" int d3_decode_route_fc1(const uint8_t* w, const float* ws, int32_t num_experts,
+                                   int32_t n, int32_t k, const uint8_t* occupancy,
+                                   int32_t capacity, const uint16_t* x, int64_t x_stride,
+                                   const void* logits, int32_t logits_dtype,
+                                   int64_t logits_stride, int32_t top_k, int32_t exact_routes,
+                                   int32_t* ids, int32_t* count, int32_t* active,
+                                   uint16_t* gate_up, void* stream) {
+  D3_REQUIRE(w && ws && occupancy && x && logits && ids && count && active && gate_up,
+             "decode_route_fc1: null pointer");
+  D3_REQUIRE(logits_dtype == D3_DTYPE_BF16 || logits_dtype == D3_DTYPE_F32,
+             "decode_route_fc1: logits must be bf16 or f32");
+  D3_REQUIRE(num_experts >= 1 && top_k >= 1 && top_k <= num_experts && n > 0 && k > 0 &&
+                 n % kGroup == 0 && k % 256 == 0,
+             "decode_route_fc1: bad shape (E=%d, top_k=%d, N=%d, K=%d)", num_experts, top_k, n, k);
+  const bool f32 = logits_dtype == D3_DTYPE_F32;
+  D3_SUPPORTED(capacity >= 1 && capacity <= kMaxSlots && top_k <= 8,
+               "decode_route_fc1: capacity %d (<= %d) x top_k %d (<= 8)", capacity, kMaxSlots, top_k);
+  D3_SUPPORTED(num_experts <= kLogitChunks * 4 * (f32 ? 4 : 8),
+               "decode_route_fc1: E=%d above the %d a workgroup ranks", num_experts,
+               kLogitChunks * 4 * (f32 ? 4 : 8));
+  D3_REQUIRE(x_stride >= k && logits_stride >= num_experts, "decode_route_fc1: row strides");
+  D3_SUPPORTED(aligned(logits, 16) && logits_stride % (f32 ? 4 : 8) == 0 && aligned(x, 16) &&
+                   x_stride % 8 == 0,
+               "decode_route_fc1: logits / x rows must be 16-byte aligned");
+  D3_SUPPORTED(static_cast<int64_t>(capacity) * x_stride * 2 < (int64_t{1} << 31) &&
+                   static_cast<int64_t>(capacity) * logits_stride * 4 < (int64_t{1} << 31),
+               "decode_route_fc1: slot rows above 2 GiB");
+  D3_REQUIRE(aligned(w, 16) && aligned(gate_up, 8), "decode_route_fc1: alignment");
+  const int kb = k / kGroup;
+  D3_SUPPORTED(kb == 8 || kb == 16, "decode_route_fc1: K=%d not in the compiled set", k);
+  D3_SUPPORTED(n % tile_rows_for(kb) == 0, "decode_route_fc1: N=%d must be a multiple of %d", n,
+               tile_rows_for(kb));
+  DecodeArgs args{};
+  args.w = w;
+  args.ws = ws;
+  args.n_rows = n;
+  args.capacity = capacity;
+  args.top_k = top_k;
+  args.exact_routes = exact_routes;
+  args.occupancy = occupancy;
+  args.x = x;
+  args.x_stride = x_stride;
+  args.logits = logits;
+  args.logits_f32 = f32 ? 1 : 0;
+  args.logits_stride = logits_stride;
+  args.num_experts = num_experts;
+  args.ids_out = ids;
+  args.count_out = count;
+  args.active_out = active;
+  args.out_bf16 = gate_up;
+  hipStream_t s = as_stream(stream);
+  if (kb == 8) launch_decode<8, 1>(num_experts, s, args);
+  else launch_decode<16, 1>(num_experts, s, args);
+  D3_LAUNCHED("decode_route_fc1");
+}
+
+extern "C" int d3_decode_route_combine(const uint8_t* occupancy, int32_t capacity,
+                                       const void* logits, int32_t logits_dtype,
+                                       int64_t logits_stride, int32_t num_experts, int32_t top_k,
+                                       int32_t hidden, const float* down, void* weights,
+                                       int32_t weights_dtype, uint16_t* out, void* stream) {
+  D3_REQUIRE(occupancy && logits && down && weights && out, "decode_route_combine: null pointer");
+  D3_REQUIRE(logits_dtype == D3_DTYPE_BF16 || logits_dtype == D3_DTYPE_F32,
+             "decode_route_combine: logits must be bf16 or f32");
+  D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
+             "decode_route_combine: weights must be bf16 or f32");
+  D3_REQUIRE(num_experts >= 1 && top_k >= 1 && top_k <= num_experts && hidden > 0 &&
+                 hidden % 4 == 0 && logits_stride >= num_experts,
+             "decode_route_combine: bad shape");
+  D3_SUPPORTED(capacity >= 1 && capacity <= kMaxSlots && top_k <= 8 && num_experts <= 256,
+               "decode_route_combine: capacity %d (<= %d), top_k %d (<= 8), E %d (<= 256)",
+               capacity, kMaxSlots, top_k, num_experts);
+  D3_REQUIRE(aligned(down, 16) && aligned(out, 8), "decode_route_combine: alignment");
+  RoutedCombineArgs args{occupancy, capacity, logits, logits_stride, num_experts, top_k,
+                         hidden, down, weights, weights_dtype == D3_DTYPE_F32 ? 1 : 0, out};
+  const int slices = (hidden + kRoutedCombineColumns - 1) / kRoutedCombineColumns;
+  const dim3 grid(capacity * slices), block(kRoutedCombineThreads);
+  hipStream_t s = as_stream(stream);
+  const bool f32 = logits_dtype == D3_DTYPE_F32;
+#define D3_COMBINE(NPL)                                                            \
+  if (f32)                                                                         \
+    hipLaunchKernelGGL((routed_combine_kernel<NPL, true>), grid, block, 0, s, args); \
+  else                                                                             \
+    hipLaunchKernelGGL((routed_combine_kernel<NPL, false>), grid, block, 0, s, args);
+  if (num_experts <= 64) {
+    D3_COMBINE(1)
+  } else if (num_experts <= 128) {
+    D3_COMBINE(2)
+  } else {
+    D3_COMBINE(4)
+  }
+#undef D3_COMBINE
+  D3_LAUNCHED("decode_route_combine");
 }

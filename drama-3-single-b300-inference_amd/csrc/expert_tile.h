@@ -46,6 +46,9 @@ struct BufferView {
   __device__ uint32_t load4(uint32_t offset) const {
     return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rsrc, offset, 0, kPolicy));
   }
+  __device__ uint32_t load1(uint32_t offset) const {
+    return static_cast<uint32_t>(static_cast<uint8_t>(__builtin_amdgcn_raw_buffer_load_b8(rsrc, offset, 0, 0)));
+  }
 };
 
 // Fragment of one row in the reference layout [N, K] (row = this lane's row).
@@ -127,12 +130,8 @@ __device__ __forceinline__ float swiglu_quant_group(uint4 graw, uint4 uraw, uint
   }
   amax = segment_max<16>(amax);
   const float scale = group_scale(amax);
-  uint32_t lo = 0u, hi = 0u;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    lo |= quantize_one(v[i], scale) << (8 * i);
-    hi |= quantize_one(v[i + 4], scale) << (8 * i);
-  }
+  const uint32_t lo = quantize_four(v, scale);
+  const uint32_t hi = quantize_four(v + 4, scale);
   *codes = make_uint2(lo, hi);
   return scale;
 }

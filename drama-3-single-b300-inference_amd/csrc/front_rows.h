@@ -30,6 +30,13 @@ __device__ __forceinline__ uint32_t route_key(float value, int column) {
   return (ordered & 0xffff0000u) | (65535u - static_cast<uint32_t>(column));
 }
 
+// route_key from the logit's fp32 bits (a bf16 logit: its bits in the high
+// half) and the tie-break field tie = 65535 - column.
+__device__ __forceinline__ uint32_t key_of_bits(uint32_t bits, uint32_t tie) {
+  const uint32_t ordered = bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+  return (ordered & 0xffff0000u) | tie;
+}
+
 // One row's logits, NPL per lane (column lane + 64 j; -inf past E).
 template <int NPL>
 struct RouteLogits {
@@ -47,13 +54,17 @@ __device__ __forceinline__ void load_route_logits(const char* base, int num_expe
   }
 }
 
-// Routes one row (one wave) from its loaded logits (E <= 64 * NPL): top-k
-// ids into ids[out_row * top_k + rank], weights likewise.
-// kPublish: ids and weights are read by other workgroups (coherent stores).
-template <int NPL, bool kPublish = false>
-__device__ __forceinline__ void route_logits(const RouteLogits<NPL>& logits, int num_experts,
-                                             int top_k, int64_t out_row, int32_t* ids32,
-                                             int64_t* ids64, void* weights, int weights_f32) {
+// Top-k of one row (one wave) from its loaded logits (E <= 64 * NPL): lane
+// k < top_k gets the rank-k expert and its normalised weight (fp32, before
+// any rounding to the stored dtype); other lanes get -1 and 0.
+struct RouteChoice {
+  int expert;
+  float weight;
+};
+
+template <int NPL>
+__device__ __forceinline__ RouteChoice route_top_k(const RouteLogits<NPL>& logits, int num_experts,
+                                                   int top_k) {
   const int lane = lane_id();
   float values[NPL];
   uint32_t keys[NPL];
@@ -100,9 +111,27 @@ __device__ __forceinline__ void route_logits(const RouteLogits<NPL>& logits, int
   float probability = 0.0f;
   if (lane < top_k) probability = expf(selected_value - row_max) / denominator;
   const float total = segment_sum<kWave>(probability);
+  return {selected, lane < top_k ? probability / total : 0.0f};
+}
+
+// The weight as read back from the stored dtype (bf16 rounding or fp32).
+__device__ __forceinline__ float stored_weight(float weight, int weights_f32) {
+  return weights_f32 ? weight : bf16_to_f32(f32_to_bf16(weight));
+}
+
+// Routes one row (one wave) from its loaded logits: top-k ids into
+// ids[out_row * top_k + rank], weights likewise.
+// kPublish: ids and weights are read by other workgroups (coherent stores).
+template <int NPL, bool kPublish = false>
+__device__ __forceinline__ void route_logits(const RouteLogits<NPL>& logits, int num_experts,
+                                             int top_k, int64_t out_row, int32_t* ids32,
+                                             int64_t* ids64, void* weights, int weights_f32) {
+  const int lane = lane_id();
+  const RouteChoice choice = route_top_k<NPL>(logits, num_experts, top_k);
   if (lane < top_k) {
     const int64_t out = out_row * top_k + lane;
-    const float weight = probability / total;
+    const int selected = choice.expert;
+    const float weight = choice.weight;
     if (ids32 != nullptr) {
       if constexpr (kPublish)
         publish_u32(ids32 + out, static_cast<uint32_t>(selected));
@@ -185,12 +214,8 @@ __device__ __forceinline__ void quantize_row_part(const RowPart& row, int width,
     }
     amax = segment_max<16>(amax);
     const float scale = group_scale(amax);
-    uint32_t lo = 0u, hi = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lo |= quantize_one(v[i], scale) << (8 * i);
-      hi |= quantize_one(v[i + 4], scale) << (8 * i);
-    }
+    const uint32_t lo = quantize_four(v, scale);
+    const uint32_t hi = quantize_four(v + 4, scale);
     if (inside) {
       float* scale_out = scales + static_cast<int64_t>(column / kGroup) * scale_stride;
       if constexpr (kPublish) {

@@ -18,6 +18,12 @@ Step (one kernel each, all on the current stream):
     (decode-sized items: FC2 computes the SwiGLU requant in its prologue,
     d3_expert_fc2_swiglu, and silu_mul_quant is not launched)
     weighted_combine sum_r w[t,r] y[t*K+r] -> bf16     (kernels.py:319-322,779)
+
+Decode step (``DecodeStep``, fragment-major weights, dense routing): no
+route sort and no front launch.  ``decode_route_fc1`` routes (expert ranks
+from the logits), quantises and runs FC1 from the slots; ``decode_fc2``
+finds each expert's routes from the ids FC1 wrote; ``decode_route_combine``
+recomputes the routing weights and combines.
 """
 
 from __future__ import annotations
@@ -298,6 +304,31 @@ class MoEWorkspace:
              s.intermediate, ptr(self.ids), ptr(row_count), s.rows, s.top_k, ptr(self.gate_up),
              None, self.exact_routes, None, ptr(self.down), stream)
 
+    def decode_route_fc1(self, experts, occupancy, x, logits, active, count,
+                         stream=None) -> None:
+        """Sortless FC1 straight from the slots (no front launch): every
+        workgroup ranks its expert in each occupied slot, quantises its
+        routes' x rows itself and writes gate_up[pair]; also writes ids,
+        ``count`` and ``active`` as the front would (not q / x_scales)."""
+        s, stream = self.shape, self._stream(stream)
+        w, ws, layout = fc1_operands(experts)
+        if layout != LAYOUT_FRAGMENT:
+            raise ValueError("sortless decode needs fragment-major weights (prepare_experts)")
+        call("d3_decode_route_fc1", ptr(w), ptr(ws), s.num_experts, 2 * s.intermediate, s.hidden,
+             ptr(occupancy), s.rows, ptr(x), x.stride(0), ptr(logits), dtype_code(logits.dtype),
+             logits.stride(0), s.top_k, self.exact_routes, ptr(self.ids), ptr(count),
+             ptr(active), ptr(self.gate_up), stream)
+
+    def decode_route_combine(self, occupancy, logits, out=None, stream=None) -> torch.Tensor:
+        """Combine of the step started by decode_route_fc1: the routing weights
+        are recomputed from the logits (and stored in ``weights``)."""
+        s, stream = self.shape, self._stream(stream)
+        out = self.out if out is None else out
+        call("d3_decode_route_combine", ptr(occupancy), s.rows, ptr(logits),
+             dtype_code(logits.dtype), logits.stride(0), s.num_experts, s.top_k, s.hidden,
+             ptr(self.down), ptr(self.weights), dtype_code(self.weights.dtype), ptr(out), stream)
+        return out
+
     def experts(self, experts, row_count=None, shared=None, out=None, stream=None):
         """FC1, SwiGLU requant, FC2 and combine over the routes sorted by front().
         With ``fused_epilogues`` two launches replace four; a dense shared
@@ -368,6 +399,12 @@ def compact_slots(occupancy: torch.Tensor, active: torch.Tensor, count: torch.Te
     call("d3_compact_slots", ptr(occupancy), occupancy.numel(), ptr(active), ptr(count), stream)
 
 
+def _strided_rows_inside(t: torch.Tensor, rows: int) -> bool:
+    """Whether ``rows`` full row strides from ``t``'s first element lie inside
+    its storage (the range a kernel's buffer view of the rows covers)."""
+    return (t.storage_offset() + rows * t.stride(0)) * t.element_size() <= t.untyped_storage().nbytes()
+
+
 class DecodeStep:
     """The 64-slot decode MoE step: device-side slot compaction, then route +
     experts over the live rows, everything sized for the slot capacity and
@@ -379,11 +416,20 @@ class DecodeStep:
     on fragment-major weights (``prepare_experts``) and bf16 logits, with the
     same buffers and results as the multi-kernel chain; other calls (and the
     default) use the chain, which is currently the faster of the two.
+
+    The sortless chain (``sortless``) normally starts with the front launch;
+    with ``frontless`` (default: whenever the sortless chain runs and the
+    inputs fit ``d3_decode_route_fc1``) the FC1 routes and quantises the
+    slots itself and the combine recomputes the routing weights, so the step
+    is three launches.  Same outputs (``out``, ``active``, ``count``,
+    workspace ``ids`` / ``weights`` / ``gate_up`` / ``down``); ``q`` and
+    ``x_scales`` are not written.
     """
 
     def __init__(self, slots: int, num_experts: int, hidden: int, intermediate: int,
                  top_k: int = 8, device="cuda", item_rows: int | None = None,
-                 fused: bool | None = None, sortless: bool | None = None):
+                 fused: bool | None = None, sortless: bool | None = None,
+                 frontless: bool | None = None):
         dev = torch.device(device)
         self.slots = slots
         self.active = torch.empty(slots, dtype=torch.int32, device=dev)
@@ -401,6 +447,9 @@ class DecodeStep:
         if sortless is None:
             sortless = decode_shapes and dense and slots <= 256 and top_k <= 8
         self.sortless = bool(sortless)
+        self.frontless = self.sortless if frontless is None else bool(frontless)
+        if self.frontless and not self.sortless:
+            raise ValueError("frontless runs the sortless chain (sortless=True)")
         sync_ints = lib.d3_moe_step_sync_ints(slots, num_experts, hidden, intermediate)
         supported = sync_ints > 0 and slots <= 256 and num_experts <= 256
         if fused and not supported:
@@ -421,9 +470,35 @@ class DecodeStep:
         if self.uses_fused(logits_slots, experts):
             return self._fused(occupancy, x_slots, logits_slots, experts, stream)
         ws.sortless = self.sortless and self.uses_sortless(experts)
+        if ws.sortless and self.uses_frontless(occupancy, x_slots, logits_slots):
+            ws.decode_route_fc1(experts, occupancy, x_slots, logits_slots, self.active,
+                                self.count, stream)
+            ws.decode_fc2(experts, self.count, stream)
+            return ws.decode_route_combine(occupancy, logits_slots, stream=stream)
         ws.front(x_slots, logits_slots, occupancy=occupancy, active=self.active,
                  count=self.count, stream=stream)
         return ws.experts(experts, self.count, stream=stream)
+
+    def uses_frontless(self, occupancy, x_slots, logits_slots) -> bool:
+        """Whether a call with these inputs runs the three-launch step."""
+        s = self.workspace.shape
+        if not self.frontless or logits_slots.dtype not in (torch.bfloat16, torch.float32):
+            return False
+        f32 = logits_slots.dtype == torch.float32
+        per_chunk = 4 if f32 else 8
+        return (occupancy.dtype == torch.uint8 and occupancy.numel() == self.slots
+                and x_slots.dtype == torch.bfloat16 and x_slots.dim() == 2
+                and x_slots.shape[0] >= self.slots and x_slots.shape[1] == s.hidden
+                and x_slots.stride(1) == 1 and x_slots.stride(0) % 8 == 0
+                and x_slots.data_ptr() % 16 == 0
+                and logits_slots.dim() == 2 and logits_slots.shape[0] >= self.slots
+                and logits_slots.shape[1] == s.num_experts and logits_slots.stride(1) == 1
+                and logits_slots.stride(0) % per_chunk == 0
+                and logits_slots.data_ptr() % 16 == 0
+                and s.num_experts <= 32 * per_chunk and s.top_k <= s.num_experts
+                # the kernels' buffer ranges span slots * row stride elements
+                and _strided_rows_inside(x_slots, self.slots)
+                and _strided_rows_inside(logits_slots, self.slots))
 
     @staticmethod
     def uses_sortless_layout(experts) -> bool:

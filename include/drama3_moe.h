@@ -290,6 +290,48 @@ int d3_decode_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32
                           int32_t exact_routes, uint16_t *out_bf16, float *out_f32, void *stream);
 
 /*
+ * A1-A3, A5, A8  Decode FC1 straight from the slots (no front launch).
+ * Replaces, for the decode step, the slot filter (src/drama3/engine.py:637-647),
+ * route_kernel's top-k (src/drama3/kernels.py:360-383), the per-128
+ * quantisation (src/drama3/moe_input.py:24-27) and expert_up_kernel
+ * (kernels.py:290-301) of DramaModel.routed_moe (src/drama3/model.py:520-583).
+ * Each (expert, weight tile) workgroup ranks its expert in every occupied
+ * slot from the logits (rank = experts with a larger routing key; a route
+ * when rank < top_k), quantises the x rows of its routes while staging them,
+ * and writes gate_up by pair exactly as d3_moe_front + d3_decode_expert_gemm
+ * mode 0 do.  It also writes that front's ids int32 [capacity, top_k] (by
+ * row), *count and active int32 [capacity] (ascending slots, -1 padded);
+ * the routing weights are left to d3_decode_route_combine, and no q /
+ * x_scales are stored.
+ *   occupancy u8 [capacity]; x bf16 [capacity rows, x_stride];
+ *   logits bf16 or f32 [capacity rows, logits_stride] (16-byte aligned rows);
+ *   w / ws fragment-major W13 and its block scales; n = 2I, k = H in
+ *   {1024, 2048}; capacity <= 256, top_k <= 8, E <= 256 (bf16 logits) or
+ *   128 (f32).
+ */
+int d3_decode_route_fc1(const uint8_t *w, const float *ws, int32_t num_experts, int32_t n,
+                        int32_t k, const uint8_t *occupancy, int32_t capacity, const uint16_t *x,
+                        int64_t x_stride, const void *logits, int32_t logits_dtype,
+                        int64_t logits_stride, int32_t top_k, int32_t exact_routes, int32_t *ids,
+                        int32_t *count, int32_t *active, uint16_t *gate_up, void *stream);
+
+/*
+ * A4, A12  Weighted combine of the step started by d3_decode_route_fc1.
+ * Replaces route_kernel's weights (src/drama3/kernels.py:360-383) and the
+ * combine (kernels.py:319-322) for the decode step.  One workgroup per
+ * (slot, 512 columns): an occupied slot's row r gets
+ * out[r] = bf16(sum_rank w[rank] * down[r * top_k + rank]) in rank order,
+ * w being the front's routing weights of the slot's logits rounded to
+ * weights_dtype (bf16 or f32), which are also stored in weights
+ * [capacity, top_k] by row.  Same bytes as d3_moe_front's weights +
+ * d3_weighted_combine.  capacity <= 256, top_k <= 8, E <= 256.
+ */
+int d3_decode_route_combine(const uint8_t *occupancy, int32_t capacity, const void *logits,
+                            int32_t logits_dtype, int64_t logits_stride, int32_t num_experts,
+                            int32_t top_k, int32_t hidden, const float *down, void *weights,
+                            int32_t weights_dtype, uint16_t *out, void *stream);
+
+/*
  * A1-A12  The whole decode MoE step in one launch.
  * Replaces DramaModel.routed_moe's decode path (src/drama3/model.py:520-583:
  * slot filter engine.py:637-647, route kernels.py:360-383, quantise

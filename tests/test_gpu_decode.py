@@ -1,7 +1,10 @@
-"""Sortless decode expert GEMMs (d3_decode_expert_gemm): every expert-GEMM
-workgroup finds its expert's routes itself, rows are indexed by pair.  The
-results are bit-identical to the sorted chain's for the same pairs: gate_up
-(mapped through the sorted layout), down and the combined output."""
+"""Sortless decode expert GEMMs (d3_decode_expert_gemm) and the three-launch
+step that starts from the slots (d3_decode_route_fc1 + FC2 +
+d3_decode_route_combine).  Every expert-GEMM workgroup finds its expert's
+routes itself and rows are indexed by pair.  All results are bit-identical
+to the sorted chain's for the same pairs: ids, routing weights, the slot
+list, gate_up (mapped through the sorted layout), down and the combined
+output."""
 
 import numpy as np
 import pytest
@@ -13,15 +16,17 @@ from oracle import moe as om
 pytestmark = pytest.mark.gpu
 
 
-def steps_for(w, device, experts):
+def steps_for(w, device, experts, slots=64):
+    """(frontless, sortless after the front, sorted chain) decode steps."""
     from drama3_amd.pipeline import DecodeStep
 
-    sortless = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device,
-                          sortless=True)
-    sorted_chain = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device,
-                              sortless=False)
-    assert sortless.uses_sortless(experts) and not sorted_chain.uses_sortless(experts)
-    return sortless, sorted_chain
+    args = (slots, w.num_experts, w.hidden, w.intermediate)
+    frontless = DecodeStep(*args, device=device, sortless=True)
+    front = DecodeStep(*args, device=device, sortless=True, frontless=False)
+    sorted_chain = DecodeStep(*args, device=device, sortless=False)
+    assert frontless.uses_sortless(experts) and front.uses_sortless(experts)
+    assert not sorted_chain.uses_sortless(experts)
+    return frontless, front, sorted_chain
 
 
 def compare(sortless, chain):
@@ -31,6 +36,8 @@ def compare(sortless, chain):
     a, b = sortless.workspace, chain.workspace
     pairs = n * a.shape.top_k
     assert torch.equal(a.ids[:n], b.ids[:n])
+    assert torch.equal(a.weights[:n].view(torch.int16 if a.weights.dtype == torch.bfloat16 else torch.int32),
+                       b.weights[:n].view(torch.int16 if b.weights.dtype == torch.bfloat16 else torch.int32))
     assert torch.equal(a.down[:pairs].view(torch.int32), b.down[:pairs].view(torch.int32))
     # chain gate_up row at sorted position p holds pair sorted_ids[p]
     total = int(b.total.item())
@@ -39,7 +46,18 @@ def compare(sortless, chain):
     chain_rows = np_bf16(b.gate_up)[positions]
     sortless_rows = np_bf16(a.gate_up)[order[positions]]
     assert np.array_equal(sortless_rows, chain_rows)
-    assert torch.equal(a.out[:n], b.out[:n])
+    assert torch.equal(a.out[:n].view(torch.int16), b.out[:n].view(torch.int16))
+    return n
+
+
+def run_all(steps, occ, xs, ls, experts):
+    for ds in steps:
+        ds(occ, xs, ls, experts)
+    torch.cuda.synchronize()
+    frontless, front, chain = steps
+    assert frontless.uses_frontless(occ, xs, ls) and not front.uses_frontless(occ, xs, ls)
+    n = compare(frontless, chain)
+    assert compare(front, chain) == n
     return n
 
 
@@ -51,14 +69,11 @@ def test_sortless_matches_sorted_chain(device, config):
     w = workloads.CONFIGS[config]()
     step = w.steps[0]
     experts = prepare_experts(w.experts.to(device))
-    sortless, chain = steps_for(w, device, experts)
+    steps = steps_for(w, device, experts)
     occ = step.occupancy.to(device)
     xs, ls = step.x_slots.to(device), step.logits_slots.to(device)
-    for launch in range(2):
-        sortless(occ, xs, ls, experts)
-        chain(occ, xs, ls, experts)
-        torch.cuda.synchronize()
-        n = compare(sortless, chain)
+    for launch in range(2):  # the second launch overwrites the first's buffers
+        n = run_all(steps, occ, xs, ls, experts)
         print(f"config {config} launch {launch}: rows {n}", flush=True)
 
 
@@ -70,7 +85,7 @@ def test_sortless_occupancies(device, pattern):
     w = workloads.config2()
     step = w.steps[0]
     experts = prepare_experts(w.experts.to(device))
-    sortless, chain = steps_for(w, device, experts)
+    steps = steps_for(w, device, experts)
     occupancy = np.zeros(64, np.uint8)
     if pattern == "last":
         occupancy[63] = 1
@@ -80,14 +95,69 @@ def test_sortless_occupancies(device, pattern):
         occupancy[1::2] = 1
     occ = torch.from_numpy(occupancy).to(device)
     xs, ls = step.x_slots.to(device), step.logits_slots.to(device)
-    sortless(occ, xs, ls, experts)
-    chain(occ, xs, ls, experts)
-    torch.cuda.synchronize()
-    assert compare(sortless, chain) == int(occupancy.sum())
+    print(f"pattern {pattern}", flush=True)
+    assert run_all(steps, occ, xs, ls, experts) == int(occupancy.sum())
+
+
+@pytest.mark.parametrize("logits_dtype", [torch.bfloat16, torch.float32])
+def test_frontless_ties_and_logit_dtypes(device, logits_dtype):
+    """Logits on a coarse grid (many exact ties: the lower expert ranks
+    first), in bf16 and f32, plus rows with +-inf and a zero x row."""
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
+
+    w = workloads.config1()
+    experts = prepare_experts(w.experts.to(device))
+    steps = steps_for(w, device, experts)
+    gen = torch.Generator("cpu").manual_seed(11)
+    logits = torch.randint(-2, 3, (64, w.num_experts), generator=gen).float() * 0.5
+    logits[5, 3] = float("inf")
+    logits[9, :] = 0.0
+    logits[12, 7] = float("-inf")
+    occupancy = (torch.rand(64, generator=gen) < 0.6).to(torch.uint8)
+    occupancy[[5, 9, 12]] = 1
+    xs = w.steps[0].x_slots.clone()
+    xs[9] = 0.0
+    ls = logits.to(logits_dtype).to(device)
+    n = run_all(steps, occupancy.to(device), xs.to(device), ls, experts)
+    print(f"{logits_dtype}: rows {n}", flush=True)
+    frontless = steps[0]
+    active, _ = om.compact_slots(occupancy.numpy())
+    weights, ids = om.route(np_f32(ls)[active])
+    assert np.array_equal(frontless.workspace.ids.cpu().numpy()[:n], ids)
+
+
+def test_frontless_more_slots_and_odd_experts(device):
+    """200 slots (four ranking passes, one weight tile per workgroup) and
+    E = 20 (partial logit chunks)."""
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.workloads import Workload, make_experts
+
+    gen = torch.Generator("cpu").manual_seed(21)
+    e, h, i, slots = 20, 1024, 256, 200
+    experts_cpu = make_experts(gen, e, h, i)
+    w = Workload("odd", 21, h, e, i, experts_cpu, [])
+    experts = prepare_experts(experts_cpu.to(device))
+    steps = steps_for(w, device, experts, slots=slots)
+    occupancy = (torch.rand(slots, generator=gen) < 0.7).to(torch.uint8)
+    occupancy[[0, 63, 64, 127, 128, 199]] = 1
+    xs = torch.randn((slots, h), generator=gen).to(torch.bfloat16).to(device)
+    ls = torch.randn((slots, e), generator=gen).to(torch.bfloat16)
+    # rows 8 apart: 16-byte aligned rows of a wider buffer (a strided view)
+    wide = torch.zeros((slots, 24), dtype=torch.bfloat16)
+    wide[:, :e] = ls
+    ls_dev = wide.to(device)[:, :e]
+    n = run_all(steps, occupancy.to(device), xs, ls_dev, experts)
+    assert n == int(occupancy.sum())
+    active, _ = om.compact_slots(occupancy.numpy())
+    weights, ids = om.route(np_f32(ls)[active])
+    expected = om.expert_ffn(np_bf16(xs.cpu())[active], ids, weights, oracle_weights(experts_cpu))
+    stats = assert_bf16_close(np_bf16(steps[0].workspace.out)[:n], expected, **EXACT)
+    print(f"slots {slots}, E {e}: rows {n} {stats}", flush=True)
 
 
 def test_sortless_matches_oracle_and_replays(device):
-    """c1 shapes (16 experts, ~32 routes each: several route tiles per
+    """c3 shapes (16 experts, ~32 routes each: several route tiles per
     expert) captured once and replayed with changing occupancy."""
     from drama3_amd import workloads
     from drama3_amd.expert_weights import prepare_experts
@@ -100,6 +170,7 @@ def test_sortless_matches_oracle_and_replays(device):
     ds = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device, sortless=True)
     occ = step.occupancy.to(device)
     xs, ls = step.x_slots.to(device), step.logits_slots.to(device)
+    assert ds.uses_frontless(occ, xs, ls)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -109,14 +180,20 @@ def test_sortless_matches_oracle_and_replays(device):
     with torch.cuda.graph(graph):
         out = ds(occ, xs, ls, experts)
     rng = np.random.default_rng(7)
-    for replay, p in enumerate([1.0, 0.3, 0.8]):
+    for replay, p in enumerate([1.0, 0.3, 0.8, 0.0]):
         occupancy = (rng.uniform(size=64) < p).astype(np.uint8)
         occ.copy_(torch.from_numpy(occupancy))
         graph.replay()
         torch.cuda.synchronize()
+        _ = torch.ones(1024, device=device).sum().item()  # eager work between replays
         active, n = om.compact_slots(occupancy)
         assert int(ds.count.item()) == n
+        assert np.array_equal(ds.active.cpu().numpy()[:n], active)
+        assert np.all(ds.active.cpu().numpy()[n:] == -1)
+        if n == 0:
+            continue
         weights, ids = om.route(np_f32(step.logits_slots)[active])
+        assert np.array_equal(ds.workspace.ids.cpu().numpy()[:n], ids)
         expected = om.expert_ffn(np_bf16(step.x_slots)[active], ids, weights, wt)
         stats = assert_bf16_close(np_bf16(out)[:n], expected, **EXACT)
         print(f"replay {replay}: rows {n} {stats}", flush=True)
@@ -134,3 +211,35 @@ def test_decode_gemm_contract(device):
     with pytest.raises(ValueError, match="K=768"):
         _lib.call("d3_decode_expert_gemm", 0, 16, 16, 4, 512, 768, 16, None, 64, 8, 16, 16, 64,
                   16, None, None)
+
+
+def test_route_fc1_and_combine_contract(device):
+    from drama3_amd import _lib
+
+    p = 256  # any aligned non-null address: every call below is rejected before a launch
+    fc1 = [p, p, 128, 1536, 2048, p, 64, p, 2048, p, _lib.DTYPE_BF16, 128, 8, 16, p, p, p, p, None]
+    bad = list(fc1)
+    bad[3 - 1] = 300  # E above what a workgroup ranks
+    with pytest.raises(ValueError, match="E=300"):
+        _lib.call("d3_decode_route_fc1", *bad)
+    bad = list(fc1)
+    bad[11] = 130  # logits rows not 16-byte aligned
+    with pytest.raises(ValueError, match="aligned"):
+        _lib.call("d3_decode_route_fc1", *bad)
+    bad = list(fc1)
+    bad[6] = 300  # capacity
+    with pytest.raises(ValueError, match="capacity"):
+        _lib.call("d3_decode_route_fc1", *bad)
+    bad = list(fc1)
+    bad[10] = _lib.DTYPE_I32
+    with pytest.raises(ValueError, match="logits"):
+        _lib.call("d3_decode_route_fc1", *bad)
+    combine = [p, 64, p, _lib.DTYPE_BF16, 128, 128, 8, 2048, p, p, _lib.DTYPE_BF16, p, None]
+    bad = list(combine)
+    bad[6] = 9  # top_k above 8
+    with pytest.raises(ValueError, match="top_k"):
+        _lib.call("d3_decode_route_combine", *bad)
+    bad = list(combine)
+    bad[0] = None
+    with pytest.raises(ValueError, match="null"):
+        _lib.call("d3_decode_route_combine", *bad)
