@@ -1,0 +1,417 @@
+// Tiled grouped FP8 expert GEMM for real contractions (packed prefill and
+// mixed batches): work items of up to 128 sorted routes against 256 weight
+// rows, the contraction streamed in 128-byte K blocks.
+//
+// Design (gfx950, wave64, MFMA 16x16x128 OCP-FP8, 4 waves per workgroup,
+// two workgroups per CU):
+//   * A workgroup owns (work item, weight row tile).  Each wave owns four
+//     16-row weight tiles (FC1: two gate tiles and the matching two up
+//     tiles) and all eight 16-route tiles of the item: 32 MFMAs per K block,
+//     128 fp32 accumulators per lane; each B fragment read from LDS feeds
+//     four MFMAs.
+//   * Weights go straight from memory into MFMA fragments one K block ahead
+//     of the MFMAs (fragment-major layout: two 1 KiB contiguous loads per
+//     tile and K block; checkpoint layout: 16 rows x 64 bytes per load).
+//     Activation rows (gathered by route: FC1 reads token sorted_ids /
+//     top_k, FC2 the sorted row) are staged one K block ahead into a
+//     two-slot LDS ring (128 routes x 144-byte rows; the 16-byte pad keeps
+//     the 16 rows of each ds_read_b128 on distinct banks); their loads are
+//     issued before the weights', so waiting for them never waits for the
+//     weights.  One barrier per K block.
+//   * Measured per workgroup (per-workgroup timestamps, config-4 FC1): the
+//     prologue (item, route ids, scales, first blocks) and the epilogue
+//     cost a third of a workgroup's time; two resident workgroups per CU
+//     hide them behind each other's K loop, which measured faster than
+//     8-wave workgroups with deeper prefetch (one per CU).  The prologue's
+//     loads are branch-free so they form one round trip per dependency.
+//   * Scales as in the other expert kernels: every MFMA is exactly one K
+//     block, rescaled with acc += mfma(w, a) * (w_scale * a_scale), K blocks
+//     in ascending order, so the sums are bit-identical to d3_expert_gemm's
+//     FP8 path.
+//   * FC1 (mode 0): a workgroup covers 128 gate rows and the 128 matching up
+//     rows, so each lane holds gate and up of the same columns: the epilogue
+//     rounds both to bf16 (the reference's FC1 output), computes SwiGLU,
+//     reduces the per-(route, 128-column) amax across lanes and waves and
+//     writes the e4m3 codes and scale, the bytes d3_silu_mul_quant would
+//     write.  FC2 (mode 1) stores fp32 rows by pair (the unpermute).
+//   * Workgroups are grouped so that two consecutive items' tiles run on one
+//     XCD together: an item's tiles share its activation rows, and an
+//     expert's consecutive items its weights, in that XCD's L2.
+#include "common.h"
+#include "expert_tile.h"
+#include "status.h"
+
+namespace d3 {
+namespace {
+
+constexpr int kGgWaves = 4;
+constexpr int kGgThreads = kGgWaves * kWave;
+constexpr int kGgRoutes = 128;                     // routes per work item (MFMA N side)
+constexpr int kGgRouteTiles = kGgRoutes / 16;      // 16-route tiles per wave
+constexpr int kGgWaveTiles = 4;                    // 16-row weight tiles per wave
+constexpr int kGgRows = kGgWaves * kGgWaveTiles * 16;  // 256 weight rows per workgroup
+constexpr int kGgStride = kGroup + 16;             // LDS bytes per staged route row
+constexpr int kGgStage = kGgRoutes * kGgStride;
+constexpr int kGgStaged = kGgRoutes * kGroup / (16 * kGgThreads);  // 16-byte copies per thread and K block
+constexpr int kGgXcds = 8;
+
+template <int KB, int MODE, bool kPacked>
+__global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2))) void grouped_gemm_kernel(
+    const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows, int out_cols,
+    const uint8_t* __restrict__ act, uint32_t act_bytes, const float* __restrict__ act_scales,
+    const int32_t* __restrict__ sorted_ids, int top_k, const int4* __restrict__ items,
+    const int32_t* __restrict__ num_items, int n_tiles, int chunk, uint8_t* __restrict__ out_codes,
+    float* __restrict__ out_scales, float* __restrict__ out_f32) {
+  constexpr int K = KB * kGroup;
+  __shared__ __attribute__((aligned(16))) uint8_t stage[2][kGgStage];
+  __shared__ float a_scale[KB][kGgRoutes];
+  __shared__ int target[kGgRoutes];  // FC1: sorted position, FC2: pair; -1 = no route
+  __shared__ float amax_part[MODE == 0 ? kGgWaves : 1][kGgRoutes];
+
+  // XCD-aware order: workgroup b runs on XCD b % 8; logical index L gives
+  // each XCD runs of `chunk` consecutive (item, tile) pairs.
+  const int b = blockIdx.x;
+  const int xcd = b % kGgXcds, j = b / kGgXcds;
+  const int logical = ((j / chunk) * kGgXcds + xcd) * chunk + j % chunk;
+  const int item_index = logical / n_tiles;
+  const int tile = logical % n_tiles;
+  if (item_index >= *num_items) return;
+  const int4 item = items[item_index];
+  const int expert = item.x;
+  const int first = item.y;
+  const int routes = min(item.z, kGgRoutes);
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int row16 = lane & 15;
+  const int group = lane >> 4;
+
+  // Weight rows of this wave's tile t (16 rows each).
+  const int n0 = tile * (MODE == 0 ? kGroup : kGgRows);
+  auto tile_row = [&](int t) {
+    if constexpr (MODE == 0)  // t = 0, 1: gate rows; t = 2, 3: the matching up rows
+      return (t < 2 ? 0 : out_cols) + n0 + 32 * wave + 16 * (t & 1);
+    else
+      return n0 + 64 * wave + 16 * t;
+  };
+  const uint8_t* wexp = w + static_cast<size_t>(expert) * n_rows * K;
+  const float* wsexp = ws + static_cast<size_t>(expert) * (n_rows / kGroup) * KB;
+
+  // Weight fragments through a buffer view of the expert: the lane offset
+  // is one VGPR, the tile / K block offset a wave-uniform scalar.  The
+  // fragment-major loads are non-temporal (every weight byte is read once).
+  constexpr int kNonTemporal = 2;
+  const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(wexp), 0, static_cast<uint32_t>(n_rows) * K, 0x00020000);
+  const uint32_t w_lane = kPacked ? lane * 16 : row16 * K + group * 16;
+  int32x8 wf[2][kGgWaveTiles];
+  auto load_weights = [&](int kb) {
+#pragma unroll
+    for (int t = 0; t < kGgWaveTiles; ++t) {
+      const uint32_t base = static_cast<uint32_t>(tile_row(t)) * K;
+      int32x4 lo, hi;
+      if constexpr (kPacked) {
+        lo = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, base + kb * 2048, kNonTemporal);
+        hi = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, base + kb * 2048 + 1024, kNonTemporal);
+      } else {
+        lo = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, base + kb * kGroup, 0);
+        hi = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, base + kb * kGroup + 64, 0);
+      }
+      int32x8 v;
+      v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
+      v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
+      wf[kb & 1][t] = v;
+    }
+  };
+  load_weights(0);  // depends on the item only
+
+  // Route rows of the item, loaded branch-free (a dead route reads the
+  // item's first id and is masked afterwards): one round trip.
+  auto route_row = [&](int r, int id) { return MODE == 0 ? id / top_k : first + r; };
+  const int part = tid & 7;
+  const int r0 = tid >> 3;
+  int ids[kGgStaged];
+#pragma unroll
+  for (int i = 0; i < kGgStaged; ++i) {
+    const int r = r0 + (kGgThreads / 8) * i;
+    ids[i] = sorted_ids[first + (r < routes ? r : 0)];
+  }
+  const int rs = tid % kGgRoutes;       // route of this thread's scales / target
+  const int k0 = tid / kGgRoutes;       // first K block of its scales
+  const int id_s = sorted_ids[first + (rs < routes ? rs : 0)];
+
+  // Staging: thread t copies 16 bytes (chunk t % 8 of the K block) of routes
+  // t / 8 + 32 i.  Dead routes read past the buffer (zeros).
+  const BufferView view(act, act_bytes);
+  uint32_t src[kGgStaged];
+#pragma unroll
+  for (int i = 0; i < kGgStaged; ++i) {
+    const int r = r0 + (kGgThreads / 8) * i;
+    src[i] = r < routes ? static_cast<uint32_t>(route_row(r, ids[i])) * K + part * 16 : kNoRow;
+  }
+  int4 staged[kGgStaged];
+  auto stage_load = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < kGgStaged; ++i) staged[i] = view.load16(src[i] + kb * kGroup);
+  };
+  auto stage_store = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < kGgStaged; ++i)
+      *reinterpret_cast<int4*>(&stage[kb & 1][(r0 + (kGgThreads / 8) * i) * kGgStride + part * 16]) =
+          staged[i];
+  };
+  stage_load(0);
+
+  // Route targets and activation scales of the item.
+  {
+    constexpr int kSplit = kGgThreads / kGgRoutes;  // threads per route row of scales
+    const bool live = rs < routes;
+    const float* srow = act_scales + static_cast<size_t>(route_row(rs, id_s)) * KB;
+    float sc[(KB + kSplit - 1) / kSplit];
+#pragma unroll
+    for (int q = 0; q * kSplit + k0 < KB; ++q) sc[q] = srow[q * kSplit + k0];
+#pragma unroll
+    for (int q = 0; q * kSplit + k0 < KB; ++q) a_scale[q * kSplit + k0][rs] = live ? sc[q] : 0.0f;
+    if (k0 == 0) target[rs] = live ? (MODE == 0 ? first + rs : id_s) : -1;
+  }
+  // Block scales of the wave's tiles for every K block (wave-uniform): FC1
+  // tiles 0-1 (gate) share one 128-row block and tiles 2-3 (up) another; a
+  // wave's four FC2 tiles lie in one block.
+  float w_rows[2][KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    w_rows[0][kb] = wsexp[(tile_row(0) / kGroup) * KB + kb];
+    w_rows[1][kb] = wsexp[(tile_row(2) / kGroup) * KB + kb];
+  }
+  stage_store(0);
+  __syncthreads();
+
+  floatx4 acc[kGgWaveTiles][kGgRouteTiles];
+#pragma unroll
+  for (int t = 0; t < kGgWaveTiles; ++t)
+#pragma unroll
+    for (int rt = 0; rt < kGgRouteTiles; ++rt) acc[t][rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    if (kb + 1 < KB) {
+      stage_load(kb + 1);  // before the weights: waiting for it never waits for them
+      load_weights(kb + 1);
+    }
+    // Keep each K block's loads in its own iteration (the unrolled loop would
+    // otherwise let the scheduler hoist later blocks' loads).
+    __builtin_amdgcn_sched_barrier(0);
+    float wsc[kGgWaveTiles];
+#pragma unroll
+    for (int t = 0; t < kGgWaveTiles; ++t) wsc[t] = w_rows[t < 2 ? 0 : 1][kb];
+    const uint8_t* buf = stage[kb & 1];
+    // Software pipeline over the route tiles: the MFMAs of tile rt, then
+    // the scale FMAs of tile rt - 1 (whose products are ready by then), so
+    // at most two tiles' products are live next to the accumulators.
+    floatx4 partial[2][kGgWaveTiles];
+    float as_prev = 0.0f;
+#pragma unroll
+    for (int rt = 0; rt <= kGgRouteTiles; ++rt) {
+      float as = 0.0f;
+      if (rt < kGgRouteTiles) {
+        const int route = 16 * rt + row16;
+        const int32x8 bfrag = load_fragment(buf + route * kGgStride, 0, group);
+        as = a_scale[kb][route];
+#pragma unroll
+        for (int t = 0; t < kGgWaveTiles; ++t) partial[rt & 1][t] = mfma_fp8(wf[kb & 1][t], bfrag);
+      }
+      if (rt > 0) {
+#pragma unroll
+        for (int t = 0; t < kGgWaveTiles; ++t) {
+          acc[t][rt - 1] += partial[(rt - 1) & 1][t] * (wsc[t] * as_prev);
+          // Materialise the sum here: the accumulators are only used under
+          // the epilogue's per-route conditions, and without this the
+          // compiler sinks every K block's FMAs (keeping every product live).
+          asm volatile("" : "+v"(acc[t][rt - 1]));
+        }
+      }
+      as_prev = as;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (kb + 1 < KB) stage_store(kb + 1);
+    __syncthreads();
+  }
+
+  if constexpr (MODE == 1) {
+#pragma unroll
+    for (int rt = 0; rt < kGgRouteTiles; ++rt) {
+      const int pair = target[16 * rt + row16];
+      if (pair < 0) continue;
+#pragma unroll
+      for (int t = 0; t < kGgWaveTiles; ++t) {
+        float* dst = out_f32 + static_cast<size_t>(pair) * n_rows + tile_row(t) + 4 * group;
+        *reinterpret_cast<float4*>(dst) = make_float4(acc[t][rt][0], acc[t][rt][1], acc[t][rt][2], acc[t][rt][3]);
+      }
+    }
+  } else {
+    // SwiGLU on the bf16-rounded FC1 outputs; lane holds gate / up columns
+    // 32 wave + 16 p + 4 group + i (p < 2, i < 4) of route 16 rt + row16.
+    float v[kGgRouteTiles][8];
+#pragma unroll
+    for (int rt = 0; rt < kGgRouteTiles; ++rt) {
+      float amax = 0.0f;
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float g = bf16_to_f32(f32_to_bf16(acc[p][rt][i]));
+          const float u = bf16_to_f32(f32_to_bf16(acc[2 + p][rt][i]));
+          const float sig = 1.0f / (1.0f + expf(-g));
+          const float a = (g * sig) * u;
+          v[rt][4 * p + i] = a;
+          amax = fmaxf(amax, fabsf(a));
+        }
+      amax = fmaxf(amax, __shfl_xor(amax, 16));
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      if (group == 0) amax_part[wave][16 * rt + row16] = amax;
+    }
+    __syncthreads();
+    const int groups = out_cols / kGroup;
+#pragma unroll
+    for (int rt = 0; rt < kGgRouteTiles; ++rt) {
+      const int route = 16 * rt + row16;
+      const int position = target[route];
+      if (position < 0) continue;
+      float amax = amax_part[0][route];
+#pragma unroll
+      for (int q = 1; q < kGgWaves; ++q) amax = fmaxf(amax, amax_part[q][route]);
+      const float scale = group_scale(amax);
+      uint8_t* dst = out_codes + static_cast<size_t>(position) * out_cols + n0 + 32 * wave + 4 * group;
+      *reinterpret_cast<uint32_t*>(dst) = quantize_four(&v[rt][0], scale);
+      *reinterpret_cast<uint32_t*>(dst + 16) = quantize_four(&v[rt][4], scale);
+      if (wave == 0 && group == 0) out_scales[static_cast<size_t>(position) * groups + tile] = scale;
+    }
+  }
+}
+
+struct GroupedLaunch {
+  int mode;
+  int layout;
+  const uint8_t* w;
+  const float* ws;
+  int n_rows;
+  int out_cols;
+  const uint8_t* a;
+  uint32_t a_bytes;
+  const float* as;
+  const int32_t* sorted_ids;
+  int top_k;
+  const int4* items;
+  const int32_t* num_items;
+  int max_items;
+  int item_rows;
+  uint8_t* codes;
+  float* scales;
+  float* out;
+};
+
+template <int KB, int MODE>
+void launch_grouped(const GroupedLaunch& g, hipStream_t s) {
+  const int n_tiles = MODE == 0 ? g.out_cols / kGroup : g.n_rows / kGgRows;
+  // Two consecutive items' tiles per XCD run.
+  const int chunk = 2 * n_tiles;
+  const int64_t logical = static_cast<int64_t>(g.max_items) * n_tiles;
+  const int64_t per_round = static_cast<int64_t>(kGgXcds) * chunk;
+  const int blocks = static_cast<int>((logical + per_round - 1) / per_round * per_round);
+#define D3_GG_ARGS dim3(blocks), dim3(kGgThreads), 0, s, g.w, g.ws, g.n_rows, g.out_cols, g.a, \
+                   g.a_bytes, g.as, g.sorted_ids, g.top_k, g.items, g.num_items, n_tiles, chunk, \
+                   g.codes, g.scales, g.out
+  if (g.layout == D3_LAYOUT_FRAGMENT)
+    hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true>), D3_GG_ARGS);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, false>), D3_GG_ARGS);
+#undef D3_GG_ARGS
+}
+
+template <int MODE>
+int dispatch_grouped(const GroupedLaunch& g, int k, hipStream_t s) {
+  switch (k / kGroup) {
+    case 2: launch_grouped<2, MODE>(g, s); return D3_OK;
+    case 4: launch_grouped<4, MODE>(g, s); return D3_OK;
+    case 6: launch_grouped<6, MODE>(g, s); return D3_OK;
+    case 8: launch_grouped<8, MODE>(g, s); return D3_OK;
+    case 12: launch_grouped<12, MODE>(g, s); return D3_OK;
+    case 16: launch_grouped<16, MODE>(g, s); return D3_OK;
+    default:
+      return set_error(D3_ERR_UNSUPPORTED, "grouped gemm: K=%d not in {256,512,768,1024,1536,2048}", k);
+  }
+}
+
+bool aligned_to(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+int check_grouped(const GroupedLaunch& g, int num_experts, int k, int64_t a_rows, const char* name) {
+  D3_REQUIRE(g.w && g.ws && g.a && g.as && g.sorted_ids && g.items && g.num_items,
+             "%s: null pointer", name);
+  D3_REQUIRE(g.layout == D3_LAYOUT_REFERENCE || g.layout == D3_LAYOUT_FRAGMENT,
+             "%s: weight_layout must be D3_LAYOUT_REFERENCE or D3_LAYOUT_FRAGMENT", name);
+  D3_REQUIRE(num_experts >= 1 && k > 0 && k % kGroup == 0, "%s: K=%d must be a positive multiple of 128",
+             name, k);
+  D3_REQUIRE(g.top_k >= 1 && g.max_items >= 0 && a_rows >= 1, "%s: bad top_k / max_items / rows", name);
+  D3_REQUIRE(g.item_rows >= 1 && g.item_rows <= kGgRoutes, "%s: item_rows %d not in [1, %d]", name,
+             g.item_rows, kGgRoutes);
+  D3_REQUIRE(a_rows * k < (int64_t{1} << 31), "%s: activation buffer beyond 2 GiB", name);
+  D3_REQUIRE(aligned_to(g.w, 16) && aligned_to(g.a, 16), "%s: operands must be 16-byte aligned", name);
+  return D3_OK;
+}
+
+}  // namespace
+}  // namespace d3
+
+using namespace d3;
+
+extern "C" int d3_grouped_fc1_swiglu(const uint8_t* w13, const float* s13, int32_t weight_layout,
+                                     int32_t num_experts, int32_t intermediate, int32_t hidden,
+                                     const uint8_t* q, int64_t q_rows, const float* x_scales,
+                                     const int32_t* sorted_ids, int32_t top_k, const int32_t* items,
+                                     const int32_t* num_items, int32_t max_items,
+                                     int32_t item_rows, uint8_t* act, float* act_scales,
+                                     void* stream) {
+  D3_REQUIRE(act && act_scales, "grouped_fc1_swiglu: null output");
+  D3_REQUIRE(intermediate > 0 && intermediate % kGroup == 0,
+             "grouped_fc1_swiglu: intermediate %d must be a multiple of 128", intermediate);
+  D3_REQUIRE(aligned_to(act, 4), "grouped_fc1_swiglu: act must be 4-byte aligned");
+  const GroupedLaunch g{0, weight_layout, w13, s13, 2 * intermediate, intermediate, q,
+                        static_cast<uint32_t>(q_rows * hidden), x_scales, sorted_ids, top_k,
+                        reinterpret_cast<const int4*>(items), num_items, max_items, item_rows, act,
+                        act_scales, nullptr};
+  int status = check_grouped(g, num_experts, hidden, q_rows, "grouped_fc1_swiglu");
+  if (status != D3_OK) return status;
+  if (max_items == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  status = dispatch_grouped<0>(g, hidden, as_stream(stream));
+  if (status != D3_OK) return status;
+  D3_LAUNCHED("grouped_fc1_swiglu");
+}
+
+extern "C" int d3_grouped_fc2(const uint8_t* w2, const float* s2, int32_t weight_layout,
+                              int32_t num_experts, int32_t hidden, int32_t intermediate,
+                              const uint8_t* act, int64_t act_rows, const float* act_scales,
+                              const int32_t* sorted_ids, int32_t top_k, const int32_t* items,
+                              const int32_t* num_items, int32_t max_items, int32_t item_rows,
+                              float* down, void* stream) {
+  D3_REQUIRE(down != nullptr, "grouped_fc2: null output");
+  D3_SUPPORTED(hidden > 0 && hidden % kGgRows == 0,
+               "grouped_fc2: hidden %d must be a multiple of %d", hidden, kGgRows);
+  D3_REQUIRE(aligned_to(down, 16), "grouped_fc2: down must be 16-byte aligned");
+  const GroupedLaunch g{1, weight_layout, w2, s2, hidden, hidden, act,
+                        static_cast<uint32_t>(act_rows * intermediate), act_scales, sorted_ids, top_k,
+                        reinterpret_cast<const int4*>(items), num_items, max_items, item_rows, nullptr,
+                        nullptr, down};
+  int status = check_grouped(g, num_experts, intermediate, act_rows, "grouped_fc2");
+  if (status != D3_OK) return status;
+  if (max_items == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  status = dispatch_grouped<1>(g, intermediate, as_stream(stream));
+  if (status != D3_OK) return status;
+  D3_LAUNCHED("grouped_fc2");
+}

@@ -48,12 +48,21 @@ SIGNATURES = {
     "d3_moe_front": (
         _i32, [_p, _i32, _p, _p, _p, _i64, _p, _i32, _i64, _i32, _p, _p, _i32, _i32, _i32, _p, _p,
                _i32, _p, _p, _i32, _i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _p, _p, _p, _p]),
+    "d3_sort_routes_wide": (
+        _i32, [_p, _i32, _i32, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _i32, _p, _i32, _p,
+               _i32, _p, _p, _p, _i64, _p]),
+    "d3_sort_wide_scratch_ints": (_i64, [_i32, _i32, _i32]),
     "d3_max_sorted_rows": (_i32, [_i32, _i32, _i32]),
     "d3_max_items": (_i32, [_i32, _i32, _i32]),
     "d3_expert_gemm": (
         _i32, [_i32, _p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32,
                _p, _p, _p]),
     "d3_expert_tile_rows": (_i32, [_i32]),
+    "d3_grouped_fc1_swiglu": (
+        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p,
+               _p]),
+    "d3_grouped_fc2": (
+        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p]),
     "d3_pack_expert_weights": (_i32, [_p, _i32, _i32, _i32, _p, _p]),
     "d3_expert_fc1_swiglu": (
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _p, _p,

@@ -14,7 +14,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr
-from .pipeline import MoEWorkspace, Shape, dtype_code, require_cuda
+from .pipeline import WIDE_SORT_PAIRS, MoEWorkspace, Shape, dtype_code, require_cuda
 
 TOP_K = 8
 
@@ -137,9 +137,14 @@ def sort_routes(topk_ids: torch.Tensor, num_experts: int, block_m: int = 16):
     sorted_ids = torch.empty(max_rows, **i32)
     expert_ids = torch.empty(max_rows // block_m, **i32)
     inverse = torch.empty(max(pairs, 1), **i32)
-    call("d3_sort_routes", ptr(ids), dtype_code(ids.dtype), rows, None, top_k, num_experts,
-         block_m, ptr(counts), ptr(starts), ptr(total), ptr(sorted_ids), ptr(expert_ids),
-         max_rows, ptr(inverse), block_m, None, 0, None, None, _lib.stream(dev))
+    args = (ptr(ids), dtype_code(ids.dtype), rows, None, top_k, num_experts, block_m, ptr(counts),
+            ptr(starts), ptr(total), ptr(sorted_ids), ptr(expert_ids), max_rows, ptr(inverse),
+            block_m, None, 0, None, None)
+    if pairs > WIDE_SORT_PAIRS:  # prefill-sized: the ranking spread over many workgroups
+        scratch = torch.empty(lib.d3_sort_wide_scratch_ints(rows, top_k, num_experts), **i32)
+        call("d3_sort_routes_wide", *args, ptr(scratch), scratch.numel(), _lib.stream(dev))
+    else:
+        call("d3_sort_routes", *args, _lib.stream(dev))
     return counts, starts, total, sorted_ids, expert_ids, inverse[:pairs]
 
 

@@ -40,9 +40,22 @@ SORT_TILE = 16  # MFMA route tile; also the padding granularity of the sorted la
 # Work items with at most this many routes take the exact (bf16-MFMA) path of
 # the expert GEMM; larger items are real contractions and take FP8 MFMAs.
 EXACT_ROUTES = 64
+# Contraction lengths compiled for the tiled grouped GEMMs (d3_grouped_*).
+GROUPED_K = (256, 512, 768, 1024, 1536, 2048)
+GROUPED_ROUTES = 128  # most routes per work item of the tiled grouped GEMMs
+GROUPED_ITEM_ROUTES = 128  # their default item size
 # Up to this many (row, rank) pairs the route sort runs inside the fused front
-# kernel (its last workgroup); larger batches use the 1024-thread sort kernel.
+# kernel (its last workgroup); larger batches use the 1024-thread sort kernel,
+# and from WIDE_SORT_PAIRS on the wide sort (one workgroup per 2048 pairs).
 FUSED_SORT_PAIRS = 8192
+WIDE_SORT_PAIRS = 8192
+
+
+def grouped_supported(hidden: int, intermediate: int) -> bool:
+    """Whether the tiled grouped FC1 (K = hidden) and FC2 (K = intermediate,
+    N = hidden in 256-row tiles) cover these shapes."""
+    return (hidden in GROUPED_K and intermediate in GROUPED_K and hidden % 256 == 0
+            and intermediate % 128 == 0)
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -93,7 +106,8 @@ class MoEWorkspace:
     def __init__(self, shape: Shape, device: torch.device | str = "cuda", tile: int = SORT_TILE,
                  item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
                  exact_routes: int = EXACT_ROUTES, fused_epilogues: bool = False,
-                 swiglu_in_fc2: bool | None = None, sortless: bool = False):
+                 swiglu_in_fc2: bool | None = None, sortless: bool = False,
+                 grouped: bool | None = None):
         lib = _lib.load()
         self.shape = shape
         self.device = torch.device(device)
@@ -101,6 +115,14 @@ class MoEWorkspace:
         self.exact_routes = exact_routes
         self.item_rows = item_rows or default_item_rows(shape.rows, tile, shape.num_experts,
                                                         shape.top_k)
+        # Contraction-sized items go to the tiled grouped GEMMs, whose items
+        # hold up to GROUPED_ROUTES routes.
+        contraction = self.item_rows > EXACT_ROUTES
+        h, i = shape.hidden, shape.intermediate
+        if grouped is None:
+            grouped = contraction and grouped_supported(h, i) and not fused_epilogues and not sortless
+        if grouped and item_rows is None and shape.rows > 128:
+            self.item_rows = GROUPED_ITEM_ROUTES
         if self.item_rows % tile:
             raise ValueError("item_rows must be a multiple of the sort tile")
         pairs = shape.pairs
@@ -149,7 +171,17 @@ class MoEWorkspace:
         self.sortless = sortless
         if sortless and (t > 256 or shape.top_k > 8):
             raise ValueError("sortless decode covers up to 256 rows and top_k <= 8")
+        # Tiled grouped GEMMs (FP8 MFMA contraction, SwiGLU requant in FC1's
+        # epilogue) for contraction-sized items: prefill and mixed batches.
+        if grouped and not (self.item_rows <= GROUPED_ROUTES and grouped_supported(h, i)):
+            raise ValueError(f"tiled grouped GEMMs need item_rows <= {GROUPED_ROUTES}, hidden and "
+                             f"intermediate in {GROUPED_K}, hidden % 256 == 0")
+        self.grouped = bool(grouped) and not sortless
         self.fc1_tickets = torch.zeros(self.max_rows * (i // 128) if self.fuse_fc1 else 1, **i32)
+        # Scratch of the wide route sort (prefill-sized batches).
+        self.wide_sort = pairs > WIDE_SORT_PAIRS
+        self.sort_scratch = torch.empty(
+            lib.d3_sort_wide_scratch_ints(t, shape.top_k, e) if self.wide_sort else 1, **i32)
         self.fc2_tickets = torch.zeros(t * (h // fc2_tile) if self.fuse_fc2 else 1, **i32)
 
     # -- stages ---------------------------------------------------------------
@@ -170,11 +202,16 @@ class MoEWorkspace:
     def sort(self, ids: torch.Tensor | None = None, row_count=None, stream=None) -> None:
         s, stream = self.shape, self._stream(stream)
         ids = self.ids if ids is None else ids
-        call("d3_sort_routes", ptr(ids), dtype_code(ids.dtype), s.rows, ptr(row_count), s.top_k,
-             s.num_experts, self.tile, ptr(self.counts), ptr(self.starts), ptr(self.total),
-             ptr(self.sorted_ids), ptr(self.expert_ids), self.max_rows, ptr(self.inverse),
-             self.item_rows, ptr(self.items), self.max_items, ptr(self.num_items),
-             ptr(self.pairs_dev), stream)
+        args = (ptr(ids), dtype_code(ids.dtype), s.rows, ptr(row_count), s.top_k,
+                s.num_experts, self.tile, ptr(self.counts), ptr(self.starts), ptr(self.total),
+                ptr(self.sorted_ids), ptr(self.expert_ids), self.max_rows, ptr(self.inverse),
+                self.item_rows, ptr(self.items), self.max_items, ptr(self.num_items),
+                ptr(self.pairs_dev))
+        if self.wide_sort:
+            call("d3_sort_routes_wide", *args, ptr(self.sort_scratch), self.sort_scratch.numel(),
+                 stream)
+        else:
+            call("d3_sort_routes", *args, stream)
 
     def front(self, x, logits, row_index=None, row_count=None, occupancy=None, active=None,
               count=None, stream=None) -> None:
@@ -206,6 +243,24 @@ class MoEWorkspace:
              s.num_experts, 2 * s.intermediate, s.hidden, ptr(self.q), ptr(self.x_scales),
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
              self.item_rows, self.exact_routes, ptr(self.gate_up), None, stream)
+
+    def grouped_fc1(self, experts, stream=None) -> None:
+        """Tiled grouped FC1 + SwiGLU requant: act / act_scales at sorted rows."""
+        s, stream = self.shape, self._stream(stream)
+        w, ws, layout = fc1_operands(experts)
+        call("d3_grouped_fc1_swiglu", ptr(w), ptr(ws), layout, s.num_experts, s.intermediate,
+             s.hidden, ptr(self.q), s.rows, ptr(self.x_scales), ptr(self.sorted_ids), s.top_k,
+             ptr(self.items), ptr(self.num_items), self.max_items, self.item_rows, ptr(self.act),
+             ptr(self.act_scales), stream)
+
+    def grouped_fc2(self, experts, stream=None) -> None:
+        """Tiled grouped FC2: fp32 down rows by pair."""
+        s, stream = self.shape, self._stream(stream)
+        w, ws, layout = fc2_operands(experts)
+        call("d3_grouped_fc2", ptr(w), ptr(ws), layout, s.num_experts, s.hidden, s.intermediate,
+             ptr(self.act), self.max_rows, ptr(self.act_scales), ptr(self.sorted_ids), s.top_k,
+             ptr(self.items), ptr(self.num_items), self.max_items, self.item_rows, ptr(self.down),
+             stream)
 
     def activation(self, stream=None) -> None:
         s, stream = self.shape, self._stream(stream)
@@ -247,8 +302,12 @@ class MoEWorkspace:
         stream = _lib.stream(self.device) if stream is None else stream
         self.quantize(x, row_index, row_count, stream)
         self.sort(ids, row_count, stream)
-        self.fc1(experts, stream)
-        self._fc2_stage(experts, stream)
+        if self.grouped:
+            self.grouped_fc1(experts, stream)
+            self.grouped_fc2(experts, stream)
+        else:
+            self.fc1(experts, stream)
+            self._fc2_stage(experts, stream)
         return self.combine(weights, row_count, shared, out, stream)
 
     def _fc2_stage(self, experts, stream) -> None:
@@ -338,6 +397,10 @@ class MoEWorkspace:
             self.decode_fc1(experts, row_count, stream)
             self.decode_fc2(experts, row_count, stream)
             return self.combine(None, row_count, shared, out, stream)
+        if self.grouped:
+            self.grouped_fc1(experts, stream)
+            self.grouped_fc2(experts, stream)
+            return self.combine(None, row_count, shared, out, stream)
         if self.fuse_fc1:
             self.fc1_swiglu(experts, stream)
         else:
@@ -358,9 +421,15 @@ class DenseExpert:
     run through the same kernels with the identity route list."""
 
     def __init__(self, rows: int, hidden: int, intermediate: int, device="cuda",
-                 item_rows: int = 128, exact_routes: int = EXACT_ROUTES):
+                 item_rows: int | None = None, exact_routes: int = EXACT_ROUTES,
+                 grouped: bool | None = None):
         self.rows, self.hidden, self.intermediate = rows, hidden, intermediate
         self.exact_routes = exact_routes
+        if grouped is None:
+            grouped = (item_rows or GROUPED_ROUTES) <= GROUPED_ROUTES and \
+                grouped_supported(hidden, intermediate)
+        self.grouped = bool(grouped)
+        item_rows = item_rows or (GROUPED_ITEM_ROUTES if self.grouped else 128)
         dev = torch.device(device)
         self.item_rows = item_rows
         chunks = -(-rows // item_rows)
@@ -380,6 +449,15 @@ class DenseExpert:
         h, i = self.hidden, self.intermediate
         w13, s13, layout13 = fc1_operands(experts)
         w2, s2, layout2 = fc2_operands(experts)
+        if self.grouped:  # identity routes: top_k 1, sorted_ids = row
+            call("d3_grouped_fc1_swiglu", ptr(w13), ptr(s13), layout13, 1, i, h, ptr(q),
+                 q.shape[0], ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items),
+                 ptr(self.num_items), self.max_items, self.item_rows, ptr(self.act),
+                 ptr(self.act_scales), stream)
+            call("d3_grouped_fc2", ptr(w2), ptr(s2), layout2, 1, h, i, ptr(self.act), self.rows,
+                 ptr(self.act_scales), ptr(self.sorted_ids), 1, ptr(self.items),
+                 ptr(self.num_items), self.max_items, self.item_rows, ptr(self.down), stream)
+            return self.down
         call("d3_expert_gemm", 0, ptr(w13), ptr(s13), layout13, 1, 2 * i, h, ptr(q),
              ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items), ptr(self.num_items),
              self.max_items, self.item_rows, self.exact_routes, ptr(self.gate_up), None, stream)

@@ -157,6 +157,26 @@ int d3_moe_front(const uint8_t *occupancy, int32_t num_slots, int32_t *active_sl
                  int32_t *items, int32_t max_items, int32_t *num_items, int32_t *pairs_out,
                  int32_t *ticket, void *stream);
 
+/*
+ * A5-A7  The same histogram / offsets / stable sort as d3_sort_routes, for
+ * prefill-sized batches: the ranking is spread over one workgroup per 2048
+ * pairs (three launches) instead of one workgroup walking every pair.
+ * Same arguments and outputs as d3_sort_routes (starts is required), plus a
+ * caller-owned int32 scratch of d3_sort_wide_scratch_ints(rows, top_k, E)
+ * ints.  Replaces expert_counts_kernel / expert_offsets_kernel /
+ * expert_scatter_kernel (src/drama3/kernels.py:658-699) as native_moe runs
+ * them for prefill (kernels.py:710-731).
+ */
+int d3_sort_routes_wide(const void *ids, int32_t ids_dtype, int32_t rows, const int32_t *row_count,
+                        int32_t top_k, int32_t num_experts, int32_t tile, int32_t *counts,
+                        int32_t *starts, int32_t *total, int32_t *sorted_ids, int32_t *expert_ids,
+                        int32_t max_rows, int32_t *inverse, int32_t item_rows, int32_t *items,
+                        int32_t max_items, int32_t *num_items, int32_t *pairs_out,
+                        int32_t *scratch, int64_t scratch_ints, void *stream);
+
+/* Scratch ints d3_sort_routes_wide needs (host-side arithmetic only). */
+int64_t d3_sort_wide_scratch_ints(int32_t rows, int32_t top_k, int32_t num_experts);
+
 /* Capacity helpers for d3_sort_routes (host-side arithmetic only). */
 int32_t d3_max_sorted_rows(int32_t pairs, int32_t num_experts, int32_t tile);
 int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);
@@ -196,6 +216,46 @@ int d3_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32_t weig
 
 /* Weight rows per workgroup tile of d3_expert_gemm for contraction length k. */
 int32_t d3_expert_tile_rows(int32_t k);
+
+/*
+ * A8-A10  Tiled grouped FC1 + SwiGLU requant for real contractions (packed
+ * prefill, mixed batches).  Replaces Fish fused_moe_gemm's FC1 as driven by
+ * native_moe (src/drama3/kernels.py:734-747) and silu_mul_quant
+ * (kernels.py:344,748).  For every work item {e, start, n} (n <= item_rows
+ * <= 128: the sort's items) the routes p in [start, start+n)
+ * gather token sorted_ids[p] / top_k of q fp8 [q_rows, hidden] (scales
+ * x_scales [q_rows, hidden/128]) and contract with w13[e] ([gate; up],
+ * fp8 [2I, hidden] in weight_layout, block scales s13[e]); FC1 is rounded
+ * to bf16, a = silu(gate) * up is requantised per 128 columns and written
+ * at sorted position p: act fp8 [rows, I], act_scales [rows, I/128].
+ * Contraction on FP8 MFMAs with the per-K128 rescale of d3_expert_gemm's
+ * FP8 path; act / act_scales equal d3_expert_gemm (mode 0, exact_routes 0)
+ * followed by d3_silu_mul_quant, byte for byte.  hidden in {256, 512, 768,
+ * 1024, 1536, 2048}; intermediate a multiple of 128.
+ */
+int d3_grouped_fc1_swiglu(const uint8_t *w13, const float *s13, int32_t weight_layout,
+                          int32_t num_experts, int32_t intermediate, int32_t hidden,
+                          const uint8_t *q, int64_t q_rows, const float *x_scales,
+                          const int32_t *sorted_ids, int32_t top_k, const int32_t *items,
+                          const int32_t *num_items, int32_t max_items, int32_t item_rows,
+                          uint8_t *act, float *act_scales, void *stream);
+
+/*
+ * A11  Tiled grouped FC2 for real contractions.  Replaces Fish
+ * fused_moe_gemm's FC2 as driven by native_moe (src/drama3/kernels.py:
+ * 764-778) before the combine: for every work item the sorted rows
+ * [start, start+n) of act fp8 [act_rows, intermediate] (act_scales
+ * [act_rows, intermediate/128]) contract with w2[e] (fp8 [hidden, I]) and
+ * are stored fp32 by pair sorted_ids[p]: down [pairs, hidden] (unpermute).
+ * Equal to d3_expert_gemm mode 1 with exact_routes 0, bit for bit.
+ * item_rows: upper bound on the routes of one item, <= 128.
+ * intermediate in {256, 512, 768, 1024, 1536, 2048}; hidden a multiple of 256.
+ */
+int d3_grouped_fc2(const uint8_t *w2, const float *s2, int32_t weight_layout,
+                   int32_t num_experts, int32_t hidden, int32_t intermediate, const uint8_t *act,
+                   int64_t act_rows, const float *act_scales, const int32_t *sorted_ids,
+                   int32_t top_k, const int32_t *items, const int32_t *num_items,
+                   int32_t max_items, int32_t item_rows, float *down, void *stream);
 
 /*
  * A9/A11 weight preparation (once, at load time).

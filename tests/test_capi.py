@@ -16,7 +16,7 @@ def declared_functions():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     out = {}
-    for match in re.finditer(r"\b(?:int|int32_t|const char \*)\s*(d3_\w+)\s*\(([^)]*)\)\s*;", text):
+    for match in re.finditer(r"\b(?:int|int32_t|int64_t|const char \*)\s*(d3_\w+)\s*\(([^)]*)\)\s*;", text):
         params = match.group(2).strip()
         out[match.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
     return out
@@ -46,10 +46,10 @@ def test_definitions_match_header_parameter_order():
     the names of every extern "C" definition with its declaration."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     declared = {m.group(1): _params(m.group(2)) for m in re.finditer(
-        r"\b(?:int|int32_t|const char \*)\s*(d3_\w+)\s*\(([^)]*)\)\s*;", text)}
+        r"\b(?:int|int32_t|int64_t|const char \*)\s*(d3_\w+)\s*\(([^)]*)\)\s*;", text)}
     defined = {}
     for src in (ROOT / "drama-3-single-b300-inference_amd" / "csrc").glob("*.*"):
-        for m in re.finditer(r'extern "C" (?:int|int32_t|const char\*) (d3_\w+)\(([^)]*)\)\s*\{',
+        for m in re.finditer(r'extern "C" (?:int|int32_t|int64_t|const char\*) (d3_\w+)\(([^)]*)\)\s*\{',
                              src.read_text()):
             defined[m.group(1)] = _params(m.group(2))
     assert set(defined) == set(declared)

@@ -1,0 +1,121 @@
+"""Tiled grouped FP8 GEMMs (d3_grouped_fc1_swiglu, d3_grouped_fc2) against
+the chain they replace on contraction-sized work items: d3_expert_gemm on its
+FP8 path (exact_routes 0) followed by d3_silu_mul_quant, and d3_expert_gemm
+FC2.  Same MFMA per K block and the same rescale order, so the fp8 codes and
+scales of the activations and the fp32 down rows must be identical, byte for
+byte, for both weight layouts; end-to-end parity with the CPU oracle is in
+test_gpu_moe (configs 4 and 5 run these kernels)."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import CONTRACTION, assert_bf16_close, np_bf16, np_f32, oracle_weights
+from oracle import moe as om
+
+pytestmark = pytest.mark.gpu
+
+
+def _workload(rows, experts, hidden, intermediate, seed):
+    from drama3_amd import workloads
+
+    gen = torch.Generator("cpu").manual_seed(seed)
+    w = workloads.make_experts(gen, experts, hidden, intermediate)
+    x = workloads._bf16(gen, (rows, hidden))
+    logits = workloads._bf16(gen, (rows, experts))
+    return w, x, logits
+
+
+def _live_positions(ws):
+    total = int(ws.total.item())
+    pairs = int(ws.pairs_dev.item())
+    sorted_ids = ws.sorted_ids[:total]
+    return torch.nonzero(sorted_ids < pairs).flatten()
+
+
+@pytest.mark.parametrize("item_rows", [64, 128])
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("shape", [(3668, 128, 2048, 768), (560, 16, 1024, 256)],
+                         ids=["c4_shapes", "c5_shapes"])
+def test_grouped_matches_fp8_chain(device, shape, packed, item_rows):
+    """Items of up to 64 routes leave half of every tile empty; 128 fill it."""
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.pipeline import MoEWorkspace, Shape
+
+    rows, e, h, i = shape
+    w, x, logits = _workload(rows, e, h, i, seed=11)
+    experts = w.to(device)
+    if packed:
+        prepare_experts(experts)
+    ws = MoEWorkspace(Shape(rows, e, h, i), device, item_rows=item_rows, grouped=True)
+    assert ws.grouped and ws.item_rows == item_rows
+    ws.front(x.to(device), logits.to(device))
+    live = _live_positions(ws)
+    print(f"rows {rows} E {e} H {h} I {i} packed {packed} item_rows {item_rows}: "
+          f"{live.numel()} routes, "
+          f"{int(ws.num_items.item())} items", flush=True)
+
+    ws.exact_routes = 0  # every item on the FP8 path of d3_expert_gemm
+    ws.fc1(experts)
+    ws.activation()
+    ws.fc2(experts)
+    torch.cuda.synchronize()
+    act_ref = ws.act[live].clone()
+    scales_ref = ws.act_scales[live].clone()
+    down_ref = ws.down.clone()
+
+    ws.act.zero_()
+    ws.act_scales.zero_()
+    ws.down.zero_()
+    ws.grouped_fc1(experts)
+    torch.cuda.synchronize()
+    assert torch.equal(ws.act[live], act_ref), "activation codes differ"
+    assert torch.equal(ws.act_scales[live].view(torch.int32), scales_ref.view(torch.int32))
+    ws.grouped_fc2(experts)
+    torch.cuda.synchronize()
+    assert torch.equal(ws.down.view(torch.int32), down_ref.view(torch.int32)), "down rows differ"
+
+
+def test_grouped_dense_expert_matches_fp8_chain(device):
+    """The shared expert (identity routes, top_k 1) through both chains."""
+    from drama3_amd.pipeline import DenseExpert, MoEWorkspace, Shape
+
+    rows, h, i = 1000, 2048, 768
+    w, x, logits = _workload(rows, 1, h, i, seed=12)
+    shared = w.to(device)
+    ws = MoEWorkspace(Shape(rows, 1, h, i), device)
+    ws.quantize(x.to(device))
+    old = DenseExpert(rows, h, i, device, exact_routes=0, grouped=False)
+    new = DenseExpert(rows, h, i, device)
+    assert new.grouped
+    ref = old.forward(ws.q, ws.x_scales, shared).clone()
+    got = new.forward(ws.q, ws.x_scales, shared)
+    torch.cuda.synchronize()
+    assert torch.equal(old.act, new.act) and torch.equal(old.act_scales, new.act_scales)
+    assert torch.equal(got.view(torch.int32), ref.view(torch.int32))
+
+
+def test_grouped_partial_items_and_oracle(device):
+    """Ragged items (an expert with 1 route, items of 1..128 routes) end to
+    end against the CPU oracle."""
+    from drama3_amd.pipeline import MoEWorkspace, Shape
+
+    rows, e, h, i = 300, 16, 1024, 256
+    w, x, logits = _workload(rows, e, h, i, seed=13)
+    # one dominant expert and one expert reached by a single route
+    logits = logits.float()
+    logits[:, 3] += 6.0
+    logits[:, 9] -= 20.0
+    logits[0, 9] = 40.0
+    logits = logits.to(torch.bfloat16)
+    experts = w.to(device)
+    ws = MoEWorkspace(Shape(rows, e, h, i), device)
+    assert ws.grouped
+    out = ws.forward(x.to(device), logits.to(device), experts)
+    torch.cuda.synchronize()
+    counts = ws.counts.cpu().numpy()
+    assert counts[9] == 1 and counts[3] == rows
+    weights, ids = om.route(np_f32(logits))
+    expected = om.expert_ffn(np_bf16(x), ids, weights, oracle_weights(w))
+    stats = assert_bf16_close(np_bf16(out), expected, **CONTRACTION)
+    print(f"ragged items: {stats}")
