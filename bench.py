@@ -48,6 +48,11 @@ def parse():
                    help="time the one-launch step (d3_moe_decode_step) instead of the kernel chain")
     p.add_argument("--cpu-sample-steps", type=int, default=3,
                    help="oracle steps timed for cpu_baseline (about 5 s each on 8 cores)")
+    p.add_argument("--no-prefill", action="store_true",
+                   help="skip the config-4 packed-prefill measurement")
+    p.add_argument("--prefill-only", action="store_true",
+                   help="measure only the config-4 packed prefill (one JSON line)")
+    p.add_argument("--prefill-steps", type=int, default=20)
     return p.parse_args()
 
 
@@ -93,6 +98,78 @@ def cpu_baseline(workload, step, samples):
     return float(np.median(times)) * 1e6, threads, out
 
 
+def bench_prefill(torch, steps: int, copies: int = 2) -> dict:
+    """Config 4: 16 packed prompts (~3.7k rows), routed top-8 FP8 MoE (H2048,
+    E128, I768) plus a dense FP8 shared expert: route + quantise, wide route
+    sort, shared expert, tiled grouped FC1 (SwiGLU requant in its epilogue)
+    and FC2, weighted combine with the shared output added.  Graph-captured
+    steps rotate over `copies` weight copies (1.2 GB > the 256 MB MALL)."""
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.pipeline import DenseExpert, MoEWorkspace, Shape
+
+    device = torch.device("cuda:0")
+    w = workloads.config4()
+    step = w.steps[0]
+    x, logits = step.packed()
+    rows = len(x)
+    ws = MoEWorkspace(Shape(rows, w.num_experts, w.hidden, w.intermediate), device)
+    dense = DenseExpert(rows, w.hidden, w.shared.intermediate, device)
+    sets = []
+    for c in range(copies):
+        routed, shared = w.experts.to(device), w.shared.to(device)
+        sets.append((prepare_experts(routed), prepare_experts(shared)))
+    xd, ld = x.to(device), logits.to(device)
+
+    def full(routed, shared):
+        ws.front(xd, ld)
+        y = dense.forward(ws.q, ws.x_scales, shared)
+        return ws.experts(routed, shared=y)
+
+    def graph_us(fns, reps):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                for fn in fns:
+                    fn()
+        g.replay()
+        torch.cuda.synchronize()
+        return time_graphs(torch, [g], max(1, steps // reps)) / (reps * len(fns))
+
+    for routed, shared in sets:
+        full(routed, shared)
+    torch.cuda.synchronize()
+    step_us = graph_us([lambda r=r, s=s: full(r, s) for r, s in sets], 2)
+    stage_us = {
+        "route_quantize": graph_us([lambda: ws.front(xd, ld)], 4),
+        "sort": graph_us([ws.sort], 4),
+        "shared_expert": graph_us([lambda s=s: dense.forward(ws.q, ws.x_scales, s) for _, s in sets], 2),
+        "fc1_swiglu": graph_us([lambda r=r: ws.grouped_fc1(r) for r, _ in sets], 2),
+        "fc2": graph_us([lambda r=r: ws.grouped_fc2(r) for r, _ in sets], 2),
+        "combine": graph_us([lambda: ws.combine(None, None, dense.down)], 4),
+    }
+    stage_us["route_quantize"] -= stage_us["sort"]  # front() = route + quantise, then the sort
+    used = int(torch.unique(ws.ids).numel())
+    flop = workloads.flops(w, rows)
+    nbytes = workloads.algorithmic_bytes(w, step, used)
+    h, i = w.hidden, w.intermediate
+    routes = rows * workloads.TOP_K
+    fc1_flop, fc2_flop = 2 * routes * 2 * i * h, 2 * routes * i * h
+    tflops = flop / step_us / 1e6
+    return {
+        "workload": w.name, "rows": rows, "sequences": len(step.cu_seqlens) - 1,
+        "us_per_step": round(step_us, 2), "tokens_per_s": round(rows / (step_us * 1e-6), 1),
+        "TFLOP_s": round(tflops, 1), "mfma_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
+        "GB_s": round(nbytes / step_us / 1e3, 1), "hbm_frac": round(nbytes / step_us / 1e3 / HBM_PEAK_GBS, 4),
+        "flop_per_step": flop, "algorithmic_bytes_per_step": nbytes, "used_experts": used,
+        "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
+        "fc1_TFLOP_s": round(fc1_flop / stage_us["fc1_swiglu"] / 1e6, 1),
+        "fc2_TFLOP_s": round(fc2_flop / stage_us["fc2"] / 1e6, 1),
+        "peak_TFLOP_s": FP8_PEAK_TFLOPS, "dtype": "fp8_e4m3 MFMA (fp32 accumulate)",
+        "timing": f"hipGraph, {copies} rotated weight copies (routed + shared, fragment-major)",
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -105,6 +182,10 @@ def main():
     from drama3_amd import workloads
     from drama3_amd.expert_weights import prepare_experts
     from drama3_amd.pipeline import DecodeStep
+
+    if args.prefill_only:
+        print(json.dumps({"prefill": bench_prefill(torch, args.prefill_steps)}), flush=True)
+        return
 
     device = torch.device("cuda:0")
     w = workloads.config2()
@@ -238,6 +319,8 @@ def main():
                          "is the BLAS thread pool, the element-wise numpy work runs on one",
                "host_cpus": len(os.sched_getaffinity(0))}
 
+    prefill = None if args.no_prefill else bench_prefill(torch, args.prefill_steps)
+
     result = {
         "metric": baseline_metric(),
         "value": round(step_gbs, 1),
@@ -282,6 +365,7 @@ def main():
         "device_copy_GB_s": round(copy_gbs, 1),
         "cpu_baseline": cpu,
         "parity": parity,
+        "prefill": prefill,
     }
     print(json.dumps(result), flush=True)
 

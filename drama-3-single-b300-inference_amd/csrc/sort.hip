@@ -36,7 +36,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_routes_kernel(
 // Scratch: chunk histograms [chunks][E] and ranks [pairs] (int32).
 // ---------------------------------------------------------------------------
 constexpr int kWideThreads = 256;
-constexpr int kWideChunk = 2048;
+constexpr int kWideChunk = 512;
 constexpr int kWideScanLds = 12288;  // chunk histogram cells staged in LDS (48 KiB)
 
 template <bool kI64>

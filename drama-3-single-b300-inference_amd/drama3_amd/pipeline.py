@@ -46,7 +46,7 @@ GROUPED_ROUTES = 128  # most routes per work item of the tiled grouped GEMMs
 GROUPED_ITEM_ROUTES = 128  # their default item size
 # Up to this many (row, rank) pairs the route sort runs inside the fused front
 # kernel (its last workgroup); larger batches use the 1024-thread sort kernel,
-# and from WIDE_SORT_PAIRS on the wide sort (one workgroup per 2048 pairs).
+# and from WIDE_SORT_PAIRS on the wide sort (one workgroup per 512 pairs).
 FUSED_SORT_PAIRS = 8192
 WIDE_SORT_PAIRS = 8192
 

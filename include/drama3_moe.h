@@ -159,7 +159,7 @@ int d3_moe_front(const uint8_t *occupancy, int32_t num_slots, int32_t *active_sl
 
 /*
  * A5-A7  The same histogram / offsets / stable sort as d3_sort_routes, for
- * prefill-sized batches: the ranking is spread over one workgroup per 2048
+ * prefill-sized batches: the ranking is spread over one workgroup per 512
  * pairs (three launches) instead of one workgroup walking every pair.
  * Same arguments and outputs as d3_sort_routes (starts is required), plus a
  * caller-owned int32 scratch of d3_sort_wide_scratch_ints(rows, top_k, E)

@@ -1,4 +1,4 @@
-"""The wide route sort (d3_sort_routes_wide: one workgroup per 2048 pairs)
+"""The wide route sort (d3_sort_routes_wide: one workgroup per 512 pairs)
 against the CPU oracle, bit for bit: histogram, padded offsets, stable
 sorted pair list with sentinel padding, expert ids, inverse map and work
 items, at prefill sizes, under skew, for int64 ids, with a device row count
