@@ -22,11 +22,13 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round to nearest even; NaN stays a quiet NaN.
+// Round to nearest even; NaN stays a quiet NaN.  Written as a select: an
+// early return for NaN compiles to a divergent branch per value.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t b = __float_as_uint(f);
-  if ((b & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((b >> 16) | 0x40u);
-  return static_cast<uint16_t>((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+  const uint32_t b = __float_as_uint(f);
+  const uint32_t rounded = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+  const uint32_t quiet = (b >> 16) | 0x40u;
+  return static_cast<uint16_t>((b & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
 // ---------------------------------------------------------------------------

@@ -99,9 +99,10 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   const float* wsexp = ws + static_cast<size_t>(expert) * (n_rows / kGroup) * KB;
 
   // Weight fragments through a buffer view of the expert: the lane offset
-  // is one VGPR, the tile / K block offset a wave-uniform scalar.  The
-  // fragment-major loads are non-temporal (every weight byte is read once).
-  constexpr int kNonTemporal = 2;
+  // is one VGPR, the tile / K block offset a wave-uniform scalar.  Loads are
+  // not marked non-temporal: an expert's other items read the same weights
+  // from L2 shortly after (measured: 18 % less L2 fetch than with nt).
+  constexpr int kNonTemporal = 0;
   const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(wexp), 0, static_cast<uint32_t>(n_rows) * K, 0x00020000);
   const uint32_t w_lane = kPacked ? lane * 16 : row16 * K + group * 16;

@@ -512,8 +512,10 @@ class DecodeStep:
         self.slots = slots
         self.active = torch.empty(slots, dtype=torch.int32, device=dev)
         self.count = torch.empty(1, dtype=torch.int32, device=dev)
+        # Decode items take the exact path of the expert GEMMs (never the
+        # FP8-only tiled grouped GEMMs of prefill-sized batches).
         self.workspace = MoEWorkspace(Shape(slots, num_experts, hidden, intermediate, top_k), dev,
-                                      item_rows=item_rows)
+                                      item_rows=item_rows, grouped=False)
         # Sortless expert GEMMs (default when the slots' routes cover the
         # experts densely: at least 4 routes per expert at full occupancy,
         # and the shapes are in the compiled set) on fragment-major weights.
