@@ -30,10 +30,10 @@
 //     FP8 path.
 //   * FC1 (mode 0): a workgroup covers 128 gate rows and the 128 matching up
 //     rows, so each lane holds gate and up of the same columns: the epilogue
-//     rounds both to bf16 (the reference's FC1 output), computes SwiGLU,
-//     reduces the per-(route, 128-column) amax across lanes and waves and
-//     writes the e4m3 codes and scale, the bytes d3_silu_mul_quant would
-//     write.  FC2 (mode 1) stores fp32 rows by pair (the unpermute).
+//     rounds both to bf16 (the reference's FC1 output), computes SwiGLU
+//     (swiglu_value), reduces the per-(route, 128-column) amax across lanes
+//     and waves and writes the e4m3 codes and scale, the bytes
+//     d3_silu_mul_quant would write.  FC2 (mode 1) stores fp32 rows by pair (the unpermute).
 //   * Workgroups are grouped so that two consecutive items' tiles run on one
 //     XCD together: an item's tiles share its activation rows, and an
 //     expert's consecutive items its weights, in that XCD's L2.
@@ -263,8 +263,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
         for (int i = 0; i < 4; ++i) {
           const float g = bf16_to_f32(f32_to_bf16(acc[p][rt][i]));
           const float u = bf16_to_f32(f32_to_bf16(acc[2 + p][rt][i]));
-          const float sig = 1.0f / (1.0f + expf(-g));
-          const float a = (g * sig) * u;
+          const float a = swiglu_value(g, u);
           v[rt][4 * p + i] = a;
           amax = fmaxf(amax, fabsf(a));
         }
@@ -283,9 +282,10 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
       for (int q = 1; q < kGgWaves; ++q) amax = fmaxf(amax, amax_part[q][route]);
       const float scale = group_scale(amax);
+      const float inv = __builtin_amdgcn_rcpf(scale);
       uint8_t* dst = out_codes + static_cast<size_t>(position) * out_cols + n0 + 32 * wave + 4 * group;
-      *reinterpret_cast<uint32_t*>(dst) = quantize_four(&v[rt][0], scale);
-      *reinterpret_cast<uint32_t*>(dst + 16) = quantize_four(&v[rt][4], scale);
+      *reinterpret_cast<uint32_t*>(dst) = requantize_four(&v[rt][0], inv);
+      *reinterpret_cast<uint32_t*>(dst + 16) = requantize_four(&v[rt][4], inv);
       if (wave == 0 && group == 0) out_scales[static_cast<size_t>(position) * groups + tile] = scale;
     }
   }
