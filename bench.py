@@ -101,20 +101,22 @@ def cpu_baseline(workload, step, samples):
 def bench_prefill(torch, steps: int, copies: int = 2) -> dict:
     """Config 4: 16 packed prompts (~3.7k rows), routed top-8 FP8 MoE (H2048,
     E128, I768) plus a dense FP8 shared expert: route + quantise, wide route
-    sort, shared expert, tiled grouped FC1 (SwiGLU requant in its epilogue)
-    and FC2, weighted combine with the shared output added.  Graph-captured
-    steps rotate over `copies` weight copies (1.2 GB > the 256 MB MALL)."""
+    sort, tiled grouped FC1 (SwiGLU requant in its epilogue) and FC2 with the
+    shared expert's rows as extra items of the same launches, weighted combine
+    with the shared output added.  Graph-captured steps rotate over `copies`
+    weight copies (1.2 GB > the 256 MB MALL)."""
     from drama3_amd import workloads
     from drama3_amd.expert_weights import prepare_experts
-    from drama3_amd.pipeline import DenseExpert, MoEWorkspace, Shape
+    from drama3_amd.pipeline import MoEWorkspace, Shape, moe_with_shared
 
     device = torch.device("cuda:0")
     w = workloads.config4()
     step = w.steps[0]
     x, logits = step.packed()
     rows = len(x)
-    ws = MoEWorkspace(Shape(rows, w.num_experts, w.hidden, w.intermediate), device)
-    dense = DenseExpert(rows, w.hidden, w.shared.intermediate, device)
+    # the shared expert's rows ride in the routed launches (shared_rows)
+    ws = MoEWorkspace(Shape(rows, w.num_experts, w.hidden, w.intermediate), device,
+                      shared_rows=rows)
     sets = []
     for c in range(copies):
         routed, shared = w.experts.to(device), w.shared.to(device)
@@ -122,9 +124,7 @@ def bench_prefill(torch, steps: int, copies: int = 2) -> dict:
     xd, ld = x.to(device), logits.to(device)
 
     def full(routed, shared):
-        ws.front(xd, ld)
-        y = dense.forward(ws.q, ws.x_scales, shared)
-        return ws.experts(routed, shared=y)
+        return moe_with_shared(ws, None, xd, ld, routed, shared)
 
     def graph_us(fns, reps):
         g = torch.cuda.CUDAGraph()
@@ -143,17 +143,16 @@ def bench_prefill(torch, steps: int, copies: int = 2) -> dict:
     stage_us = {
         "route_quantize": graph_us([lambda: ws.front(xd, ld)], 4),
         "sort": graph_us([ws.sort], 4),
-        "shared_expert": graph_us([lambda s=s: dense.forward(ws.q, ws.x_scales, s) for _, s in sets], 2),
-        "fc1_swiglu": graph_us([lambda r=r: ws.grouped_fc1(r) for r, _ in sets], 2),
-        "fc2": graph_us([lambda r=r: ws.grouped_fc2(r) for r, _ in sets], 2),
-        "combine": graph_us([lambda: ws.combine(None, None, dense.down)], 4),
+        "fc1_swiglu": graph_us([lambda r=r, s=s: ws.grouped_fc1(r, s) for r, s in sets], 2),
+        "fc2": graph_us([lambda r=r, s=s: ws.grouped_fc2(r, s) for r, s in sets], 2),
+        "combine": graph_us([lambda: ws.combine(None, None, ws.shared_down)], 4),
     }
     stage_us["route_quantize"] -= stage_us["sort"]  # front() = route + quantise, then the sort
     used = int(torch.unique(ws.ids).numel())
     flop = workloads.flops(w, rows)
     nbytes = workloads.algorithmic_bytes(w, step, used)
     h, i = w.hidden, w.intermediate
-    routes = rows * workloads.TOP_K
+    routes = rows * workloads.TOP_K + rows  # routed pairs + the shared expert's rows
     fc1_flop, fc2_flop = 2 * routes * 2 * i * h, 2 * routes * i * h
     tflops = flop / step_us / 1e6
     return {

@@ -55,13 +55,25 @@ constexpr int kGgStage = kGgRoutes * kGgStride;
 constexpr int kGgStaged = kGgRoutes * kGroup / (16 * kGgThreads);  // 16-byte copies per thread and K block
 constexpr int kGgXcds = 8;
 
+// A dense shared expert folded into the routed launch: items after the
+// routed ones cover its rows [128 j, 128 j + 128) with identity routes and
+// its own weights.  FC1 reads q row r and writes act row pos + r; FC2 reads
+// act row pos + r and writes fp32 row pair + r.
+struct SharedItems {
+  const uint8_t* w;  // nullptr: none
+  const float* ws;
+  int rows;
+  int pos;
+  int pair;
+};
+
 template <int KB, int MODE, bool kPacked>
 __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2))) void grouped_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows, int out_cols,
     const uint8_t* __restrict__ act, uint32_t act_bytes, const float* __restrict__ act_scales,
     const int32_t* __restrict__ sorted_ids, int top_k, const int4* __restrict__ items,
-    const int32_t* __restrict__ num_items, int n_tiles, int chunk, uint8_t* __restrict__ out_codes,
-    float* __restrict__ out_scales, float* __restrict__ out_f32) {
+    const int32_t* __restrict__ num_items, int max_items, SharedItems shared, int n_tiles, int chunk,
+    uint8_t* __restrict__ out_codes, float* __restrict__ out_scales, float* __restrict__ out_f32) {
   constexpr int K = KB * kGroup;
   __shared__ __attribute__((aligned(16))) uint8_t stage[2][kGgStage];
   __shared__ float a_scale[KB][kGgRoutes];
@@ -75,11 +87,19 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   const int logical = ((j / chunk) * kGgXcds + xcd) * chunk + j % chunk;
   const int item_index = logical / n_tiles;
   const int tile = logical % n_tiles;
-  if (item_index >= *num_items) return;
-  const int4 item = items[item_index];
-  const int expert = item.x;
-  const int first = item.y;
-  const int routes = min(item.z, kGgRoutes);
+  const bool dense = item_index >= max_items;  // a shared-expert item (uniform)
+  int expert = 0, first, routes;
+  if (!dense) {
+    if (item_index >= *num_items) return;
+    const int4 item = items[item_index];
+    expert = item.x;
+    first = item.y;
+    routes = min(item.z, kGgRoutes);
+  } else {
+    first = (item_index - max_items) * kGgRoutes;
+    if (first >= shared.rows) return;
+    routes = min(kGgRoutes, shared.rows - first);
+  }
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -95,8 +115,8 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     else
       return n0 + 64 * wave + 16 * t;
   };
-  const uint8_t* wexp = w + static_cast<size_t>(expert) * n_rows * K;
-  const float* wsexp = ws + static_cast<size_t>(expert) * (n_rows / kGroup) * KB;
+  const uint8_t* wexp = dense ? shared.w : w + static_cast<size_t>(expert) * n_rows * K;
+  const float* wsexp = dense ? shared.ws : ws + static_cast<size_t>(expert) * (n_rows / kGroup) * KB;
 
   // Weight fragments through a buffer view of the expert: the lane offset
   // is one VGPR, the tile / K block offset a wave-uniform scalar.  Loads are
@@ -128,19 +148,23 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   load_weights(0);  // depends on the item only
 
   // Route rows of the item, loaded branch-free (a dead route reads the
-  // item's first id and is masked afterwards): one round trip.
-  auto route_row = [&](int r, int id) { return MODE == 0 ? id / top_k : first + r; };
+  // item's first id and is masked afterwards): one round trip.  Shared-expert
+  // items map row r of the item to token first + r.
+  auto route_row = [&](int r, int id) {
+    if (dense) return MODE == 0 ? first + r : shared.pos + first + r;
+    return MODE == 0 ? id / top_k : first + r;
+  };
   const int part = tid & 7;
   const int r0 = tid >> 3;
   int ids[kGgStaged];
 #pragma unroll
   for (int i = 0; i < kGgStaged; ++i) {
     const int r = r0 + (kGgThreads / 8) * i;
-    ids[i] = sorted_ids[first + (r < routes ? r : 0)];
+    ids[i] = dense ? 0 : sorted_ids[first + (r < routes ? r : 0)];
   }
   const int rs = tid % kGgRoutes;       // route of this thread's scales / target
   const int k0 = tid / kGgRoutes;       // first K block of its scales
-  const int id_s = sorted_ids[first + (rs < routes ? rs : 0)];
+  const int id_s = dense ? 0 : sorted_ids[first + (rs < routes ? rs : 0)];
 
   // Staging: thread t copies 16 bytes (chunk t % 8 of the K block) of routes
   // t / 8 + 32 i.  Dead routes read past the buffer (zeros).
@@ -174,7 +198,9 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     for (int q = 0; q * kSplit + k0 < KB; ++q) sc[q] = srow[q * kSplit + k0];
 #pragma unroll
     for (int q = 0; q * kSplit + k0 < KB; ++q) a_scale[q * kSplit + k0][rs] = live ? sc[q] : 0.0f;
-    if (k0 == 0) target[rs] = live ? (MODE == 0 ? first + rs : id_s) : -1;
+    int t = MODE == 0 ? first + rs : id_s;
+    if (dense) t = (MODE == 0 ? shared.pos : shared.pair) + first + rs;
+    if (k0 == 0) target[rs] = live ? t : -1;
   }
   // Block scales of the wave's tiles for every K block (wave-uniform): FC1
   // tiles 0-1 (gate) share one 128-row block and tiles 2-3 (up) another; a
@@ -307,6 +333,7 @@ struct GroupedLaunch {
   const int32_t* num_items;
   int max_items;
   int item_rows;
+  SharedItems shared;
   uint8_t* codes;
   float* scales;
   float* out;
@@ -317,12 +344,13 @@ void launch_grouped(const GroupedLaunch& g, hipStream_t s) {
   const int n_tiles = MODE == 0 ? g.out_cols / kGroup : g.n_rows / kGgRows;
   // Two consecutive items' tiles per XCD run.
   const int chunk = 2 * n_tiles;
-  const int64_t logical = static_cast<int64_t>(g.max_items) * n_tiles;
+  const int shared_items = g.shared.w ? (g.shared.rows + kGgRoutes - 1) / kGgRoutes : 0;
+  const int64_t logical = (static_cast<int64_t>(g.max_items) + shared_items) * n_tiles;
   const int64_t per_round = static_cast<int64_t>(kGgXcds) * chunk;
   const int blocks = static_cast<int>((logical + per_round - 1) / per_round * per_round);
 #define D3_GG_ARGS dim3(blocks), dim3(kGgThreads), 0, s, g.w, g.ws, g.n_rows, g.out_cols, g.a, \
-                   g.a_bytes, g.as, g.sorted_ids, g.top_k, g.items, g.num_items, n_tiles, chunk, \
-                   g.codes, g.scales, g.out
+                   g.a_bytes, g.as, g.sorted_ids, g.top_k, g.items, g.num_items, g.max_items, \
+                   g.shared, n_tiles, chunk, g.codes, g.scales, g.out
   if (g.layout == D3_LAYOUT_FRAGMENT)
     hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true>), D3_GG_ARGS);
   else
@@ -371,19 +399,26 @@ extern "C" int d3_grouped_fc1_swiglu(const uint8_t* w13, const float* s13, int32
                                      const uint8_t* q, int64_t q_rows, const float* x_scales,
                                      const int32_t* sorted_ids, int32_t top_k, const int32_t* items,
                                      const int32_t* num_items, int32_t max_items,
-                                     int32_t item_rows, uint8_t* act, float* act_scales,
+                                     int32_t item_rows, const uint8_t* shared_w13,
+                                     const float* shared_s13, int32_t shared_rows,
+                                     int32_t shared_act_row, uint8_t* act, float* act_scales,
                                      void* stream) {
   D3_REQUIRE(act && act_scales, "grouped_fc1_swiglu: null output");
+  D3_REQUIRE(!shared_w13 || (shared_s13 && shared_rows >= 0 && shared_rows <= q_rows &&
+                             shared_act_row >= 0 && aligned_to(shared_w13, 16)),
+             "grouped_fc1_swiglu: shared expert needs scales, 0 <= rows <= q_rows, a row offset "
+             "and 16-byte aligned weights");
   D3_REQUIRE(intermediate > 0 && intermediate % kGroup == 0,
              "grouped_fc1_swiglu: intermediate %d must be a multiple of 128", intermediate);
   D3_REQUIRE(aligned_to(act, 4), "grouped_fc1_swiglu: act must be 4-byte aligned");
   const GroupedLaunch g{0, weight_layout, w13, s13, 2 * intermediate, intermediate, q,
                         static_cast<uint32_t>(q_rows * hidden), x_scales, sorted_ids, top_k,
-                        reinterpret_cast<const int4*>(items), num_items, max_items, item_rows, act,
+                        reinterpret_cast<const int4*>(items), num_items, max_items, item_rows,
+                        SharedItems{shared_w13, shared_s13, shared_rows, shared_act_row, 0}, act,
                         act_scales, nullptr};
   int status = check_grouped(g, num_experts, hidden, q_rows, "grouped_fc1_swiglu");
   if (status != D3_OK) return status;
-  if (max_items == 0) {
+  if (max_items == 0 && !(shared_w13 && shared_rows > 0)) {
     clear_error();
     return D3_OK;
   }
@@ -397,18 +432,26 @@ extern "C" int d3_grouped_fc2(const uint8_t* w2, const float* s2, int32_t weight
                               const uint8_t* act, int64_t act_rows, const float* act_scales,
                               const int32_t* sorted_ids, int32_t top_k, const int32_t* items,
                               const int32_t* num_items, int32_t max_items, int32_t item_rows,
-                              float* down, void* stream) {
+                              const uint8_t* shared_w2, const float* shared_s2,
+                              int32_t shared_rows, int32_t shared_act_row,
+                              int32_t shared_out_row, float* down, void* stream) {
   D3_REQUIRE(down != nullptr, "grouped_fc2: null output");
+  D3_REQUIRE(!shared_w2 || (shared_s2 && shared_rows >= 0 && shared_act_row >= 0 &&
+                            static_cast<int64_t>(shared_act_row) + shared_rows <= act_rows &&
+                            shared_out_row >= 0 && aligned_to(shared_w2, 16)),
+             "grouped_fc2: shared expert needs scales, its act rows inside act_rows, an output "
+             "row offset and 16-byte aligned weights");
   D3_SUPPORTED(hidden > 0 && hidden % kGgRows == 0,
                "grouped_fc2: hidden %d must be a multiple of %d", hidden, kGgRows);
   D3_REQUIRE(aligned_to(down, 16), "grouped_fc2: down must be 16-byte aligned");
   const GroupedLaunch g{1, weight_layout, w2, s2, hidden, hidden, act,
                         static_cast<uint32_t>(act_rows * intermediate), act_scales, sorted_ids, top_k,
-                        reinterpret_cast<const int4*>(items), num_items, max_items, item_rows, nullptr,
-                        nullptr, down};
+                        reinterpret_cast<const int4*>(items), num_items, max_items, item_rows,
+                        SharedItems{shared_w2, shared_s2, shared_rows, shared_act_row, shared_out_row},
+                        nullptr, nullptr, down};
   int status = check_grouped(g, num_experts, intermediate, act_rows, "grouped_fc2");
   if (status != D3_OK) return status;
-  if (max_items == 0) {
+  if (max_items == 0 && !(shared_w2 && shared_rows > 0)) {
     clear_error();
     return D3_OK;
   }

@@ -60,9 +60,10 @@ SIGNATURES = {
     "d3_expert_tile_rows": (_i32, [_i32]),
     "d3_grouped_fc1_swiglu": (
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p,
-               _p]),
+               _i32, _i32, _p, _p, _p]),
     "d3_grouped_fc2": (
-        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p]),
+        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p,
+               _i32, _i32, _i32, _p, _p]),
     "d3_pack_expert_weights": (_i32, [_p, _i32, _i32, _i32, _p, _p]),
     "d3_expert_fc1_swiglu": (
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _p, _p,

@@ -107,7 +107,7 @@ class MoEWorkspace:
                  item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
                  exact_routes: int = EXACT_ROUTES, fused_epilogues: bool = False,
                  swiglu_in_fc2: bool | None = None, sortless: bool = False,
-                 grouped: bool | None = None):
+                 grouped: bool | None = None, shared_rows: int = 0):
         lib = _lib.load()
         self.shape = shape
         self.device = torch.device(device)
@@ -145,10 +145,15 @@ class MoEWorkspace:
         self.items = torch.empty((max(self.max_items, 1), 4), **i32)
         self.num_items = torch.empty(1, **i32)
         self.ticket = torch.zeros(1, **i32)  # fused-sort ticket: 0 between launches
+        # A dense shared expert folded into the tiled grouped launches takes
+        # shared_rows extra activation rows (after the sorted ones) and fp32
+        # output rows (after the pairs).
+        self.shared_rows = shared_rows
         self.gate_up = torch.empty((self.max_rows, 2 * i), dtype=torch.bfloat16, device=dev)
-        self.act = torch.empty((self.max_rows, i), dtype=torch.uint8, device=dev)
-        self.act_scales = torch.empty((self.max_rows, i // 128), dtype=torch.float32, device=dev)
-        self.down = torch.empty((pairs, h), dtype=torch.float32, device=dev)
+        self.act = torch.empty((self.max_rows + shared_rows, i), dtype=torch.uint8, device=dev)
+        self.act_scales = torch.empty((self.max_rows + shared_rows, i // 128), dtype=torch.float32,
+                                      device=dev)
+        self.down = torch.empty((pairs + shared_rows, h), dtype=torch.float32, device=dev)
         self.out = torch.empty((t, h), dtype=torch.bfloat16, device=dev)
         # Optional fused epilogues (SwiGLU requant in FC1, combine in FC2)
         # when the tiling allows; their tickets start at 0 and every launch
@@ -244,23 +249,45 @@ class MoEWorkspace:
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
              self.item_rows, self.exact_routes, ptr(self.gate_up), None, stream)
 
-    def grouped_fc1(self, experts, stream=None) -> None:
-        """Tiled grouped FC1 + SwiGLU requant: act / act_scales at sorted rows."""
+    def _shared_operands(self, shared, operands, layout):
+        if shared is None:
+            return None, None, 0
+        if self.shared_rows < self.shape.rows:
+            raise ValueError("fold a shared expert into a workspace built with shared_rows >= rows")
+        w, ws, shared_layout = operands(shared)
+        if shared_layout != layout:
+            raise ValueError("the shared expert's weights must use the routed experts' layout")
+        if w.shape[0] != 1:
+            raise ValueError("a shared expert is one [1, N, K] expert")
+        return w, ws, self.shape.rows
+
+    def grouped_fc1(self, experts, shared=None, stream=None) -> None:
+        """Tiled grouped FC1 + SwiGLU requant: act / act_scales at sorted rows
+        (and, with ``shared``, the dense shared expert's rows after them)."""
         s, stream = self.shape, self._stream(stream)
         w, ws, layout = fc1_operands(experts)
+        sw, sws, srows = self._shared_operands(shared, fc1_operands, layout)
         call("d3_grouped_fc1_swiglu", ptr(w), ptr(ws), layout, s.num_experts, s.intermediate,
              s.hidden, ptr(self.q), s.rows, ptr(self.x_scales), ptr(self.sorted_ids), s.top_k,
-             ptr(self.items), ptr(self.num_items), self.max_items, self.item_rows, ptr(self.act),
-             ptr(self.act_scales), stream)
+             ptr(self.items), ptr(self.num_items), self.max_items, self.item_rows, ptr(sw),
+             ptr(sws), srows, self.max_rows, ptr(self.act), ptr(self.act_scales), stream)
 
-    def grouped_fc2(self, experts, stream=None) -> None:
-        """Tiled grouped FC2: fp32 down rows by pair."""
+    def grouped_fc2(self, experts, shared=None, stream=None) -> None:
+        """Tiled grouped FC2: fp32 down rows by pair (and, with ``shared``, the
+        shared expert's rows after the pairs: ``shared_down``)."""
         s, stream = self.shape, self._stream(stream)
         w, ws, layout = fc2_operands(experts)
+        sw, sws, srows = self._shared_operands(shared, fc2_operands, layout)
         call("d3_grouped_fc2", ptr(w), ptr(ws), layout, s.num_experts, s.hidden, s.intermediate,
-             ptr(self.act), self.max_rows, ptr(self.act_scales), ptr(self.sorted_ids), s.top_k,
-             ptr(self.items), ptr(self.num_items), self.max_items, self.item_rows, ptr(self.down),
+             ptr(self.act), self.max_rows + self.shared_rows, ptr(self.act_scales),
+             ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
+             self.item_rows, ptr(sw), ptr(sws), srows, self.max_rows, s.pairs, ptr(self.down),
              stream)
+
+    @property
+    def shared_down(self) -> torch.Tensor:
+        """fp32 [rows, H] output of a folded shared expert."""
+        return self.down[self.shape.pairs:self.shape.pairs + self.shape.rows]
 
     def activation(self, stream=None) -> None:
         s, stream = self.shape, self._stream(stream)
@@ -303,8 +330,8 @@ class MoEWorkspace:
         self.quantize(x, row_index, row_count, stream)
         self.sort(ids, row_count, stream)
         if self.grouped:
-            self.grouped_fc1(experts, stream)
-            self.grouped_fc2(experts, stream)
+            self.grouped_fc1(experts, stream=stream)
+            self.grouped_fc2(experts, stream=stream)
         else:
             self.fc1(experts, stream)
             self._fc2_stage(experts, stream)
@@ -398,8 +425,8 @@ class MoEWorkspace:
             self.decode_fc2(experts, row_count, stream)
             return self.combine(None, row_count, shared, out, stream)
         if self.grouped:
-            self.grouped_fc1(experts, stream)
-            self.grouped_fc2(experts, stream)
+            self.grouped_fc1(experts, stream=stream)
+            self.grouped_fc2(experts, stream=stream)
             return self.combine(None, row_count, shared, out, stream)
         if self.fuse_fc1:
             self.fc1_swiglu(experts, stream)
@@ -452,11 +479,12 @@ class DenseExpert:
         if self.grouped:  # identity routes: top_k 1, sorted_ids = row
             call("d3_grouped_fc1_swiglu", ptr(w13), ptr(s13), layout13, 1, i, h, ptr(q),
                  q.shape[0], ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items),
-                 ptr(self.num_items), self.max_items, self.item_rows, ptr(self.act),
-                 ptr(self.act_scales), stream)
+                 ptr(self.num_items), self.max_items, self.item_rows, None, None, 0, 0,
+                 ptr(self.act), ptr(self.act_scales), stream)
             call("d3_grouped_fc2", ptr(w2), ptr(s2), layout2, 1, h, i, ptr(self.act), self.rows,
                  ptr(self.act_scales), ptr(self.sorted_ids), 1, ptr(self.items),
-                 ptr(self.num_items), self.max_items, self.item_rows, ptr(self.down), stream)
+                 ptr(self.num_items), self.max_items, self.item_rows, None, None, 0, 0, 0,
+                 ptr(self.down), stream)
             return self.down
         call("d3_expert_gemm", 0, ptr(w13), ptr(s13), layout13, 1, 2 * i, h, ptr(q),
              ptr(x_scales), ptr(self.sorted_ids), 1, ptr(self.items), ptr(self.num_items),
@@ -467,6 +495,50 @@ class DenseExpert:
              ptr(self.act_scales), ptr(self.sorted_ids), 1, ptr(self.items), ptr(self.num_items),
              self.max_items, self.item_rows, self.exact_routes, None, ptr(self.down), stream)
         return self.down
+
+
+def moe_with_shared(ws: MoEWorkspace, dense: DenseExpert | None, x, logits, experts,
+                    shared_experts, row_index=None, row_count=None, out=None,
+                    side: torch.cuda.Stream | None = None):
+    """Routed top-k experts plus an always-on dense shared expert, the shape of
+    the reference's ``moe_parts`` (``model.py:503-518``).  Returns ``out``
+    [rows, H] bf16: the combine of the routed rows plus the shared output.
+
+    With a tiled-grouped workspace built with ``shared_rows >= rows`` the
+    shared expert's rows are extra work items of the routed FC1 / FC2
+    launches (they fill those launches' last rounds instead of under-filling
+    launches of their own).  Otherwise ``dense`` runs it: on ``side`` (a
+    default-priority stream, as the reference runs its shared expert on a
+    side stream joined before the combine, ``model.py:506-517``) or in line.
+    Graph-capturable either way.
+    """
+    main = torch.cuda.current_stream(ws.device)
+    stream = main.cuda_stream
+    if ws.sortless:
+        raise ValueError("moe_with_shared needs a sorted-route workspace")
+    ws.front(x, logits, row_index, row_count, stream=stream)
+    if ws.grouped and ws.shared_rows >= ws.shape.rows:
+        ws.grouped_fc1(experts, shared_experts, stream=stream)
+        ws.grouped_fc2(experts, shared_experts, stream=stream)
+        return ws.combine(None, row_count, ws.shared_down, out, stream)
+    if dense is None:
+        raise ValueError("without a shared-expert workspace, pass a DenseExpert")
+    if side is None:
+        shared_y = dense.forward(ws.q, ws.x_scales, shared_experts, stream=stream)
+    else:
+        side.wait_stream(main)  # q / x_scales are ready
+        shared_y = dense.forward(ws.q, ws.x_scales, shared_experts, stream=side.cuda_stream)
+    if ws.grouped:
+        ws.grouped_fc1(experts, stream=stream)
+        ws.grouped_fc2(experts, stream=stream)
+    elif ws.fuse_fc1 or ws.fuse_fc2:
+        raise ValueError("moe_with_shared runs the unfused chain")
+    else:
+        ws.fc1(experts, stream)
+        ws._fc2_stage(experts, stream)
+    if side is not None:
+        main.wait_stream(side)
+    return ws.combine(None, row_count, shared_y, out, stream)
 
 
 def compact_slots(occupancy: torch.Tensor, active: torch.Tensor, count: torch.Tensor,

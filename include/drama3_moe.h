@@ -232,13 +232,20 @@ int32_t d3_expert_tile_rows(int32_t k);
  * FP8 path; act / act_scales equal d3_expert_gemm (mode 0, exact_routes 0)
  * followed by d3_silu_mul_quant, byte for byte.  hidden in {256, 512, 768,
  * 1024, 1536, 2048}; intermediate a multiple of 128.
+ * Optional dense shared expert in the same launch (the reference's moe_parts
+ * shared expert, src/drama3/model.py:503-518; shared_w13 NULL for none):
+ * fp8 [2I, hidden] in weight_layout with scales shared_s13, applied to q rows
+ * [0, shared_rows), its act / act_scales written at rows shared_act_row + r
+ * (act then needs max sorted rows + shared_rows rows).
  */
 int d3_grouped_fc1_swiglu(const uint8_t *w13, const float *s13, int32_t weight_layout,
                           int32_t num_experts, int32_t intermediate, int32_t hidden,
                           const uint8_t *q, int64_t q_rows, const float *x_scales,
                           const int32_t *sorted_ids, int32_t top_k, const int32_t *items,
                           const int32_t *num_items, int32_t max_items, int32_t item_rows,
-                          uint8_t *act, float *act_scales, void *stream);
+                          const uint8_t *shared_w13, const float *shared_s13,
+                          int32_t shared_rows, int32_t shared_act_row, uint8_t *act,
+                          float *act_scales, void *stream);
 
 /*
  * A11  Tiled grouped FC2 for real contractions.  Replaces Fish
@@ -250,12 +257,18 @@ int d3_grouped_fc1_swiglu(const uint8_t *w13, const float *s13, int32_t weight_l
  * Equal to d3_expert_gemm mode 1 with exact_routes 0, bit for bit.
  * item_rows: upper bound on the routes of one item, <= 128.
  * intermediate in {256, 512, 768, 1024, 1536, 2048}; hidden a multiple of 256.
+ * Optional dense shared expert (shared_w2 NULL for none): act rows
+ * shared_act_row + r, r < shared_rows, contract with shared_w2 (fp8 [hidden,
+ * I] in weight_layout, scales shared_s2) into fp32 rows shared_out_row + r
+ * of down.
  */
 int d3_grouped_fc2(const uint8_t *w2, const float *s2, int32_t weight_layout,
                    int32_t num_experts, int32_t hidden, int32_t intermediate, const uint8_t *act,
                    int64_t act_rows, const float *act_scales, const int32_t *sorted_ids,
                    int32_t top_k, const int32_t *items, const int32_t *num_items,
-                   int32_t max_items, int32_t item_rows, float *down, void *stream);
+                   int32_t max_items, int32_t item_rows, const uint8_t *shared_w2,
+                   const float *shared_s2, int32_t shared_rows, int32_t shared_act_row,
+                   int32_t shared_out_row, float *down, void *stream);
 
 /*
  * A9/A11 weight preparation (once, at load time).

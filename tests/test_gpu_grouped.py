@@ -119,3 +119,67 @@ def test_grouped_partial_items_and_oracle(device):
     expected = om.expert_ffn(np_bf16(x), ids, weights, oracle_weights(w))
     stats = assert_bf16_close(np_bf16(out), expected, **CONTRACTION)
     print(f"ragged items: {stats}")
+
+
+def test_shared_expert_on_side_stream_and_folded_graph_replays(device):
+    """moe_with_shared with the shared expert on a side stream (the
+    reference's moe_parts layout) and folded into the routed launches both
+    equal the sequential chain bit for bit, eagerly and over repeated graph
+    replays with eager work in between."""
+    from drama3_amd import workloads
+    from drama3_amd.pipeline import DenseExpert, MoEWorkspace, Shape, moe_with_shared
+
+    rows, e, h, i = 1500, 64, 1024, 512
+    gen = torch.Generator("cpu").manual_seed(31)
+    w = workloads.make_experts(gen, e, h, i)
+    sw = workloads.make_experts(gen, 1, h, i)
+    x = workloads._bf16(gen, (rows, h)).to(device)
+    logits = workloads._bf16(gen, (rows, e)).to(device)
+    experts, shared = w.to(device), sw.to(device)
+    ws = MoEWorkspace(Shape(rows, e, h, i), device)
+    dense = DenseExpert(rows, h, i, device)
+    assert ws.grouped and dense.grouped
+    expected = moe_with_shared(ws, dense, x, logits, experts, shared).clone()
+    side = torch.cuda.Stream(device)
+    got = moe_with_shared(ws, dense, x, logits, experts, shared, side=side)
+    torch.cuda.synchronize()
+    assert torch.equal(got, expected)
+
+    g = torch.cuda.CUDAGraph()
+    warm = torch.cuda.Stream(device)
+    warm.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(warm):
+        moe_with_shared(ws, dense, x, logits, experts, shared, side=side)
+    torch.cuda.current_stream().wait_stream(warm)
+    with torch.cuda.graph(g):
+        out = moe_with_shared(ws, dense, x, logits, experts, shared, side=side)
+    for replay in range(3):
+        ws.out.zero_()
+        dense.down.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, expected), f"replay {replay}"
+    # the shared expert folded into the routed launches: the same bytes
+    folded = MoEWorkspace(Shape(rows, e, h, i), device, shared_rows=rows)
+    got = moe_with_shared(folded, None, x, logits, experts, shared)
+    torch.cuda.synchronize()
+    assert torch.equal(got, expected)
+    assert torch.equal(folded.shared_down, dense.down)
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        out2 = moe_with_shared(folded, None, x, logits, experts, shared)
+    for replay in range(3):
+        folded.out.zero_()
+        folded.down.zero_()
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out2, expected), f"folded replay {replay}"
+    # against the oracle
+    weights, ids = om.route(np_f32(logits))
+    routed = om.expert_ffn(np_bf16(x), ids, weights, oracle_weights(w))
+    so = oracle_weights(sw)
+    shared_expected = om.dense_ffn(np_bf16(x), so.w13[0], so.s13[0], so.w2[0], so.s2[0])
+    stats = assert_bf16_close(np_bf16(out), om.add_shared(routed, shared_expected), **CONTRACTION)
+    print(f"side-stream shared expert: {stats}")
