@@ -53,6 +53,8 @@ def parse():
     p.add_argument("--prefill-only", action="store_true",
                    help="measure only the config-4 packed prefill (one JSON line)")
     p.add_argument("--prefill-steps", type=int, default=20)
+    p.add_argument("--no-reference-shape", action="store_true",
+                   help="skip the decode step at the reference model's MoE shape (E256, I512)")
     return p.parse_args()
 
 
@@ -167,6 +169,45 @@ def bench_prefill(torch, steps: int, copies: int = 2) -> dict:
         "peak_TFLOP_s": FP8_PEAK_TFLOPS, "dtype": "fp8_e4m3 MFMA (fp32 accumulate)",
         "timing": f"hipGraph, {copies} rotated weight copies (routed + shared, fragment-major)",
     }
+
+
+def bench_reference_shape(torch, steps: int = 30, copies: int = 3) -> dict:
+    """The decode step at the reference model's own MoE shape (H2048, 256
+    experts, I512, top-8; `model.py:565-571`), all 64 slots live, seeded
+    uniform synthetic routing, three rotated weight copies (cold)."""
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.pipeline import DecodeStep
+
+    device = torch.device("cuda:0")
+    e, h, i, slots = 256, 2048, 512, workloads.SLOTS
+    gen = torch.Generator("cpu").manual_seed(7)
+    first = workloads.make_experts(gen, e, h, i).to(device)
+    sets = [first] + [workloads.Experts(*(t.clone() for t in first.tensors()))
+                      for _ in range(copies - 1)]
+    for c in sets:
+        prepare_experts(c)
+    occ = torch.ones(slots, dtype=torch.uint8, device=device)
+    x = workloads._bf16(gen, (slots, h)).to(device)
+    logits = workloads._bf16(gen, (slots, e)).to(device)
+    ds = DecodeStep(slots, e, h, i, device=device)
+    for c in sets:
+        ds(occ, x, logits, c)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in sets:
+            ds(occ, x, logits, c)
+    g.replay()
+    us = time_graphs(torch, [g], max(1, steps // copies)) / copies
+    used = int(torch.unique(ds.workspace.ids[:slots]).numel())
+    per_expert = 3 * h * i + 4 * ((2 * i // 128) * (h // 128) + (h // 128) * (i // 128))
+    nbytes = used * per_expert + 4 * slots * h + 2 * slots * e + 6 * slots * workloads.TOP_K
+    return {"workload": "decode, 64 live slots, H2048 E256 I512 top-8 (the reference model's MoE)",
+            "us_per_step": round(us, 2), "used_experts": used, "algorithmic_bytes_per_step": nbytes,
+            "GB_s": round(nbytes / us / 1e3, 1), "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "step": "FC1 from the slots + sortless FC2 + routed combine",
+            "timing": f"hipGraph, {copies} rotated weight copies"}
 
 
 def main():
@@ -319,6 +360,7 @@ def main():
                "host_cpus": len(os.sched_getaffinity(0))}
 
     prefill = None if args.no_prefill else bench_prefill(torch, args.prefill_steps)
+    reference_shape = None if args.no_reference_shape else bench_reference_shape(torch)
 
     result = {
         "metric": baseline_metric(),
@@ -365,6 +407,7 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "prefill": prefill,
+        "reference_shape": reference_shape,
     }
     print(json.dumps(result), flush=True)
 

@@ -608,18 +608,18 @@ void launch_tiles(int num_experts, hipStream_t s, const DecodeArgs& a) {
 // Weight tiles per workgroup: enough that the whole grid is about one round
 // of resident workgroups (two per CU), so each workgroup streams its tiles
 // back to back instead of the GPU turning workgroups over; a divisor of the
-// expert's tile count.  Experts averaging more than 8 routes at full
-// capacity take one tile per workgroup (each further route tile would walk
-// all of a workgroup's tiles again).
+// expert's tile count (8 for 256 experts of 16 tiles).  Experts averaging
+// more than 8 routes at full capacity take one tile per workgroup (each
+// further route tile would walk all of a workgroup's tiles again).
 constexpr int kResidentGroups = 512;
 int tiles_per_group(int num_experts, int tiles, int capacity, int top_k, int mode) {
   if (capacity * top_k > 8 * num_experts) return 1;
-  const int options[] = {1, 2, 4, 6};
-  const int limit = mode != 2 ? 6 : 4;
+  const int options[] = {1, 2, 4, 6, 8};
   for (int t : options)
-    if (t <= limit && tiles % t == 0 && num_experts * (tiles / t) <= kResidentGroups) return t;
-  for (int i = 3; i >= 0; --i)
-    if (options[i] <= limit && tiles % options[i] == 0) return options[i];
+    if ((t != 6 || mode != 2) && tiles % t == 0 && num_experts * (tiles / t) <= kResidentGroups)
+      return t;
+  for (int i = 4; i >= 0; --i)
+    if ((options[i] != 6 || mode != 2) && tiles % options[i] == 0) return options[i];
   return 1;
 }
 
@@ -633,7 +633,9 @@ void launch_decode(int num_experts, hipStream_t s, const DecodeArgs& a) {
       return;
     }
   }
-  if (t == 4)
+  if (t == 8)
+    launch_tiles<KB, MODE, 8>(num_experts, s, a);
+  else if (t == 4)
     launch_tiles<KB, MODE, 4>(num_experts, s, a);
   else if (t == 2)
     launch_tiles<KB, MODE, 2>(num_experts, s, a);

@@ -243,3 +243,28 @@ def test_route_fc1_and_combine_contract(device):
     bad[0] = None
     with pytest.raises(ValueError, match="null"):
         _lib.call("d3_decode_route_combine", *bad)
+
+
+def test_real_drama3_shape_eight_tiles_per_workgroup(device):
+    """The reference model's own MoE shape (H2048, 256 experts, I512; 64 live
+    slots): 16 weight tiles per expert, eight per workgroup in both GEMMs;
+    bit-identical to the sorted chain and within tolerance of the oracle."""
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.workloads import Workload, make_experts
+
+    gen = torch.Generator("cpu").manual_seed(41)
+    e, h, i = 256, 2048, 512
+    experts_cpu = make_experts(gen, e, h, i)
+    w = Workload("real", 41, h, e, i, experts_cpu, [])
+    experts = prepare_experts(experts_cpu.to(device))
+    steps = steps_for(w, device, experts)
+    occupancy = torch.ones(64, dtype=torch.uint8)
+    occupancy[[5, 30]] = 0
+    xs = torch.randn((64, h), generator=gen).to(torch.bfloat16).to(device)
+    ls = torch.randn((64, e), generator=gen).to(torch.bfloat16)
+    n = run_all(steps, occupancy.to(device), xs, ls.to(device), experts)
+    active, _ = om.compact_slots(occupancy.numpy())
+    weights, ids = om.route(np_f32(ls)[active])
+    expected = om.expert_ffn(np_bf16(xs.cpu())[active], ids, weights, oracle_weights(experts_cpu))
+    stats = assert_bf16_close(np_bf16(steps[0].workspace.out)[:n], expected, **EXACT)
+    print(f"E 256 I 512: rows {n} {stats}", flush=True)
