@@ -114,12 +114,38 @@ __global__ __launch_bounds__(kSortThreads) void wide_scan_kernel(
     __syncthreads();
   }
   // Per expert: exclusive scan of its chunk counts (offsets written back in
-  // place) -> count.
+  // place) -> count.  Staged in LDS, each expert's chunks are split over
+  // `share` threads (contiguous chunk ranges, their partial sums scanned in
+  // LDS), so the serial chain is chunks / share long.
   int count = 0;
-  if (tid < num_experts) {
+  if (in_lds) {
+    int* partial = staged + cells;  // [E][share]
+    const int share = kSortThreads / num_experts;
+    const int e = tid / share;
+    const int j = tid % share;
+    const int per = (chunks + share - 1) / share;
+    const int c0 = j * per;
+    const int c1 = min(chunks, c0 + per);
+    int sum = 0;
+    if (e < num_experts)
+      for (int c = c0; c < c1; ++c) sum += staged[c * num_experts + e];
+    if (e < num_experts) partial[e * share + j] = sum;
+    __syncthreads();
+    if (e < num_experts) {
+      int base = 0;
+      for (int q = 0; q < j; ++q) base += partial[e * share + q];
+      for (int c = c0; c < c1; ++c) {
+        const int v = staged[c * num_experts + e];
+        chunk_counts[static_cast<size_t>(c) * num_experts + e] = base;
+        base += v;
+      }
+    }
+    if (tid < num_experts)
+      for (int q = 0; q < share; ++q) count += partial[tid * share + q];
+  } else if (tid < num_experts) {
     for (int c = 0; c < chunks; ++c) {
       int32_t* slot = chunk_counts + static_cast<size_t>(c) * num_experts + tid;
-      const int v = in_lds ? staged[c * num_experts + tid] : *slot;
+      const int v = *slot;
       *slot = count;
       count += v;
     }
@@ -286,7 +312,9 @@ extern "C" int d3_sort_routes_wide(const void* ids, int32_t ids_dtype, int32_t r
   hipStream_t s = as_stream(stream);
   const size_t rank_shared = sizeof(int) * static_cast<size_t>(num_experts) * (1 + kWideThreads / kWave);
   const int cells = chunks * num_experts;
-  const size_t scan_shared = sizeof(int) * (kSortThreads / kWave + (cells <= kWideScanLds ? cells : 0));
+  // wave totals + staged chunk counts + per-thread partial sums
+  const size_t scan_shared =
+      sizeof(int) * (kSortThreads / kWave + (cells <= kWideScanLds ? cells + kSortThreads : 0));
   const int scatter_blocks = static_cast<int>((pairs + kWideThreads - 1) / kWideThreads);
   if (chunks > 0) {
     if (ids_dtype == D3_DTYPE_I64)
