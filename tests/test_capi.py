@@ -82,7 +82,10 @@ def test_capacity_helpers(lib):
     for pairs, experts, tile in ((32, 16, 16), (384, 128, 16), (33280, 128, 64), (0, 8, 16)):
         assert lib.d3_max_sorted_rows(pairs, experts, tile) == om.max_sorted_rows(pairs, experts, tile)
     assert lib.d3_max_items(384, 128, 64) == (384 + 128 * 63) // 64
-    assert lib.d3_abi_version() == 3
+    assert lib.d3_abi_version() == 4
+    # wide sort scratch: chunk histograms [ceil(pairs / 512)][E] + ranks [pairs]
+    assert lib.d3_sort_wide_scratch_ints(3668, 8, 128) == (-(-3668 * 8 // 512)) * 128 + 3668 * 8
+    assert lib.d3_sort_wide_scratch_ints(-1, 8, 128) == -1
 
 
 def test_contract_violations_raise_value_error(lib):
@@ -108,7 +111,26 @@ def test_contract_violations_raise_value_error(lib):
                   16, None)
     with pytest.raises(ValueError, match="multiple of 16"):
         _lib.call("d3_pack_expert_weights", 16, 4, 24, 128, 32, None)
-    assert "K=" in lib.d3_last_error().decode()
+    # tiled grouped GEMMs: item size, K, shared-expert operands, N tiling
+    with pytest.raises(ValueError, match="item_rows 256"):
+        _lib.call("d3_grouped_fc1_swiglu", 16, 16, 0, 4, 256, 1024, 16, 100, 16, 16, 8, 16, 16, 4,
+                  256, None, None, 0, 0, 16, 16, None)
+    with pytest.raises(ValueError, match="K=384"):
+        _lib.call("d3_grouped_fc1_swiglu", 16, 16, 0, 4, 256, 384, 16, 100, 16, 16, 8, 16, 16, 4,
+                  128, None, None, 0, 0, 16, 16, None)
+    with pytest.raises(ValueError, match="shared expert"):
+        _lib.call("d3_grouped_fc1_swiglu", 16, 16, 0, 4, 256, 1024, 16, 100, 16, 16, 8, 16, 16, 4,
+                  128, 16, None, 100, 0, 16, 16, None)
+    with pytest.raises(ValueError, match="shared expert"):
+        _lib.call("d3_grouped_fc2", 16, 16, 0, 4, 1024, 256, 16, 100, 16, 16, 8, 16, 16, 4, 128,
+                  16, 16, 60, 50, 0, 16, None)
+    with pytest.raises(ValueError, match="multiple of 256"):
+        _lib.call("d3_grouped_fc2", 16, 16, 0, 4, 640, 256, 16, 100, 16, 16, 8, 16, 16, 4, 128,
+                  None, None, 0, 0, 0, 16, None)
+    with pytest.raises(ValueError, match="scratch"):
+        _lib.call("d3_sort_routes_wide", 16, 2, 1100, None, 8, 128, 16, 16, 16, 16, 16, 16,
+                  lib.d3_max_sorted_rows(8800, 128, 16), 16, 16, None, 0, None, None, 16, 10, None)
+    assert "scratch of 10 ints" in lib.d3_last_error().decode()
 
 
 def test_product_code_does_not_import_the_oracle():

@@ -76,6 +76,35 @@ def test_grouped_matches_fp8_chain(device, shape, packed, item_rows):
     assert torch.equal(ws.down.view(torch.int32), down_ref.view(torch.int32)), "down rows differ"
 
 
+@pytest.mark.parametrize("shape", [(300, 8, 512, 512), (260, 8, 1536, 256), (400, 16, 256, 1536)],
+                         ids=["h512_i512", "h1536_i256", "h256_i1536"])
+def test_grouped_other_contraction_lengths(device, shape):
+    """K of 256 ... 2048 on both GEMMs (FC1 K = H, FC2 K = I), fragment-major
+    weights, against the FP8 chain byte for byte."""
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.pipeline import MoEWorkspace, Shape
+
+    rows, e, h, i = shape
+    w, x, logits = _workload(rows, e, h, i, seed=17)
+    experts = prepare_experts(w.to(device))
+    ws = MoEWorkspace(Shape(rows, e, h, i), device, item_rows=128, grouped=True)
+    ws.front(x.to(device), logits.to(device))
+    live = _live_positions(ws)
+    ws.exact_routes = 0
+    ws.fc1(experts)
+    ws.activation()
+    ws.fc2(experts)
+    torch.cuda.synchronize()
+    act_ref, scales_ref, down_ref = ws.act[live].clone(), ws.act_scales[live].clone(), ws.down.clone()
+    ws.grouped_fc1(experts)
+    ws.grouped_fc2(experts)
+    torch.cuda.synchronize()
+    assert torch.equal(ws.act[live], act_ref)
+    assert torch.equal(ws.act_scales[live].view(torch.int32), scales_ref.view(torch.int32))
+    pairs = ws.shape.pairs
+    assert torch.equal(ws.down[:pairs].view(torch.int32), down_ref[:pairs].view(torch.int32))
+
+
 def test_grouped_dense_expert_matches_fp8_chain(device):
     """The shared expert (identity routes, top_k 1) through both chains."""
     from drama3_amd.pipeline import DenseExpert, MoEWorkspace, Shape
