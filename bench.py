@@ -55,6 +55,8 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=20)
     p.add_argument("--no-reference-shape", action="store_true",
                    help="skip the decode step at the reference model's MoE shape (E256, I512)")
+    p.add_argument("--no-mixed", action="store_true",
+                   help="skip the config-5 mixed decode + prefill step")
     return p.parse_args()
 
 
@@ -210,6 +212,55 @@ def bench_reference_shape(torch, steps: int = 30, copies: int = 3) -> dict:
             "timing": f"hipGraph, {copies} rotated weight copies"}
 
 
+def bench_mixed(torch, steps: int = 50) -> dict:
+    """Config 5's mixed step as one captured graph (``MixedStep``): 48 live
+    decode slots of 64 (decode bucket 64), two 256-row prompts in a 640-row
+    prefill suffix (128 padding rows), E16 H1024 I256 top-8.  Timed twice:
+    distinct prompts, and the second prompt sharing its first 128 rows with
+    the first (prefix reuse folds them)."""
+    from drama3_amd import workloads
+    from drama3_amd.mixed import MixedStep
+
+    device = torch.device("cuda:0")
+    w = workloads.config5()
+    experts = w.experts.to(device)
+    slots, d, capacity = workloads.SLOTS, 64, 640
+    step = MixedStep(slots, d, capacity, slots // 2, 3, w.num_experts, w.hidden, w.intermediate,
+                     device=device)
+    gen = torch.Generator("cpu").manual_seed(5)
+    full = step.rows.full
+    step.occupancy.copy_(w.steps[0].occupancy)
+    step.boundaries.copy_(torch.tensor([0, 256, 512, capacity], dtype=torch.int32))
+    step.sequence_slots.copy_(torch.tensor([40, 41, slots - 1]))
+    step.x.copy_(workloads._bf16(gen, (full, w.hidden)))
+    step.logits.copy_(workloads._bf16(gen, (full, w.num_experts)))
+    step.shared.copy_(workloads._bf16(gen, (full, w.hidden)))
+    step.gate.copy_(workloads._bf16(gen, (full,)))
+    step.norm_weight.copy_(workloads._bf16(gen, (w.hidden,)))
+    residual = workloads._bf16(gen, (full, w.hidden)).to(device)
+    frames = torch.randint(0, 1024, (capacity, 11), generator=gen)
+    step.frames.copy_(frames)
+    step.residual.copy_(residual)
+    step.capture(experts)
+    out = {}
+    for name, shared_rows in (("distinct_prompts", 0), ("shared_prefix_128", 128)):
+        f = frames.clone()
+        f[256:256 + shared_rows] = f[:shared_rows]
+        step.frames.copy_(f)
+        step.replay()
+        torch.cuda.synchronize()
+        kept = int(step.rows.keep_count.item())
+        us = time_graphs(torch, [step.graph], steps)
+        out[name] = {"us_per_step": round(us, 2), "moe_rows": kept,
+                     "tokens_per_s": round((48 + 512) / (us * 1e-6), 1)}
+    return {"workload": "config 5 mixed step: 48 of 64 decode slots + 2 x 256 prompt rows "
+                        "(640-row suffix), E16 H1024 I256 top-8",
+            "rows": full, "live_rows": 48 + 512, **out,
+            "step": "d3_mixed_rows + row_metadata + MoE on the kept rows + residual/RMSNorm "
+                    "combine onto all rows, one hipGraph",
+            "timing": "graph replays; the residual is updated in place on every replay"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -361,6 +412,7 @@ def main():
 
     prefill = None if args.no_prefill else bench_prefill(torch, args.prefill_steps)
     reference_shape = None if args.no_reference_shape else bench_reference_shape(torch)
+    mixed = None if args.no_mixed else bench_mixed(torch)
 
     result = {
         "metric": baseline_metric(),
@@ -408,6 +460,7 @@ def main():
         "parity": parity,
         "prefill": prefill,
         "reference_shape": reference_shape,
+        "mixed": mixed,
     }
     print(json.dumps(result), flush=True)
 

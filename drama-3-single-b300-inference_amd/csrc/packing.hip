@@ -93,10 +93,208 @@ __global__ __launch_bounds__(kThreads) void requests_save_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Mixed decode + prefill rows (one workgroup).  Row space: decode rows
+// [0, decode_rows) then the packed prefill suffix [decode_rows, full).
+// ---------------------------------------------------------------------------
+constexpr int kMixedThreads = 1024;
+constexpr int kMixedWaves = kMixedThreads / kWave;
+constexpr int kMixedMaxRows = 8192;   // row space with prefix reuse (LDS owner table)
+constexpr int kMixedMaxPrompts = 16;  // prompts compared for prefix reuse
+
+// Exclusive rank of `flag` among the workgroup's threads (thread order) and
+// the workgroup's total.  Two barriers; `wave_counts` is free again on return.
+__device__ __forceinline__ int block_rank(bool flag, int* wave_counts, int* total) {
+  const int wave = threadIdx.x / kWave;
+  const uint64_t mask = __ballot(flag);
+  if (lane_id() == 0) wave_counts[wave] = __popcll(mask);
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < kMixedWaves; ++w) {
+    before += w < wave ? wave_counts[w] : 0;
+    all += wave_counts[w];
+  }
+  __syncthreads();
+  *total = all;
+  return before + __popcll(mask & lanemask_lt());
+}
+
+// One mixed step's rows on the device (the host-side preparation of
+// mixed_graph.py:139-179 and the prefix-reuse ownership of
+// row_reuse.py:74-101, from device data so that a captured graph needs no
+// host sync):
+//   1. occupied slots, ascending (active / count), and the decode rows'
+//      slots: the first min(count, decode_rows) occupied slots, then
+//      padding_start + j for the remaining rows j;
+//   2. with frames: prompt i (suffix rows [b[i], b[i+1])) aliases its first
+//      L rows to the same positions of the earliest earlier prompt j with the
+//      longest agreeing leading run L (every code compared); owners chain to
+//      canonical rows because prompts are processed in order;
+//   3. live rows (occupied decode rows, suffix rows below b[prompts]) that
+//      own themselves are the MoE rows (keep, ascending; keep_count); every
+//      live row reads back its owner's MoE row (inverse), other rows row 0.
+// Boundaries are clamped to [0, capacity] and made non-decreasing, so every
+// frame read stays inside the suffix's capacity rows.
+__global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
+    const uint8_t* __restrict__ occupancy, int num_slots, int decode_rows, int64_t padding_start,
+    const int32_t* __restrict__ boundaries, int prompts, int capacity,
+    const int64_t* __restrict__ frames, int codes, int32_t* __restrict__ active,
+    int32_t* __restrict__ count, int64_t* __restrict__ decode_slots, int32_t* __restrict__ keep,
+    int32_t* __restrict__ keep_count, int64_t* __restrict__ inverse) {
+  __shared__ int32_t owner_of[kMixedMaxRows];  // owner row; -(rank + 1) once kept
+  __shared__ int wave_counts[kMixedWaves];
+  __shared__ int starts[kMixedMaxPrompts + 1];
+  __shared__ int common[kMixedMaxPrompts * kMixedMaxPrompts];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int full = decode_rows + capacity;
+  const bool reuse = frames != nullptr && prompts >= 2;
+
+  // 1. slot compaction and decode row slots
+  int occupied = 0;
+  for (int start = 0; start < num_slots; start += kMixedThreads) {
+    const int slot = start + tid;
+    const bool live = slot < num_slots && occupancy[slot] != 0;
+    int chunk;
+    const int at = occupied + block_rank(live, wave_counts, &chunk);
+    if (live) {
+      active[at] = slot;
+      if (at < decode_rows) decode_slots[at] = slot;
+    }
+    occupied += chunk;
+  }
+  for (int i = occupied + tid; i < num_slots; i += kMixedThreads) active[i] = -1;
+  const int used = occupied < decode_rows ? occupied : decode_rows;
+  for (int j = used + tid; j < decode_rows; j += kMixedThreads) decode_slots[j] = padding_start + j;
+  if (tid == 0) *count = occupied;
+
+  // 2. clamped boundaries and prefix ownership
+  // b[prompts] after clamping: the largest clamped boundary.
+  int live_prefill = 0;
+  for (int i = 0; i <= prompts; ++i) {
+    const int b = boundaries[i];
+    const int clamped = b > capacity ? capacity : b;
+    live_prefill = clamped > live_prefill ? clamped : live_prefill;
+  }
+  if (reuse) {
+    if (tid == 0) {
+      int previous = 0;
+      for (int i = 0; i <= prompts; ++i) {
+        int b = boundaries[i];
+        b = b < previous ? previous : (b > capacity ? capacity : b);
+        starts[i] = b;
+        previous = b;
+      }
+    }
+    for (int r = tid; r < full; r += kMixedThreads) owner_of[r] = r;
+    __syncthreads();
+    // common[i][j], j < i: first differing row of prompts i and j (or the
+    // shorter length).
+    const int pairs = prompts * (prompts - 1) / 2;
+    if (tid < pairs) {
+      int i = 1, base = 0;
+      while (base + i <= tid) base += i++;
+      const int j = tid - base;
+      const int li = starts[i + 1] - starts[i], lj = starts[j + 1] - starts[j];
+      common[i * kMixedMaxPrompts + j] = li < lj ? li : lj;
+    }
+    __syncthreads();
+    const int wave = tid / kWave;
+    for (int q = wave; q < pairs; q += kMixedWaves) {
+      int i = 1, base = 0;
+      while (base + i <= q) base += i++;
+      const int j = q - base;
+      const int li = starts[i + 1] - starts[i], lj = starts[j + 1] - starts[j];
+      const int limit = li < lj ? li : lj;
+      for (int p = lane_id(); p < limit; p += kWave) {
+        const int64_t* a = frames + static_cast<int64_t>(starts[i] + p) * codes;
+        const int64_t* b = frames + static_cast<int64_t>(starts[j] + p) * codes;
+        bool differ = false;
+        for (int c = 0; c < codes; ++c) differ |= a[c] != b[c];
+        if (differ) atomicMin(&common[i * kMixedMaxPrompts + j], p);
+      }
+    }
+    __syncthreads();
+    for (int i = 1; i < prompts; ++i) {
+      int longest = 0, source = 0;
+      for (int j = 0; j < i; ++j) {
+        const int n = common[i * kMixedMaxPrompts + j];
+        if (n > longest) {
+          longest = n;
+          source = j;
+        }
+      }
+      for (int p = tid; p < longest; p += kMixedThreads)
+        owner_of[decode_rows + starts[i] + p] = owner_of[decode_rows + starts[source] + p];
+      __syncthreads();
+    }
+  }
+
+  // 3. MoE rows and the read-back map
+  int kept_total = 0;
+  for (int start = 0; start < full; start += kMixedThreads) {
+    const int r = start + tid;
+    const bool in = r < full;
+    const bool live = in && (r < decode_rows ? r < used : r - decode_rows < live_prefill);
+    const int owner = reuse && in ? owner_of[r] : r;
+    const bool kept = live && owner == r;
+    int chunk;
+    const int at = kept_total + block_rank(kept, wave_counts, &chunk);
+    if (kept) {
+      keep[at] = r;
+      if (reuse) owner_of[r] = -(at + 1);
+    }
+    if (reuse) __syncthreads();
+    if (in) {
+      int64_t back = 0;
+      if (live) {
+        if (reuse) {
+          const int s = owner_of[owner];
+          back = s < 0 ? -(s + 1) : 0;
+        } else {
+          back = at;
+        }
+      }
+      inverse[r] = back;
+    }
+    kept_total += chunk;
+  }
+  for (int i = kept_total + tid; i < full; i += kMixedThreads) keep[i] = 0;
+  if (tid == 0) *keep_count = kept_total;
+}
+
 }  // namespace
 }  // namespace d3
 
 using namespace d3;
+
+extern "C" int d3_mixed_rows(const uint8_t* occupancy, int32_t num_slots, int32_t decode_rows,
+                             int64_t padding_start, const int32_t* boundaries, int32_t prompts,
+                             int32_t capacity, const int64_t* frames, int32_t codes,
+                             int32_t* active_slots, int32_t* count, int64_t* decode_slots,
+                             int32_t* keep, int32_t* keep_count, int64_t* inverse,
+                             void* stream) {
+  D3_REQUIRE(occupancy && boundaries && active_slots && count && keep && keep_count && inverse,
+             "mixed_rows: null pointer");
+  D3_REQUIRE(decode_rows == 0 || decode_slots, "mixed_rows: null decode_slots");
+  D3_REQUIRE(num_slots > 0 && num_slots <= (1 << 20), "mixed_rows: num_slots out of range");
+  D3_REQUIRE(decode_rows >= 0 && capacity >= 0 && prompts >= 0,
+             "mixed_rows: negative decode_rows, capacity or prompts");
+  const int64_t full = static_cast<int64_t>(decode_rows) + capacity;
+  D3_REQUIRE(full >= 1 && full <= (1 << 30), "mixed_rows: %lld rows out of range",
+             static_cast<long long>(full));
+  D3_REQUIRE(frames == nullptr || codes >= 1, "mixed_rows: frames need codes >= 1");
+  if (frames != nullptr && prompts >= 2) {
+    D3_SUPPORTED(prompts <= kMixedMaxPrompts, "mixed_rows: prefix reuse over %d prompts (max %d)",
+                 prompts, kMixedMaxPrompts);
+    D3_SUPPORTED(full <= kMixedMaxRows, "mixed_rows: prefix reuse over %lld rows (max %d)",
+                 static_cast<long long>(full), kMixedMaxRows);
+  }
+  hipLaunchKernelGGL(mixed_rows_kernel, dim3(1), dim3(kMixedThreads), 0, as_stream(stream),
+                     occupancy, num_slots, decode_rows, padding_start, boundaries, prompts,
+                     capacity, frames, codes, active_slots, count, decode_slots, keep, keep_count,
+                     inverse);
+  D3_LAUNCHED("mixed_rows");
+}
 
 extern "C" int d3_row_metadata(const int32_t* cu_seqlens, const int64_t* sequence_slots,
                                int32_t sequences, int32_t capacity, const int64_t* frames,

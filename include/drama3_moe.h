@@ -525,6 +525,43 @@ int d3_row_metadata(const int32_t *cu_seqlens, const int64_t *sequence_slots,
                     void *stream);
 
 /*
+ * A13  Rows of one mixed decode + prefill step, from device data (one launch,
+ * graph-capturable, no host sync).
+ * Replaces the host-side row preparation of MixedGraph.prepare
+ * (src/drama3/mixed_graph.py:139-179: decode slots padded with reserved
+ * slots, packed prompt suffix) and the row ownership of plan_row_reuse
+ * (src/drama3/row_reuse.py:46-109) whose keep / inverse lists
+ * mixed_backbone feeds to the MoE and to combine_experts_add_norm_inverse
+ * (src/drama3/mixed_model.py:193-198,239-242).
+ * Row space: decode rows [0, decode_rows), then the prefill suffix's
+ * capacity rows.
+ *   occupancy u8 [num_slots] -> active_slots int32 [num_slots] (ascending,
+ *     -1 padded), *count; decode_slots int64 [decode_rows]: the first
+ *     min(count, decode_rows) occupied slots, then padding_start + j;
+ *   boundaries int32 [prompts + 1]: prompt i is suffix rows [b[i], b[i+1])
+ *     (the reference layout's boundaries, prompts = its sequences before
+ *     the padding sequence); suffix rows from b[prompts] on are padding;
+ *   frames int64 [capacity, codes] (the suffix's frames) or NULL: with
+ *     frames and prompts >= 2, each prompt's leading rows alias the rows of
+ *     the earlier prompt with the longest agreeing leading run (the
+ *     reference's prefix reuse; <= 16 prompts, <= 8192 rows);
+ *   keep int32 [full]: the live rows (occupied decode rows, prompt rows)
+ *     that own themselves, ascending, then 0; *keep_count of them;
+ *   inverse int64 [full]: the keep index of each live row's owner, 0 for
+ *     padding rows.
+ * The MoE runs on rows keep[0 .. keep_count) (a front row_index / device
+ * row_count); combine_experts_add_norm with inverse maps its rows back.
+ * Padding rows never reach the MoE (the reference computes and discards
+ * them).  More occupied slots than decode_rows: *count reports them all and
+ * the first decode_rows become rows.
+ */
+int d3_mixed_rows(const uint8_t *occupancy, int32_t num_slots, int32_t decode_rows,
+                  int64_t padding_start, const int32_t *boundaries, int32_t prompts,
+                  int32_t capacity, const int64_t *frames, int32_t codes, int32_t *active_slots,
+                  int32_t *count, int64_t *decode_slots, int32_t *keep, int32_t *keep_count,
+                  int64_t *inverse, void *stream);
+
+/*
  * A1  Per-slot request state gather / update.
  * Replace DeviceRequests.load / .save and their _load / _save kernels
  * (src/drama3/runtime_state.py:10-56,94-124).  State layout: last [S, 11],

@@ -466,3 +466,117 @@ def mixed_rows(decode_slots, prompt_lengths):
     kind = np.concatenate([np.zeros(decode_slots.size, np.int32), np.ones(int(cu[-1]), np.int32)])
     owner = np.concatenate([decode_slots, np.repeat(np.arange(lengths.size), lengths)])
     return kind, owner.astype(np.int64), cu
+
+
+# ---------------------------------------------------------------------------
+# A13 mixed decode + prefill rows and prefix row reuse
+# ---------------------------------------------------------------------------
+def prompt_row_owners(prompts, decode_rows, full_rows):
+    """Owner row of every mixed row under prefix reuse (``row_reuse.py:74-92``).
+
+    Rows are decode rows [0, decode_rows) then each prompt's rows in order.
+    Prompt i's first ``longest`` rows alias the same positions of the earlier
+    prompt j whose rows agree with prompt i's for the longest leading run
+    (all columns compared; the first such j on ties); aliased rows take
+    prompt j's owners, so owners are canonical (owner[owner[r]] == owner[r]).
+    Every other row owns itself.
+    """
+    arrays = [np.asarray(p) for p in prompts]
+    owners = np.arange(full_rows, dtype=np.int64)
+    offsets = []
+    offset = decode_rows
+    for index, current in enumerate(arrays):
+        longest, previous_owner = 0, None
+        for previous, other in enumerate(arrays[:index]):
+            limit = min(len(current), len(other))
+            same = np.all(current[:limit] == other[:limit], axis=1)
+            different = np.flatnonzero(~same)
+            common = int(different[0]) if len(different) else limit
+            if common > longest:
+                longest, previous_owner = common, previous
+        if longest:
+            start = offsets[previous_owner]
+            owners[offset:offset + longest] = owners[start:start + longest]
+        offsets.append(offset)
+        offset += len(current)
+    return owners
+
+
+def plan_row_reuse(prompts, decode_rows, prefill_capacity, compact_capacities):
+    """``plan_row_reuse`` (``row_reuse.py:46-109``) without its argument
+    checks: (compact_rows, unique_rows, packed int64 [compact + full]) or
+    None when no compact capacity holds the unique rows rounded up to 64.
+    packed = [kept rows ascending, zero padded to compact | for every row the
+    kept-row index of its owner]."""
+    full_rows = decode_rows + prefill_capacity
+    capacities = sorted(set(compact_capacities))
+    if not capacities:
+        return None
+    owners = prompt_row_owners(prompts, decode_rows, full_rows)
+    keep = np.flatnonzero(owners == np.arange(full_rows))
+    unique = len(keep)
+    minimum = (unique + 63) // 64 * 64
+    compact = next((k for k in capacities if k >= minimum), None)
+    if compact is None:
+        return None
+    lookup = np.empty_like(owners)
+    lookup[keep] = np.arange(unique, dtype=np.int64)
+    packed = np.zeros(compact + full_rows, dtype=np.int64)
+    packed[:unique] = keep
+    packed[compact:] = lookup[owners]
+    return compact, unique, packed
+
+
+@dataclass
+class MixedLayout:
+    active: np.ndarray        # int32 [S]: occupied slots ascending, then -1
+    count: int                # occupied slots
+    decode_slots: np.ndarray  # int64 [decode_rows]
+    keep: np.ndarray          # int32 [full]: MoE source rows, then 0
+    keep_count: int
+    inverse: np.ndarray       # int64 [full]: MoE row read back by every row
+
+
+def mixed_layout(occupancy, decode_rows, padding_start, boundaries, prompts, capacity,
+                 frames=None, codes=11):
+    """The device contract of one mixed step's rows (``d3_mixed_rows``).
+
+    Decode rows: the ascending occupied slots, then reserved padding slots
+    ``padding_start + j`` for rows j >= count (``mixed_graph.py:147-152``).
+    Prefill rows: the packed suffix of capacity rows whose first
+    ``boundaries[prompts]`` rows are the prompts (``mixed_graph.py:161-179``:
+    the remaining sequences are empty or padding).  Live rows are the
+    occupied decode rows and the prompt rows; with ``frames`` (the suffix's
+    int64 rows) prompt rows alias earlier prompts' rows by
+    ``prompt_row_owners``.  The MoE runs on the live rows that own themselves
+    (``keep`` ascending, ``keep_count`` of them, the reference's compact rows
+    of ``mixed_model.py:193-198,239-242``); every live row reads back its
+    owner's MoE row (``inverse``, the reference's lookup); rows that are not
+    live (decode padding, prefill padding) read MoE row 0.
+    """
+    active, count = compact_slots(occupancy)
+    slots_out = np.full(len(occupancy), -1, dtype=np.int32)
+    slots_out[:count] = active
+    used = min(count, decode_rows)
+    decode_slots = padding_start + np.arange(decode_rows, dtype=np.int64)
+    decode_slots[:used] = active[:used]
+    full = decode_rows + capacity
+    cu = np.asarray(boundaries, dtype=np.int64)
+    lengths = [int(cu[i + 1] - cu[i]) for i in range(prompts)]
+    live_prefill = int(cu[prompts])
+    if frames is not None:
+        rows = np.asarray(frames, dtype=np.int64).reshape(-1, codes)
+        arrays = [rows[cu[i]:cu[i] + n] for i, n in enumerate(lengths)]
+        owners = prompt_row_owners(arrays, decode_rows, full)
+    else:
+        owners = np.arange(full, dtype=np.int64)
+    r = np.arange(full)
+    live = np.where(r < decode_rows, r < used, (r - decode_rows) < live_prefill)
+    kept = live & (owners == r)
+    keep_rows = np.flatnonzero(kept)
+    keep = np.zeros(full, dtype=np.int32)
+    keep[:len(keep_rows)] = keep_rows
+    rank = np.zeros(full, dtype=np.int64)
+    rank[keep_rows] = np.arange(len(keep_rows))
+    inverse = np.where(live, rank[owners], 0).astype(np.int64)
+    return MixedLayout(slots_out, count, decode_slots, keep, len(keep_rows), inverse)
