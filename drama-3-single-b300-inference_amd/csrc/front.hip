@@ -111,7 +111,14 @@ __global__ __launch_bounds__(kFrontThreads) void quantize_kernel(
 // workgroup resets the ticket so the next launch (or graph replay) starts at 0.
 // ---------------------------------------------------------------------------
 constexpr int kMaxFrontExperts = 512;
-constexpr int kFrontSortInts = sort_shared_ints(kFrontThreads, kMaxFrontExperts);
+constexpr int kMaxFusedSortExperts = kFrontThreads;  // the block sorts: one expert per thread
+constexpr int kMaxFusedSortPairs = 8192;
+constexpr int kFrontPerThread = kMaxFusedSortPairs / kFrontThreads;
+constexpr int kFrontSortInts =
+    sort_shared_ints(kFrontThreads, kMaxFusedSortExperts) >
+            mask_sort_shared_ints(kFrontThreads, kMaxFusedSortExperts, kMaskWords)
+        ? sort_shared_ints(kFrontThreads, kMaxFusedSortExperts)
+        : mask_sort_shared_ints(kFrontThreads, kMaxFusedSortExperts, kMaskWords);
 
 struct FrontArgs {
   const uint8_t* occupancy;
@@ -211,8 +218,15 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
     if (threadIdx.x == 0) ticket_shared = take_ticket(a.ticket);
     __syncthreads();
     if (ticket_shared != static_cast<int>(gridDim.x) - 1) return;
-    sort_routes_block<kFrontThreads, false, true>(a.ids, live * a.top_k, a.num_experts, a.tile,
-                                                   a.item_rows, smem, a.sort);
+    // The router's ids name distinct experts per row: the row-mask sort,
+    // unless its masks exceed the LDS share (then the chunked ballot sort).
+    const bool masked = a.num_experts * mask_words(live) <= kMaskWords &&
+                        sort_rows_block<kFrontThreads, kFrontPerThread, false, true>(
+                            a.ids, live, a.top_k, a.num_experts, a.tile, a.item_rows, smem,
+                            kMaskWords, a.sort);
+    if (!masked)
+      sort_routes_block<kFrontThreads, false, true>(a.ids, live * a.top_k, a.num_experts, a.tile,
+                                                     a.item_rows, smem, a.sort);
     if (threadIdx.x == 0) reset_ticket(a.ticket);
   }
 }
@@ -374,8 +388,12 @@ extern "C" int d3_moe_front(const uint8_t* occupancy, int32_t num_slots, int32_t
     D3_REQUIRE(counts && starts && total && expert_ids && ticket, "moe_front: sort outputs");
     D3_REQUIRE(tile >= 1 && tile <= 1024, "moe_front: bad tile %d", tile);
     const int64_t pairs = static_cast<int64_t>(rows) * top_k;
-    D3_SUPPORTED(pairs <= 8192, "moe_front: %lld pairs exceed the fused sort (use d3_sort_routes)",
+    D3_SUPPORTED(pairs <= kMaxFusedSortPairs,
+                 "moe_front: %lld pairs exceed the fused sort (use d3_sort_routes)",
                  static_cast<long long>(pairs));
+    D3_SUPPORTED(num_experts <= kMaxFusedSortExperts,
+                 "moe_front: the fused sort covers up to %d experts (use d3_sort_routes)",
+                 kMaxFusedSortExperts);
     const int32_t need = d3_max_sorted_rows(static_cast<int32_t>(pairs), num_experts, tile);
     D3_REQUIRE(max_rows >= need && max_rows % tile == 0, "moe_front: max_rows %d < required %d",
                max_rows, need);

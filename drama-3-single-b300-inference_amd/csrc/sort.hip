@@ -13,13 +13,23 @@ namespace {
 constexpr int kSortThreads = 1024;
 constexpr int kMaxSortExperts = 512;  // LDS: (4 + 16 waves) * E ints <= 40 KiB
 
+constexpr int kSortPerThread = 8;        // row-mask sort: up to 8192 pairs
+constexpr int kSortMaskCells = 4096;     // row-mask sort: E * ceil(rows / 64) <= 4096 (48 KiB)
+
+// mask_cells > 0: try the row-mask sort first (it gives up, writing
+// nothing, when a row repeats an expert; the chunked ballot sort then runs).
 template <bool kI64>
 __global__ __launch_bounds__(kSortThreads) void sort_routes_kernel(
     const void* __restrict__ ids, int rows, const int32_t* __restrict__ row_count, int top_k,
-    int num_experts, int tile, int item_rows, SortOutputs out) {
+    int num_experts, int tile, int item_rows, int mask_cells, SortOutputs out) {
   extern __shared__ int smem[];
-  const int pairs = live_rows(row_count, rows) * top_k;
-  sort_routes_block<kSortThreads, kI64>(ids, pairs, num_experts, tile, item_rows, smem, out);
+  const int live = live_rows(row_count, rows);
+  if (mask_cells > 0 &&
+      sort_rows_block<kSortThreads, kSortPerThread, kI64, false>(
+          ids, live, top_k, num_experts, tile, item_rows, smem, mask_cells, out))
+    return;
+  __syncthreads();  // the row-mask attempt's LDS is reused
+  sort_routes_block<kSortThreads, kI64>(ids, live * top_k, num_experts, tile, item_rows, smem, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -250,16 +260,26 @@ extern "C" int d3_sort_routes(const void* ids, int32_t ids_dtype, int32_t rows,
   } else {
     item_rows = tile;
   }
-  const size_t shared = sizeof(int) * static_cast<size_t>(sort_shared_ints(kSortThreads, num_experts));
+  // The row-mask sort covers batches whose masks (sized for the capacity
+  // rows) and pairs fit; the ballot sort everything else.
+  const int64_t cells = static_cast<int64_t>(num_experts) * mask_words(rows);
+  const int mask_cells =
+      pairs <= kSortThreads * kSortPerThread && cells <= kSortMaskCells ? static_cast<int>(cells) : 0;
+  int shared_ints = sort_shared_ints(kSortThreads, num_experts);
+  if (mask_cells > 0) {
+    const int mask_ints = mask_sort_shared_ints(kSortThreads, num_experts, mask_cells);
+    shared_ints = mask_ints > shared_ints ? mask_ints : shared_ints;
+  }
+  const size_t shared = sizeof(int) * static_cast<size_t>(shared_ints);
   const SortOutputs out{counts, starts, total, sorted_ids, expert_ids, max_rows, inverse,
                         reinterpret_cast<int4*>(items), max_items, num_items, pairs_out};
   hipStream_t s = as_stream(stream);
   if (ids_dtype == D3_DTYPE_I64)
     hipLaunchKernelGGL(sort_routes_kernel<true>, dim3(1), dim3(kSortThreads), shared, s, ids,
-                       rows, row_count, top_k, num_experts, tile, item_rows, out);
+                       rows, row_count, top_k, num_experts, tile, item_rows, mask_cells, out);
   else
     hipLaunchKernelGGL(sort_routes_kernel<false>, dim3(1), dim3(kSortThreads), shared, s, ids,
-                       rows, row_count, top_k, num_experts, tile, item_rows, out);
+                       rows, row_count, top_k, num_experts, tile, item_rows, mask_cells, out);
   D3_LAUNCHED("sort_routes");
 }
 

@@ -44,10 +44,12 @@ EXACT_ROUTES = 64
 GROUPED_K = (256, 512, 768, 1024, 1536, 2048)
 GROUPED_ROUTES = 128  # most routes per work item of the tiled grouped GEMMs
 GROUPED_ITEM_ROUTES = 128  # their default item size
-# Up to this many (row, rank) pairs the route sort runs inside the fused front
-# kernel (its last workgroup); larger batches use the 1024-thread sort kernel,
-# and from WIDE_SORT_PAIRS on the wide sort (one workgroup per 512 pairs).
+# Up to this many (row, rank) pairs the route sort can run inside the fused
+# front kernel (its last workgroup; opt-in, MoEWorkspace(fused_sort=True));
+# otherwise the 1024-thread sort kernel follows the front, and from
+# WIDE_SORT_PAIRS on the wide sort (one workgroup per 512 pairs).
 FUSED_SORT_PAIRS = 8192
+FUSED_SORT_EXPERTS = 256
 WIDE_SORT_PAIRS = 8192
 
 
@@ -107,9 +109,13 @@ class MoEWorkspace:
                  item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
                  exact_routes: int = EXACT_ROUTES, fused_epilogues: bool = False,
                  swiglu_in_fc2: bool | None = None, sortless: bool = False,
-                 grouped: bool | None = None, shared_rows: int = 0):
+                 grouped: bool | None = None, shared_rows: int = 0, fused_sort: bool = False):
         lib = _lib.load()
         self.shape = shape
+        # front(): sort in the front launch's last workgroup (256 threads)
+        # instead of the 1024-thread sort launch after it; the separate launch
+        # is the faster of the two at every measured size (48-1024 rows).
+        self.fused_sort = fused_sort
         self.device = torch.device(device)
         self.tile = tile
         self.exact_routes = exact_routes
@@ -224,7 +230,8 @@ class MoEWorkspace:
         (two when the batch exceeds the fused sort).  With ``occupancy`` the
         rows are the live slots (``active`` / ``count`` receive the list)."""
         s, stream = self.shape, self._stream(stream)
-        fused = s.pairs <= FUSED_SORT_PAIRS and not self.sortless
+        fused = (self.fused_sort and s.pairs <= FUSED_SORT_PAIRS
+                 and s.num_experts <= FUSED_SORT_EXPERTS and not self.sortless)
         slots = occupancy.numel() if occupancy is not None else 0
         if occupancy is not None and slots != s.rows:
             raise ValueError("slot mode needs a workspace with one row per slot")

@@ -143,8 +143,10 @@ int d3_sort_routes(const void *ids, int32_t ids_dtype, int32_t rows, const int32
  * (row_count ? *row_count : rows) reading source row row_index ? row_index[r]
  * : r of x and logits.  Row r of ids / weights / q / scales is output row r.
  * With sorted_ids != NULL the last workgroup to finish also sorts the routes
- * (rows * top_k <= 8192); `ticket` is a device int32 that must hold 0 before
- * the first launch and is left at 0 by every launch.
+ * (rows * top_k <= 8192, num_experts <= 256; the same outputs as
+ * d3_sort_routes, ranked through per-expert bit masks of rows since the
+ * router's top_k experts of a row are distinct); `ticket` is a device int32
+ * that must hold 0 before the first launch and is left at 0 by every launch.
  */
 int d3_moe_front(const uint8_t *occupancy, int32_t num_slots, int32_t *active_slots,
                  int32_t *count, const uint16_t *x, int64_t x_row_stride, const void *logits,

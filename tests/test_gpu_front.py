@@ -39,7 +39,7 @@ def test_fused_front_matches_standalone_kernels(device, hidden, experts, p):
     x, logits, xd, ld = _inputs(device, slots, hidden, experts, int(p * 100) + experts)
     occ = (np.random.default_rng(experts).uniform(size=slots) < p).astype(np.uint8)
     occ_d = torch.from_numpy(occ).to(device)
-    fused = MoEWorkspace(Shape(slots, experts, hidden, 256), device)
+    fused = MoEWorkspace(Shape(slots, experts, hidden, 256), device, fused_sort=True)
     active = torch.empty(slots, dtype=torch.int32, device=device)
     count = torch.empty(1, dtype=torch.int32, device=device)
     for launch in range(3):  # the ticket must be back to 0 after every launch
@@ -74,24 +74,50 @@ def test_fused_front_matches_standalone_kernels(device, hidden, experts, p):
         assert np.array_equal(got["q"], q) and np.array_equal(got["scales"], s)
 
 
-def test_fused_front_row_mode_with_index(device):
-    """Row mode (mixed batches): row_index gathers rows, the sort is fused
-    while pairs <= 8192 and falls back to the sort kernel beyond."""
+@pytest.mark.parametrize("rows,experts,live", [
+    (560, 16, None),    # 4480 pairs: fused row-mask sort
+    (1100, 16, None),   # 8800 pairs: the standalone sort kernel
+    (1024, 128, None),  # 8192 pairs, 128 x 16 mask words: the row-mask sort at its limits
+    (600, 256, None),   # 256 x 10 mask words: the fused ballot sort
+    (1000, 128, 301),   # device row count below capacity
+    (1, 16, None),
+])
+@pytest.mark.parametrize("fused", [True, False])
+def test_fused_front_row_mode_with_index(device, rows, experts, live, fused):
+    """Row mode (mixed batches): row_index gathers rows; the sort is fused
+    (opt-in) while pairs <= 8192 (row masks while E x ceil(rows / 64) <= 2048,
+    else the chunked ballot sort) and otherwise the sort kernel's (row masks
+    while they fit, else the ballot sort); every variant gives the oracle's
+    sort, inverse map and work items."""
     from drama3_amd.pipeline import MoEWorkspace, Shape
 
-    for rows in (560, 1100):  # 4480 pairs (fused) and 8800 pairs (standalone sort)
-        x, logits, xd, ld = _inputs(device, rows + 7, 1024, 16, rows)
-        index = torch.from_numpy(np.random.default_rng(rows).permutation(rows + 7)[:rows]).to(torch.int32)
-        ws = MoEWorkspace(Shape(rows, 16, 1024, 256), device)
-        ws.front(xd, ld, row_index=index.to(device))
+    x, logits, xd, ld = _inputs(device, rows + 7, 1024, experts, rows + experts)
+    index = torch.from_numpy(np.random.default_rng(rows).permutation(rows + 7)[:rows]).to(torch.int32)
+    ws = MoEWorkspace(Shape(rows, experts, 1024, 256), device, item_rows=128 if rows > 128 else None,
+                      fused_sort=fused)
+    count = None if live is None else torch.tensor([live], dtype=torch.int32, device=device)
+    n = rows if live is None else live
+    for _ in range(2):
+        ws.front(xd, ld, row_index=index.to(device), row_count=count)
         torch.cuda.synchronize()
-        idx = index.numpy()
+        idx = index.numpy()[:n]
         weights, ids = om.route(np_f32(logits)[idx])
-        assert np.array_equal(ws.ids.cpu().numpy(), ids)
-        o = om.sort_routes(ids, 16, ws.tile)
+        assert np.array_equal(ws.ids.cpu().numpy()[:n], ids)
+        o = om.sort_routes(ids, experts, ws.tile)
         assert int(ws.total.item()) == o.total
-        assert np.array_equal(ws.sorted_ids.cpu().numpy()[:o.total], o.sorted_ids)
-        assert np.array_equal(ws.inverse.cpu().numpy(), o.inverse)
+        assert np.array_equal(ws.counts.cpu().numpy(), o.counts)
+        assert np.array_equal(ws.starts.cpu().numpy(), o.starts)
+        sorted_ids = ws.sorted_ids.cpu().numpy()
+        assert np.array_equal(sorted_ids[:o.total], o.sorted_ids)
+        assert np.all(sorted_ids[o.total:] == n * 8)
+        assert np.array_equal(ws.expert_ids.cpu().numpy()[:o.total // ws.tile], o.expert_ids)
+        assert np.array_equal(ws.inverse.cpu().numpy()[:n * 8], o.inverse)
+        # work items: each expert's routes in chunks of item_rows, in expert order
+        want = [(e, int(o.starts[e]) + j, min(ws.item_rows, int(o.counts[e]) - j), 0)
+                for e in range(experts) for j in range(0, int(o.counts[e]), ws.item_rows)]
+        num_items = int(ws.num_items.item())
+        assert num_items == len(want)
+        assert np.array_equal(ws.items.cpu().numpy().reshape(-1, 4)[:num_items], np.array(want))
         assert int(ws.ticket.item()) == 0
 
 

@@ -150,6 +150,30 @@ def test_sort_routes(device, tokens, experts, tile, dtype):
     assert np.array_equal(inverse.cpu().numpy(), o.inverse)
 
 
+@pytest.mark.parametrize("tokens,experts,where", [(300, 16, "last"), (40, 8, "every"),
+                                                  (1000, 64, "first")])
+def test_sort_routes_repeated_expert_in_a_row(device, tokens, experts, where):
+    """Ids that repeat an expert inside a row (not router output, but the
+    operator accepts them): the row-mask sort must hand over to the ballot
+    sort and the result is still the oracle's stable sort."""
+    from drama3_amd.kernels import sort_routes
+
+    rng = np.random.default_rng(tokens + experts)
+    ids = np.stack([rng.permutation(experts)[:8] for _ in range(tokens)])
+    if where == "every":
+        ids = rng.integers(0, experts, ids.shape)
+    else:
+        row = tokens - 1 if where == "last" else 0
+        ids[row, 5] = ids[row, 2]
+    counts, starts, total, sorted_ids, expert_ids, inverse = sort_routes(
+        torch.from_numpy(ids).to(torch.int32).to(device), experts, 16)
+    o = om.sort_routes(ids, experts, 16)
+    assert np.array_equal(counts.cpu().numpy(), o.counts)
+    assert int(total.item()) == o.total
+    assert np.array_equal(sorted_ids.cpu().numpy()[:o.total], o.sorted_ids)
+    assert np.array_equal(inverse.cpu().numpy(), o.inverse)
+
+
 def test_sort_routes_skewed_single_expert(device):
     from drama3_amd.kernels import sort_routes
 
