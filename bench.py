@@ -57,6 +57,9 @@ def parse():
                    help="skip the decode step at the reference model's MoE shape (E256, I512)")
     p.add_argument("--no-mixed", action="store_true",
                    help="skip the config-5 mixed decode + prefill step")
+    p.add_argument("--mixed-only", action="store_true",
+                   help="measure only the config-5 mixed step (one JSON line)")
+    p.add_argument("--mixed-steps", type=int, default=50)
     return p.parse_args()
 
 
@@ -277,6 +280,9 @@ def main():
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(torch, args.prefill_steps)}), flush=True)
         return
+    if args.mixed_only:
+        print(json.dumps({"mixed": bench_mixed(torch, args.mixed_steps)}), flush=True)
+        return
 
     device = torch.device("cuda:0")
     w = workloads.config2()
@@ -412,7 +418,7 @@ def main():
 
     prefill = None if args.no_prefill else bench_prefill(torch, args.prefill_steps)
     reference_shape = None if args.no_reference_shape else bench_reference_shape(torch)
-    mixed = None if args.no_mixed else bench_mixed(torch)
+    mixed = None if args.no_mixed else bench_mixed(torch, args.mixed_steps)
 
     result = {
         "metric": baseline_metric(),
