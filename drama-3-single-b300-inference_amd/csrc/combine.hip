@@ -9,6 +9,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "expert_tile.h"
 #include "status.h"
 
 namespace d3 {
@@ -86,28 +87,52 @@ __global__ __launch_bounds__(kThreads) void combine_experts_kernel(
   }
 }
 
-// kMode 0: add_norm(x, residual); 1: combine_experts_add_norm(_inverse).
+// Per-route fp32 rows of the MoE (down [rows * top_k, width], by pair) and
+// their routing weights, for kMode 2.
+struct RouteRows {
+  const float* down;
+  const void* weights;
+  int weights_f32;
+  int top_k;
+};
+
+// kMode 0: add_norm(x, residual); 1: combine_experts_add_norm(_inverse);
+// 2: mode 1 with each routed row reduced here from the per-route rows: the
+//    rank-order fp32 sum of d3_weighted_combine, rounded to bf16 as it does,
+//    so the bytes equal d3_weighted_combine followed by mode 1.
 template <int kMode>
 __global__ __launch_bounds__(kThreads) void add_norm_kernel(
     const uint16_t* __restrict__ routed, const uint16_t* __restrict__ shared,
     const uint16_t* __restrict__ gate, int64_t gate_stride, const int64_t* __restrict__ inverse,
     uint16_t* __restrict__ residual, const uint16_t* __restrict__ weight, float eps, int width,
-    uint16_t* __restrict__ out) {
+    uint16_t* __restrict__ out, RouteRows routes) {
   __shared__ float scratch[kThreads / kWave];
   const int row = blockIdx.x;
   const int source = inverse != nullptr ? static_cast<int>(inverse[row]) : row;
   const int64_t src = static_cast<int64_t>(source) * width;
   const int64_t dst = static_cast<int64_t>(row) * width;
   float g = 0.0f;
-  if constexpr (kMode == 1) g = gate_bf16(gate, gate_stride, source);
+  if constexpr (kMode != 0) g = gate_bf16(gate, gate_stride, source);
   float values[kMaxPerThread];
   float squares = 0.0f;
   int count = 0;
   for (int column = threadIdx.x * 4; column < width; column += kThreads * 4, count += 4) {
     float r[4], res[4], v[4];
-    load4(routed + src + column, r);
+    if constexpr (kMode == 2) {
+      const float4 sum = routes.top_k == 8
+                             ? combine4_fixed<8>(routes.down, routes.weights, routes.weights_f32,
+                                                 source, width, column)
+                             : combine4(routes.down, routes.weights, routes.weights_f32, source,
+                                        routes.top_k, width, column);
+      r[0] = round_bf16(sum.x);
+      r[1] = round_bf16(sum.y);
+      r[2] = round_bf16(sum.z);
+      r[3] = round_bf16(sum.w);
+    } else {
+      load4(routed + src + column, r);
+    }
     load4(residual + dst + column, res);
-    if constexpr (kMode == 1) {
+    if constexpr (kMode != 0) {
       float s[4];
       load4(shared + src + column, s);
 #pragma unroll
@@ -190,8 +215,37 @@ extern "C" int d3_combine_experts_add_norm(const uint16_t* routed, const uint16_
     return D3_OK;
   }
   hipLaunchKernelGGL(add_norm_kernel<1>, dim3(rows), dim3(kThreads), 0, as_stream(stream), routed,
-                     shared, gate, gate_stride, inverse, residual, weight, eps, width, out);
+                     shared, gate, gate_stride, inverse, residual, weight, eps, width, out,
+                     RouteRows{});
   D3_LAUNCHED("combine_experts_add_norm");
+}
+
+extern "C" int d3_combine_routes_add_norm(const float* down, const void* route_weights,
+                                          int32_t weights_dtype, int32_t top_k,
+                                          const uint16_t* shared, const uint16_t* gate,
+                                          int64_t gate_stride, const int64_t* inverse,
+                                          uint16_t* residual, const uint16_t* weight, float eps,
+                                          int32_t rows, int32_t width, uint16_t* out,
+                                          void* stream) {
+  D3_REQUIRE(down && route_weights && shared && gate && residual && weight && out,
+             "combine_routes_add_norm: null pointer");
+  D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
+             "combine_routes_add_norm: weights must be bf16 or f32");
+  D3_REQUIRE(top_k >= 1 && top_k <= 16, "combine_routes_add_norm: bad top_k %d", top_k);
+  D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0 && width <= kThreads * kMaxPerThread,
+             "combine_routes_add_norm: width %d must be a multiple of 4 and <= 8192", width);
+  D3_REQUIRE((reinterpret_cast<uintptr_t>(down) & 15u) == 0 && aligned8(shared) &&
+                 aligned8(residual) && aligned8(out) && aligned8(weight),
+             "combine_routes_add_norm: alignment");
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  const RouteRows routes{down, route_weights, weights_dtype == D3_DTYPE_F32 ? 1 : 0, top_k};
+  hipLaunchKernelGGL(add_norm_kernel<2>, dim3(rows), dim3(kThreads), 0, as_stream(stream),
+                     nullptr, shared, gate, gate_stride, inverse, residual, weight, eps, width,
+                     out, routes);
+  D3_LAUNCHED("combine_routes_add_norm");
 }
 
 extern "C" int d3_add_norm(const uint16_t* x, uint16_t* residual, const uint16_t* weight, float eps,
@@ -206,7 +260,7 @@ extern "C" int d3_add_norm(const uint16_t* x, uint16_t* residual, const uint16_t
     return D3_OK;
   }
   hipLaunchKernelGGL(add_norm_kernel<0>, dim3(rows), dim3(kThreads), 0, as_stream(stream), x,
-                     nullptr, nullptr, 0, nullptr, residual, weight, eps, width, out);
+                     nullptr, nullptr, 0, nullptr, residual, weight, eps, width, out, RouteRows{});
   D3_LAUNCHED("add_norm");
 }
 

@@ -419,31 +419,8 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(
 // ---------------------------------------------------------------------------
 // Weighted combine: out[t] = bf16(sum_r w[t,r] * down[t*K + r]) in rank order.
 // ---------------------------------------------------------------------------
-// One workgroup per (row, 512-column slice).  With top_k = 8 every load of
-// the slice (8 route rows + 8 weights + the row count) is issued before the
-// first FMA.
-template <int kTopK>
-__device__ __forceinline__ float4 combine4_fixed(const float* down, const void* weights,
-                                                 int weights_f32, int token, int hidden,
-                                                 int column) {
-  float w[kTopK];
-  float4 y[kTopK];
-#pragma unroll
-  for (int r = 0; r < kTopK; ++r) {
-    w[r] = route_weight(weights, weights_f32, static_cast<size_t>(token) * kTopK + r);
-    y[r] = *reinterpret_cast<const float4*>(down + (static_cast<size_t>(token) * kTopK + r) * hidden +
-                                            column);
-  }
-  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-  for (int r = 0; r < kTopK; ++r) {
-    acc.x = fmaf(w[r], y[r].x, acc.x);
-    acc.y = fmaf(w[r], y[r].y, acc.y);
-    acc.z = fmaf(w[r], y[r].z, acc.z);
-    acc.w = fmaf(w[r], y[r].w, acc.w);
-  }
-  return acc;
-}
+// One workgroup per (row, 512-column slice); with top_k = 8 every load of
+// the slice is issued before the first FMA (combine4_fixed).
 
 // 128 threads x 4 columns: a c2 decode step (52 rows x 2048 columns) spreads
 // over 208 workgroups, so most CUs have one row slice in flight.

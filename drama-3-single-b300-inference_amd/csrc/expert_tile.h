@@ -191,6 +191,31 @@ __device__ __forceinline__ float4 combine4(const float* down, const void* weight
   return acc;
 }
 
+// combine4 for a compile-time top_k: every route row and weight is loaded
+// before the first FMA; the same rank-order chain, so the same bits.
+template <int kTopK>
+__device__ __forceinline__ float4 combine4_fixed(const float* down, const void* weights,
+                                                 int weights_f32, int token, int hidden,
+                                                 int column) {
+  float w[kTopK];
+  float4 y[kTopK];
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    w[r] = route_weight(weights, weights_f32, static_cast<size_t>(token) * kTopK + r);
+    y[r] = *reinterpret_cast<const float4*>(down + (static_cast<size_t>(token) * kTopK + r) * hidden +
+                                            column);
+  }
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    acc.x = fmaf(w[r], y[r].x, acc.x);
+    acc.y = fmaf(w[r], y[r].y, acc.y);
+    acc.z = fmaf(w[r], y[r].z, acc.z);
+    acc.w = fmaf(w[r], y[r].w, acc.w);
+  }
+  return acc;
+}
+
 __device__ __forceinline__ uint2 pack_bf16x4(float4 v) {
   const uint32_t lo = f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
   const uint32_t hi = f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);

@@ -89,6 +89,8 @@ SIGNATURES = {
     "d3_combine_experts": (_i32, [_p, _p, _p, _i64, _i32, _i32, _p, _p]),
     "d3_combine_experts_add_norm": (
         _i32, [_p, _p, _p, _i64, _p, _p, _p, _f32, _i32, _i32, _p, _p]),
+    "d3_combine_routes_add_norm": (_i32, [_p, _p, _i32, _i32, _p, _p, _i64, _p, _p, _p, _f32,
+                                          _i32, _i32, _p, _p]),
     "d3_add_norm": (_i32, [_p, _p, _p, _f32, _i32, _i32, _p, _p]),
     "d3_silu_mul": (_i32, [_p, _i64, _i32, _i32, _p, _p]),
     "d3_row_metadata": (_i32, [_p, _p, _i32, _i32, _p, _i32, _i64, _p, _p, _p, _p]),

@@ -82,11 +82,12 @@ class MixedRows:
 class MixedStep:
     """The MoE side of one mixed step, graph-capturable with fixed buffers.
 
-    Per step (``run``): the mixed rows, the prefill suffix's row metadata
+    Per step (``forward``): the mixed rows, the prefill suffix's row metadata
     (``row_metadata`` of ``mixed_graph.py:96-107``), the routed experts over
     the kept rows (``model.moe_parts(normalized.index_select(0, keep), ...)``,
     ``mixed_model.py:237-243``) and ``combine_experts_add_norm_inverse`` back
-    onto every row (``mixed_model.py:198-201``).
+    onto every row (``mixed_model.py:198-201``), the routed rows' weighted
+    combine folded into that last launch (``routed`` is then not written).
 
     Inputs written into the staging buffers before a replay: ``occupancy``,
     ``boundaries`` (int32 [sequences + 1], the reference layout's boundaries
@@ -100,7 +101,8 @@ class MixedStep:
 
     def __init__(self, slots: int, decode_rows: int, capacity: int, padding_start: int,
                  sequences: int, num_experts: int, hidden: int, intermediate: int,
-                 top_k: int = 8, codes: int = 11, reuse: bool = True, device="cuda"):
+                 top_k: int = 8, codes: int = 11, reuse: bool = True, device="cuda",
+                 separate_combine: bool = False):
         dev = torch.device(device)
         self.device = dev
         self.rows = MixedRows(slots, decode_rows, capacity, padding_start, dev)
@@ -109,6 +111,9 @@ class MixedStep:
             raise ValueError(f"prefix reuse needs <= {MAX_REUSE_PROMPTS} prompts and "
                              f"<= {MAX_REUSE_ROWS} rows")
         self.sequences, self.reuse, self.hidden = sequences, reuse, hidden
+        # separate_combine: the routed combine (into ``routed``) and the
+        # residual + RMSNorm combine as two launches instead of one.
+        self.separate_combine = separate_combine
         bf16 = dict(dtype=torch.bfloat16, device=dev)
         self.occupancy = torch.zeros(slots, dtype=torch.uint8, device=dev)
         self.boundaries = torch.zeros(sequences + 1, dtype=torch.int32, device=dev)
@@ -139,16 +144,18 @@ class MixedStep:
         if r.capacity:
             packed_row_metadata(self.boundaries, self.sequence_slots, r.capacity, self.positions,
                                 self.row_slots)
-        self.workspace.forward(self.x, self.logits, experts, row_index=r.keep,
-                               row_count=r.keep_count, out=self.routed, stream=stream)
-        self._combine(stream)
+        ws = self.workspace
+        ws.front(self.x, self.logits, r.keep, r.keep_count, stream=stream)
+        ws.routes_down(experts, r.keep_count, stream)
+        if self.separate_combine:
+            ws.combine(None, r.keep_count, None, self.routed, stream)
+            call("d3_combine_experts_add_norm", ptr(self.routed), ptr(self.shared),
+                 ptr(self.gate), 1, ptr(r.inverse), ptr(self.residual), ptr(self.norm_weight),
+                 float(self.epsilon), r.full, self.hidden, ptr(self.out), stream)
+        else:
+            ws.combine_add_norm(self.shared, self.gate, self.residual, self.norm_weight,
+                                self.epsilon, r.inverse, self.out, stream)
         return self.out
-
-    def _combine(self, stream) -> None:
-        full, h = self.rows.full, self.hidden
-        call("d3_combine_experts_add_norm", ptr(self.routed), ptr(self.shared), ptr(self.gate), 1,
-             ptr(self.rows.inverse), ptr(self.residual), ptr(self.norm_weight),
-             float(self.epsilon), full, h, ptr(self.out), stream)
 
     def capture(self, experts, pool=None) -> None:
         """Capture ``forward`` once (after two warm-up runs on a side stream,

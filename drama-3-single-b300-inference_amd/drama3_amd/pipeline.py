@@ -427,27 +427,57 @@ class MoEWorkspace:
         With ``fused_epilogues`` two launches replace four; a dense shared
         expert is always added by the separate combine."""
         stream = _lib.stream(self.device) if stream is None else stream
+        if self.fuse_fc2 and shared is None and not (self.sortless or self.grouped):
+            if self.fuse_fc1:
+                self.fc1_swiglu(experts, stream)
+            else:
+                self.fc1(experts, stream)
+                self.activation(stream)
+            return self.fc2_combine(experts, out, stream)
+        self.routes_down(experts, row_count, stream)
+        return self.combine(None, row_count, shared, out, stream)
+
+    def routes_down(self, experts, row_count=None, stream=None) -> torch.Tensor:
+        """Everything experts() runs before the combine: the fp32 per-route
+        rows in ``down`` (by pair)."""
+        stream = _lib.stream(self.device) if stream is None else stream
         if self.sortless:
             self.decode_fc1(experts, row_count, stream)
             self.decode_fc2(experts, row_count, stream)
-            return self.combine(None, row_count, shared, out, stream)
-        if self.grouped:
+        elif self.grouped:
             self.grouped_fc1(experts, stream=stream)
             self.grouped_fc2(experts, stream=stream)
-            return self.combine(None, row_count, shared, out, stream)
-        if self.fuse_fc1:
+        elif self.fuse_fc1:
             self.fc1_swiglu(experts, stream)
-        else:
-            self.fc1(experts, stream)
-        if self.fuse_fc2 and shared is None:
-            if not self.fuse_fc1:
-                self.activation(stream)
-            return self.fc2_combine(experts, out, stream)
-        if self.fuse_fc1:
             self.fc2(experts, stream)
         else:
+            self.fc1(experts, stream)
             self._fc2_stage(experts, stream)
-        return self.combine(None, row_count, shared, out, stream)
+        return self.down
+
+    def combine_add_norm(self, shared, gate, residual, norm_weight, epsilon, inverse=None,
+                         out=None, stream=None) -> torch.Tensor:
+        """The weighted combine of ``down`` fused with
+        ``combine_experts_add_norm(_inverse)``: row r of ``residual`` / ``out``
+        takes MoE row ``inverse[r]`` (int64; None = r) of the routed combine,
+        gated ``shared`` and ``gate``; ``residual`` is updated in place.  The
+        same bytes as combine() followed by that operator."""
+        s, stream = self.shape, self._stream(stream)
+        require_cuda(shared, gate, residual, norm_weight, inverse, out)
+        rows, width = residual.shape
+        if width != s.hidden or shared.shape[1] != s.hidden or len(shared) < 1:
+            raise ValueError("shared and residual rows must be [*, hidden]")
+        if inverse is not None and (inverse.dtype != torch.int64 or inverse.numel() != rows):
+            raise ValueError("inverse must be int64 [rows]")
+        if inverse is None and rows > s.rows:
+            raise ValueError("without inverse, residual rows index MoE rows directly")
+        gate_stride = gate.stride(0)
+        out = torch.empty_like(residual) if out is None else out
+        call("d3_combine_routes_add_norm", ptr(self.down), ptr(self.weights),
+             dtype_code(self.weights.dtype), s.top_k, ptr(shared), ptr(gate), gate_stride,
+             ptr(inverse), ptr(residual), ptr(norm_weight), float(epsilon), rows, width, ptr(out),
+             stream)
+        return out
 
 
 class DenseExpert:

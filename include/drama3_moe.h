@@ -500,6 +500,25 @@ int d3_combine_experts_add_norm(const uint16_t *routed, const uint16_t *shared,
                                 uint16_t *out, void *stream);
 
 /*
+ * A11 + A12  Weighted combine of the per-route rows, then combine + residual
+ * + RMSNorm, in one launch.
+ * Replaces native_moe's down.view(T, 8, H).sum(1) (src/drama3/kernels.py:779)
+ * followed by combine_experts_add_norm(_inverse) (kernels.py:448-556).
+ * Row r reads MoE row m = inverse[r] (int64) when inverse != NULL, else r;
+ * routed = bf16(sum_k w[m, k] * down[m * top_k + k, :]) in rank order with
+ * fp32 accumulation (exactly d3_weighted_combine's bytes), then the
+ * d3_combine_experts_add_norm rule.  down f32 [MoE rows * top_k, width]
+ * (16-byte aligned); w bf16 or f32 [MoE rows, top_k]; shared bf16
+ * [MoE rows, width]; gate bf16 (row stride gate_stride); residual bf16
+ * [rows, width] updated in place; out bf16 [rows, width].  width <= 8192.
+ */
+int d3_combine_routes_add_norm(const float *down, const void *route_weights,
+                               int32_t weights_dtype, int32_t top_k, const uint16_t *shared,
+                               const uint16_t *gate, int64_t gate_stride, const int64_t *inverse,
+                               uint16_t *residual, const uint16_t *weight, float eps,
+                               int32_t rows, int32_t width, uint16_t *out, void *stream);
+
+/*
  * Residual add + RMSNorm without the MoE combine.
  * Replaces add_norm (src/drama3/kernels.py:405-424).
  */

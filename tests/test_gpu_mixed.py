@@ -147,9 +147,12 @@ def test_mixed_step_graph_replays(device):
     padding from slot 32 on), two 256-row prompts with shared prefixes in a
     640-row suffix.  One capture; four replays with 4 slots retired and 4
     admitted between them and eager work in between; each replay equals an
-    eager run bit for bit and the oracle (layout exact, routed rows within
-    the FP8 contraction tolerance, combine within one ulp on those rows)."""
+    eager run bit for bit, its fused routed + residual combine equals the
+    two-launch chain bit for bit, and it matches the oracle (layout exact,
+    routed rows within the FP8 contraction tolerance, combine within one ulp
+    on those rows)."""
     from drama3_amd import workloads
+    from drama3_amd.kernels import combine_experts_add_norm_inverse
     from drama3_amd.mixed import MixedStep
 
     w = workloads.config5()
@@ -172,11 +175,19 @@ def test_mixed_step_graph_replays(device):
         scratch = torch.randn(1000, 1000, device=device).sum()  # eager work between replays
         out = step.replay().clone()
         torch.cuda.synchronize()
-        routed = step.routed.clone()
         residual = step.residual.clone()
         keep = step.rows.keep.cpu().numpy()
         keep_count = int(step.rows.keep_count.item())
         inverse = step.rows.inverse.cpu().numpy()
+        # the fused routed + residual combine equals the two-launch chain bit
+        # for bit (d3_weighted_combine, then d3_combine_experts_add_norm)
+        routed = step.workspace.combine(None, step.rows.keep_count, None, step.routed).clone()
+        res2 = host["residual"].to(device)
+        out2 = combine_experts_add_norm_inverse(routed, step.shared, step.gate, step.rows.inverse,
+                                                res2, step.norm_weight, step.epsilon)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+        assert torch.equal(residual.view(torch.int16), res2.view(torch.int16))
         # the layout
         expected = om.mixed_layout(occupancy, d, padding_start, host["boundaries"], 2, capacity,
                                    host["frames"])

@@ -336,6 +336,44 @@ def test_fc2_swiglu_prologue_matches_separate_stages(device, hidden, inter, expe
     assert torch.equal(ws.down.view(torch.int32), separate.view(torch.int32))
 
 
+# --------------------------------------------------------------------------- A11 + A12
+@pytest.mark.parametrize("top_k,wdtype,with_inverse", [(8, torch.bfloat16, True),
+                                                       (8, torch.float32, False),
+                                                       (6, torch.bfloat16, True),
+                                                       (1, torch.float32, True)])
+def test_combine_routes_add_norm_equals_two_launches(device, top_k, wdtype, with_inverse):
+    """d3_combine_routes_add_norm = d3_weighted_combine followed by
+    d3_combine_experts_add_norm, byte for byte (routed, residual and out)."""
+    from drama3_amd import _lib
+    from drama3_amd._lib import call, ptr
+
+    rng = np.random.default_rng(top_k + (7 if with_inverse else 0))
+    moe_rows, rows, width = 37, 50, 1024
+    down = torch.from_numpy(rng.standard_normal((moe_rows * top_k, width)).astype(np.float32)).to(device)
+    w = torch.from_numpy(rng.random((moe_rows, top_k)).astype(np.float32)).to(wdtype).to(device)
+    shared = bf16_tensor(rng, (moe_rows, width), device)
+    gate = bf16_tensor(rng, (moe_rows,), device)
+    norm = bf16_tensor(rng, (width,), device, 0.1)
+    res0 = bf16_tensor(rng, (rows if with_inverse else moe_rows, width), device)
+    inverse = (torch.from_numpy(rng.integers(0, moe_rows, rows)).to(device) if with_inverse
+               else None)
+    n = len(res0)
+    wcode = 1 if wdtype == torch.float32 else 0
+    stream = _lib.stream(device)
+    routed = torch.empty((moe_rows, width), dtype=torch.bfloat16, device=device)
+    call("d3_weighted_combine", ptr(down), ptr(w), wcode, moe_rows, top_k, width, None, None,
+         ptr(routed), stream)
+    res_a, out_a = res0.clone(), torch.empty_like(res0)
+    call("d3_combine_experts_add_norm", ptr(routed), ptr(shared), ptr(gate), 1, ptr(inverse),
+         ptr(res_a), ptr(norm), 1e-6, n, width, ptr(out_a), stream)
+    res_b, out_b = res0.clone(), torch.empty_like(res0)
+    call("d3_combine_routes_add_norm", ptr(down), ptr(w), wcode, top_k, ptr(shared), ptr(gate), 1,
+         ptr(inverse), ptr(res_b), ptr(norm), 1e-6, n, width, ptr(out_b), stream)
+    torch.cuda.synchronize()
+    assert torch.equal(res_a.view(torch.int16), res_b.view(torch.int16))
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16))
+
+
 # --------------------------------------------------------------------------- A12
 def test_combine_kernels(device):
     from drama3_amd.kernels import (add_norm, combine_experts, combine_experts_add_norm,
