@@ -211,7 +211,9 @@ def bench_reference_shape(torch, steps: int = 30, copies: int = 3) -> dict:
     return {"workload": "decode, 64 live slots, H2048 E256 I512 top-8 (the reference model's MoE)",
             "us_per_step": round(us, 2), "used_experts": used, "algorithmic_bytes_per_step": nbytes,
             "GB_s": round(nbytes / us / 1e3, 1), "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-            "step": "FC1 from the slots + sortless FC2 + routed combine",
+            "step": ("FC1 from the slots + sortless FC2 + routed combine"
+                     if ds.workspace.sortless and ds.uses_frontless(occ, x, logits)
+                     else "front + route sort + expert GEMMs + combine"),
             "timing": f"hipGraph, {copies} rotated weight copies"}
 
 

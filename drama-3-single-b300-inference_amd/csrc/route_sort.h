@@ -318,11 +318,14 @@ __device__ bool sort_rows_block(const void* __restrict__ ids, int rows, int top_
   const int words = mask_words(rows);
   const int cells = num_experts * words;
 
+  // Every loop over this thread's pairs stops at the last chunk holding a
+  // pair (a uniform exit: small batches pay for the chunks they use).
+  const int chunks = (pairs + THREADS - 1) / THREADS;
   int expert[kPerThread];
 #pragma unroll
   for (int c = 0; c < kPerThread; ++c) {
     const int p = c * THREADS + tid;
-    expert[c] = p < pairs ? load_route_id<kI64, kCollect>(ids, p) : -1;
+    expert[c] = c < chunks && p < pairs ? load_route_id<kI64, kCollect>(ids, p) : -1;
   }
   for (int i = tid; i < cells; i += THREADS) masks[i] = 0;
   __syncthreads();
@@ -335,6 +338,7 @@ __device__ bool sort_rows_block(const void* __restrict__ ids, int rows, int top_
   bool repeated = false;
 #pragma unroll
   for (int c = 0; c < kPerThread; ++c) {
+    if (c >= chunks) break;
     const int e = expert[c];
     const int r = row_of(c * THREADS + tid);
     if (e >= 0 && e < num_experts) {
@@ -359,6 +363,7 @@ __device__ bool sort_rows_block(const void* __restrict__ ids, int rows, int top_
                           &total, &total_items);
 #pragma unroll
   for (int c = 0; c < kPerThread; ++c) {
+    if (c >= chunks) break;
     const int p = c * THREADS + tid;
     const int e = expert[c];
     if (e >= 0 && e < num_experts) {
