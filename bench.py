@@ -54,7 +54,8 @@ def parse():
                    help="measure only the config-4 packed prefill (one JSON line)")
     p.add_argument("--prefill-steps", type=int, default=20)
     p.add_argument("--no-reference-shape", action="store_true",
-                   help="skip the decode step at the reference model's MoE shape (E256, I512)")
+                   help="skip the decode step and the whole MoE layer at the reference model's "
+                        "shape (E256, I512)")
     p.add_argument("--no-mixed", action="store_true",
                    help="skip the config-5 mixed decode + prefill step")
     p.add_argument("--mixed-only", action="store_true",
@@ -214,6 +215,49 @@ def bench_reference_shape(torch, steps: int = 30, copies: int = 3) -> dict:
             "step": ("FC1 from the slots + sortless FC2 + routed combine"
                      if ds.workspace.sortless and ds.uses_frontless(occ, x, logits)
                      else "front + route sort + expert GEMMs + combine"),
+            "timing": f"hipGraph, {copies} rotated weight copies"}
+
+
+def bench_moe_layer(torch, steps: int = 30, copies: int = 3) -> dict:
+    """One whole MoE layer (``MoELayer``: packed bf16 input projection, routed
+    top-8 FP8 experts, bf16 shared expert, combine) at the reference model's
+    shape (64 rows, H2048, E256, I512, shared I512), shared expert on a side
+    stream and in line; three rotated weight copies per graph (cold)."""
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.moe_layer import MoELayer, pack_input_projection
+
+    device = torch.device("cuda:0")
+    rows, e, h, i, si = 64, 256, 2048, 512, 512
+    gen = torch.Generator("cpu").manual_seed(9)
+
+    def bf16(*shape, scale):
+        return (torch.randn(shape, generator=gen) * scale).to(torch.bfloat16).to(device)
+
+    sets = []
+    for _ in range(copies):
+        experts = prepare_experts(workloads.make_experts(gen, e, h, i).to(device))
+        projection = pack_input_projection(bf16(si, h, scale=h ** -0.5), bf16(si, h, scale=h ** -0.5),
+                                           bf16(e, h, scale=h ** -0.5), bf16(1, h, scale=h ** -0.5))
+        sets.append((experts, projection, bf16(h, si, scale=si ** -0.5)))
+    x = workloads._bf16(gen, (rows, h)).to(device)
+    out = {}
+    for name, overlap in (("side_stream", True), ("in_line", False)):
+        layer = MoELayer(rows, e, h, i, si, device=device, overlap=overlap)
+        for experts, projection, down in sets:
+            layer(x, projection, down, experts)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for experts, projection, down in sets:
+                layer(x, projection, down, experts)
+        g.replay()
+        out[name] = round(time_graphs(torch, [g], max(1, steps // copies)) / copies, 2)
+    return {"workload": "one MoE layer, 64 rows, H2048 E256 I512 top-8 + bf16 shared expert "
+                        "(I512), packed input projection (the reference model's layer)",
+            "us_per_layer": out,
+            "step": "bf16 projection GEMM -> [routed experts (decode step) || SwiGLU + bf16 "
+                    "down GEMM] -> combine_experts",
             "timing": f"hipGraph, {copies} rotated weight copies"}
 
 
@@ -421,6 +465,7 @@ def main():
     prefill = None if args.no_prefill else bench_prefill(torch, args.prefill_steps)
     reference_shape = None if args.no_reference_shape else bench_reference_shape(torch)
     mixed = None if args.no_mixed else bench_mixed(torch, args.mixed_steps)
+    moe_layer = None if args.no_reference_shape else bench_moe_layer(torch)
 
     result = {
         "metric": baseline_metric(),
@@ -469,6 +514,7 @@ def main():
         "prefill": prefill,
         "reference_shape": reference_shape,
         "mixed": mixed,
+        "moe_layer": moe_layer,
     }
     print(json.dumps(result), flush=True)
 
