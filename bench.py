@@ -305,8 +305,9 @@ def bench_mixed(torch, steps: int = 50) -> dict:
     return {"workload": "config 5 mixed step: 48 of 64 decode slots + 2 x 256 prompt rows "
                         "(640-row suffix), E16 H1024 I256 top-8",
             "rows": full, "live_rows": 48 + 512, **out,
-            "step": "d3_mixed_rows + row_metadata + MoE on the kept rows, then the routed "
-                    "combine + residual + RMSNorm onto all rows in one launch; one hipGraph",
+            "step": "d3_mixed_rows (with the suffix's row metadata) + MoE on the kept rows, "
+                    "then the routed combine + residual + RMSNorm onto all rows in one launch; "
+                    "one hipGraph",
             "timing": "graph replays; the residual is updated in place on every replay"}
 
 

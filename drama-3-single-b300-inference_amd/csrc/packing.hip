@@ -138,9 +138,11 @@ __device__ __forceinline__ int block_rank(bool flag, int* wave_counts, int* tota
 __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
     const uint8_t* __restrict__ occupancy, int num_slots, int decode_rows, int64_t padding_start,
     const int32_t* __restrict__ boundaries, int prompts, int capacity,
-    const int64_t* __restrict__ frames, int codes, int32_t* __restrict__ active,
-    int32_t* __restrict__ count, int64_t* __restrict__ decode_slots, int32_t* __restrict__ keep,
-    int32_t* __restrict__ keep_count, int64_t* __restrict__ inverse) {
+    const int64_t* __restrict__ frames, int codes, const int64_t* __restrict__ sequence_slots,
+    int sequences, int32_t* __restrict__ active, int32_t* __restrict__ count,
+    int64_t* __restrict__ decode_slots, int32_t* __restrict__ keep,
+    int32_t* __restrict__ keep_count, int64_t* __restrict__ inverse,
+    int64_t* __restrict__ positions, int64_t* __restrict__ row_slots) {
   __shared__ int32_t owner_of[kMixedMaxRows];  // owner row; -(rank + 1) once kept
   __shared__ int wave_counts[kMixedWaves];
   __shared__ int starts[kMixedMaxPrompts + 1];
@@ -229,6 +231,17 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
     }
   }
 
+  // Optional: the suffix rows' positions and slots, row_metadata_kernel's
+  // rule on the raw boundaries (sequences + 1 of them).
+  if (positions != nullptr) {
+    for (int r = tid; r < capacity; r += kMixedThreads) {
+      int sequence = 0;
+      for (int i = 1; i < sequences; ++i) sequence += r >= boundaries[i];
+      positions[r] = r - boundaries[sequence];
+      row_slots[r] = sequence_slots[sequence];
+    }
+  }
+
   // 3. MoE rows and the read-back map
   int kept_total = 0;
   for (int start = 0; start < full; start += kMixedThreads) {
@@ -270,9 +283,10 @@ using namespace d3;
 extern "C" int d3_mixed_rows(const uint8_t* occupancy, int32_t num_slots, int32_t decode_rows,
                              int64_t padding_start, const int32_t* boundaries, int32_t prompts,
                              int32_t capacity, const int64_t* frames, int32_t codes,
+                             const int64_t* sequence_slots, int32_t sequences,
                              int32_t* active_slots, int32_t* count, int64_t* decode_slots,
                              int32_t* keep, int32_t* keep_count, int64_t* inverse,
-                             void* stream) {
+                             int64_t* positions, int64_t* row_slots, void* stream) {
   D3_REQUIRE(occupancy && boundaries && active_slots && count && keep && keep_count && inverse,
              "mixed_rows: null pointer");
   D3_REQUIRE(decode_rows == 0 || decode_slots, "mixed_rows: null decode_slots");
@@ -283,6 +297,9 @@ extern "C" int d3_mixed_rows(const uint8_t* occupancy, int32_t num_slots, int32_
   D3_REQUIRE(full >= 1 && full <= (1 << 30), "mixed_rows: %lld rows out of range",
              static_cast<long long>(full));
   D3_REQUIRE(frames == nullptr || codes >= 1, "mixed_rows: frames need codes >= 1");
+  D3_REQUIRE(positions == nullptr ||
+                 (row_slots && sequence_slots && sequences >= 1 && sequences >= prompts),
+             "mixed_rows: row metadata needs row_slots, sequence_slots and sequences >= prompts");
   if (frames != nullptr && prompts >= 2) {
     D3_SUPPORTED(prompts <= kMixedMaxPrompts, "mixed_rows: prefix reuse over %d prompts (max %d)",
                  prompts, kMixedMaxPrompts);
@@ -291,8 +308,8 @@ extern "C" int d3_mixed_rows(const uint8_t* occupancy, int32_t num_slots, int32_
   }
   hipLaunchKernelGGL(mixed_rows_kernel, dim3(1), dim3(kMixedThreads), 0, as_stream(stream),
                      occupancy, num_slots, decode_rows, padding_start, boundaries, prompts,
-                     capacity, frames, codes, active_slots, count, decode_slots, keep, keep_count,
-                     inverse);
+                     capacity, frames, codes, sequence_slots, sequences, active_slots, count,
+                     decode_slots, keep, keep_count, inverse, positions, row_slots);
   D3_LAUNCHED("mixed_rows");
 }
 

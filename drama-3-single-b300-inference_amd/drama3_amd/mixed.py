@@ -20,7 +20,6 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr
-from .packed_prefill import packed_row_metadata
 from .pipeline import MoEWorkspace, Shape, require_cuda
 
 MAX_REUSE_PROMPTS = 16
@@ -56,11 +55,26 @@ class MixedRows:
         self.inverse = torch.empty(self.full, **i64)
 
     def __call__(self, occupancy: torch.Tensor, boundaries: torch.Tensor, prompts: int,
-                 frames: torch.Tensor | None = None, stream=None) -> None:
+                 frames: torch.Tensor | None = None, stream=None,
+                 sequence_slots: torch.Tensor | None = None, positions: torch.Tensor | None = None,
+                 row_slots: torch.Tensor | None = None) -> None:
         """occupancy uint8 [slots]; boundaries int32 [>= prompts + 1] (prompt
         i = suffix rows [b[i], b[i+1]), rows from b[prompts] on are padding);
-        frames int64 [capacity, codes] of the suffix (prefix reuse) or None."""
-        require_cuda(occupancy, boundaries, frames)
+        frames int64 [capacity, codes] of the suffix (prefix reuse) or None.
+        With ``positions`` / ``row_slots`` (int64 [capacity]) the same launch
+        writes the suffix's row metadata (``row_metadata`` of
+        ``packed_prefill.py:51-78``) over all ``len(boundaries) - 1``
+        sequences, whose slots ``sequence_slots`` holds."""
+        require_cuda(occupancy, boundaries, frames, sequence_slots, positions, row_slots)
+        sequences = 0
+        if positions is not None:
+            sequences = boundaries.numel() - 1
+            if (row_slots is None or sequence_slots is None or sequence_slots.numel() < sequences
+                    or positions.dtype != torch.int64 or row_slots.dtype != torch.int64
+                    or sequence_slots.dtype != torch.int64
+                    or min(positions.numel(), row_slots.numel()) < self.capacity):
+                raise ValueError("row metadata needs int64 positions / row_slots [capacity] and "
+                                 "one int64 sequence slot per sequence")
         if occupancy.dtype != torch.uint8 or occupancy.numel() != self.slots:
             raise ValueError(f"occupancy must be uint8 [{self.slots}]")
         if boundaries.dtype != torch.int32 or not boundaries.is_contiguous() \
@@ -74,16 +88,17 @@ class MixedRows:
             codes = frames.shape[1]
         stream = _lib.stream(occupancy.device) if stream is None else stream
         call("d3_mixed_rows", ptr(occupancy), self.slots, self.decode_rows, self.padding_start,
-             ptr(boundaries), prompts, self.capacity, ptr(frames), codes, ptr(self.active),
-             ptr(self.count), ptr(self.decode_slots), ptr(self.keep), ptr(self.keep_count),
-             ptr(self.inverse), stream)
+             ptr(boundaries), prompts, self.capacity, ptr(frames), codes, ptr(sequence_slots),
+             sequences, ptr(self.active), ptr(self.count), ptr(self.decode_slots), ptr(self.keep),
+             ptr(self.keep_count), ptr(self.inverse), ptr(positions), ptr(row_slots), stream)
 
 
 class MixedStep:
     """The MoE side of one mixed step, graph-capturable with fixed buffers.
 
-    Per step (``forward``): the mixed rows, the prefill suffix's row metadata
-    (``row_metadata`` of ``mixed_graph.py:96-107``), the routed experts over
+    Per step (``forward``): the mixed rows and the prefill suffix's row
+    metadata (``row_metadata`` of ``mixed_graph.py:96-107``) in one launch,
+    the routed experts over
     the kept rows (``model.moe_parts(normalized.index_select(0, keep), ...)``,
     ``mixed_model.py:237-243``) and ``combine_experts_add_norm_inverse`` back
     onto every row (``mixed_model.py:198-201``), the routed rows' weighted
@@ -140,10 +155,8 @@ class MixedStep:
         stream = _lib.stream(self.device)
         r = self.rows
         r(self.occupancy, self.boundaries, self.sequences - 1,
-          self.frames if self.reuse else None, stream)
-        if r.capacity:
-            packed_row_metadata(self.boundaries, self.sequence_slots, r.capacity, self.positions,
-                                self.row_slots)
+          self.frames if self.reuse else None, stream, self.sequence_slots, self.positions,
+          self.row_slots)
         ws = self.workspace
         ws.front(self.x, self.logits, r.keep, r.keep_count, stream=stream)
         ws.routes_down(experts, r.keep_count, stream)

@@ -575,12 +575,17 @@ int d3_row_metadata(const int32_t *cu_seqlens, const int64_t *sequence_slots,
  * Padding rows never reach the MoE (the reference computes and discards
  * them).  More occupied slots than decode_rows: *count reports them all and
  * the first decode_rows become rows.
+ * With positions != NULL the same launch also writes d3_row_metadata's
+ * positions / row_slots int64 [capacity] of the suffix (boundaries then hold
+ * sequences + 1 entries, sequence_slots int64 [sequences], sequences >=
+ * prompts; NULL skips them).
  */
 int d3_mixed_rows(const uint8_t *occupancy, int32_t num_slots, int32_t decode_rows,
                   int64_t padding_start, const int32_t *boundaries, int32_t prompts,
-                  int32_t capacity, const int64_t *frames, int32_t codes, int32_t *active_slots,
+                  int32_t capacity, const int64_t *frames, int32_t codes,
+                  const int64_t *sequence_slots, int32_t sequences, int32_t *active_slots,
                   int32_t *count, int64_t *decode_slots, int32_t *keep, int32_t *keep_count,
-                  int64_t *inverse, void *stream);
+                  int64_t *inverse, int64_t *positions, int64_t *row_slots, void *stream);
 
 /*
  * A1  Per-slot request state gather / update.

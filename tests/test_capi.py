@@ -82,7 +82,7 @@ def test_capacity_helpers(lib):
     for pairs, experts, tile in ((32, 16, 16), (384, 128, 16), (33280, 128, 64), (0, 8, 16)):
         assert lib.d3_max_sorted_rows(pairs, experts, tile) == om.max_sorted_rows(pairs, experts, tile)
     assert lib.d3_max_items(384, 128, 64) == (384 + 128 * 63) // 64
-    assert lib.d3_abi_version() == 6
+    assert lib.d3_abi_version() == 7
     # wide sort scratch: chunk histograms [ceil(pairs / 512)][E] + ranks [pairs]
     assert lib.d3_sort_wide_scratch_ints(3668, 8, 128) == (-(-3668 * 8 // 512)) * 128 + 3668 * 8
     assert lib.d3_sort_wide_scratch_ints(-1, 8, 128) == -1
@@ -133,14 +133,17 @@ def test_contract_violations_raise_value_error(lib):
     assert "scratch of 10 ints" in lib.d3_last_error().decode()
     # mixed rows: null outputs, prefix reuse limits (prompts, row space)
     with pytest.raises(ValueError, match="null pointer"):
-        _lib.call("d3_mixed_rows", 16, 64, 48, 32, 16, 2, 512, None, 11, 16, 16, 16, None, 16, 16,
-                  None)
+        _lib.call("d3_mixed_rows", 16, 64, 48, 32, 16, 2, 512, None, 11, None, 0, 16, 16, 16, None,
+                  16, 16, None, None, None)
     with pytest.raises(ValueError, match="17 prompts"):
-        _lib.call("d3_mixed_rows", 16, 64, 48, 32, 16, 17, 512, 16, 11, 16, 16, 16, 16, 16, 16,
-                  None)
+        _lib.call("d3_mixed_rows", 16, 64, 48, 32, 16, 17, 512, 16, 11, None, 0, 16, 16, 16, 16,
+                  16, 16, None, None, None)
     with pytest.raises(ValueError, match="9048 rows"):
-        _lib.call("d3_mixed_rows", 16, 64, 48, 32, 16, 2, 9000, 16, 11, 16, 16, 16, 16, 16, 16,
-                  None)
+        _lib.call("d3_mixed_rows", 16, 64, 48, 32, 16, 2, 9000, 16, 11, None, 0, 16, 16, 16, 16,
+                  16, 16, None, None, None)
+    with pytest.raises(ValueError, match="row metadata needs"):
+        _lib.call("d3_mixed_rows", 16, 64, 48, 32, 16, 2, 512, None, 11, 16, 1, 16, 16, 16, 16,
+                  16, 16, 16, 16, None)
 
 
 def test_product_code_does_not_import_the_oracle():

@@ -52,13 +52,22 @@ def layout_inputs(rng, slots, live, lengths, capacity, share=0.8):
 
 def run_layout(device, occupancy, decode_rows, padding_start, boundaries, prompts, capacity,
                frames):
+    """The layout, and the suffix's row metadata from the same launch
+    (checked against the oracle's row_metadata here)."""
     from drama3_amd.mixed import MixedRows
 
     rows = MixedRows(len(occupancy), decode_rows, capacity, padding_start, device)
     f = None if frames is None else torch.from_numpy(frames).to(device)
+    sequences = len(boundaries) - 1
+    seq_slots = np.arange(sequences, dtype=np.int64) + 7
+    positions = torch.full((max(capacity, 1),), -5, dtype=torch.int64, device=device)
+    row_slots = torch.full_like(positions, -5)
     rows(torch.from_numpy(occupancy).to(device), torch.from_numpy(boundaries).to(device),
-         prompts, f)
+         prompts, f, None, torch.from_numpy(seq_slots).to(device), positions, row_slots)
     torch.cuda.synchronize()
+    want_pos, want_slots, _ = om.row_metadata(boundaries, seq_slots, capacity)
+    assert np.array_equal(positions.cpu().numpy()[:capacity], want_pos)
+    assert np.array_equal(row_slots.cpu().numpy()[:capacity], want_slots)
     return rows
 
 
@@ -142,7 +151,8 @@ def rng_torch(rng):
     return torch.Generator("cpu").manual_seed(int(rng.integers(0, 2 ** 31)))
 
 
-def test_mixed_step_graph_replays(device):
+@pytest.mark.parametrize("reuse", [True, False])
+def test_mixed_step_graph_replays(device, reuse):
     """Config-5 shape: 48 live decode slots of 64 (decode bucket 64, reserved
     padding from slot 32 on), two 256-row prompts with shared prefixes in a
     640-row suffix.  One capture; four replays with 4 slots retired and 4
@@ -161,7 +171,7 @@ def test_mixed_step_graph_replays(device):
     slots, d, capacity, padding_start = 64, 64, 640, 32
     sequence_slots = [40, 41, 63]
     step = MixedStep(slots, d, capacity, padding_start, 3, w.num_experts, w.hidden,
-                     w.intermediate, device=device)
+                     w.intermediate, device=device, reuse=reuse)
     rng = np.random.default_rng(11)
     norm = torch.randn(w.hidden, generator=rng_torch(rng)).to(torch.bfloat16)
     step.norm_weight.copy_(norm)
@@ -190,7 +200,7 @@ def test_mixed_step_graph_replays(device):
         assert torch.equal(residual.view(torch.int16), res2.view(torch.int16))
         # the layout
         expected = om.mixed_layout(occupancy, d, padding_start, host["boundaries"], 2, capacity,
-                                   host["frames"])
+                                   host["frames"] if reuse else None)
         assert_layout(step.rows, expected, d)
         positions, row_slots, _ = om.row_metadata(host["boundaries"], sequence_slots, capacity)
         assert np.array_equal(step.positions.cpu().numpy(), positions)
