@@ -101,6 +101,8 @@ constexpr int kMixedThreads = 1024;
 constexpr int kMixedWaves = kMixedThreads / kWave;
 constexpr int kMixedMaxRows = 8192;   // row space with prefix reuse (LDS owner table)
 constexpr int kMixedMaxPrompts = 16;  // prompts compared for prefix reuse
+constexpr int kMixedMaxBounds = 1025; // boundaries staged in LDS (1024 sequences)
+constexpr int kMixedMaxCodes = 16;    // frame codes compared from registers
 
 // Exclusive rank of `flag` among the workgroup's threads (thread order) and
 // the workgroup's total.  Two barriers; `wave_counts` is free again on return.
@@ -147,9 +149,15 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
   __shared__ int wave_counts[kMixedWaves];
   __shared__ int starts[kMixedMaxPrompts + 1];
   __shared__ int common[kMixedMaxPrompts * kMixedMaxPrompts];
+  __shared__ int bounds[kMixedMaxBounds];
   const int tid = static_cast<int>(threadIdx.x);
   const int full = decode_rows + capacity;
   const bool reuse = frames != nullptr && prompts >= 2;
+  // Every boundary read below goes to this LDS copy (one parallel load; a
+  // loop over global boundaries pays a memory round trip per entry).  The
+  // compaction's barriers order it before its first use.
+  const int nbounds = (prompts > sequences ? prompts : sequences) + 1;
+  for (int i = tid; i < nbounds; i += kMixedThreads) bounds[i] = boundaries[i];
 
   // 1. slot compaction and decode row slots
   int occupied = 0;
@@ -172,8 +180,9 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
   // 2. clamped boundaries and prefix ownership
   // b[prompts] after clamping: the largest clamped boundary.
   int live_prefill = 0;
+  __syncthreads();  // bounds written
   for (int i = 0; i <= prompts; ++i) {
-    const int b = boundaries[i];
+    const int b = bounds[i];
     const int clamped = b > capacity ? capacity : b;
     live_prefill = clamped > live_prefill ? clamped : live_prefill;
   }
@@ -181,7 +190,7 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
     if (tid == 0) {
       int previous = 0;
       for (int i = 0; i <= prompts; ++i) {
-        int b = boundaries[i];
+        int b = bounds[i];
         b = b < previous ? previous : (b > capacity ? capacity : b);
         starts[i] = b;
         previous = b;
@@ -211,7 +220,22 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
         const int64_t* a = frames + static_cast<int64_t>(starts[i] + p) * codes;
         const int64_t* b = frames + static_cast<int64_t>(starts[j] + p) * codes;
         bool differ = false;
-        for (int c = 0; c < codes; ++c) differ |= a[c] != b[c];
+        if (codes <= kMixedMaxCodes) {
+          // Issue every load of both rows before the first compare (a loop
+          // that compares as it loads waits a round trip per code).
+          int64_t va[kMixedMaxCodes], vb[kMixedMaxCodes];
+#pragma unroll
+          for (int c = 0; c < kMixedMaxCodes; ++c)
+            if (c < codes) {
+              va[c] = a[c];
+              vb[c] = b[c];
+            }
+#pragma unroll
+          for (int c = 0; c < kMixedMaxCodes; ++c)
+            if (c < codes) differ |= va[c] != vb[c];
+        } else {
+          for (int c = 0; c < codes; ++c) differ |= a[c] != b[c];
+        }
         if (differ) atomicMin(&common[i * kMixedMaxPrompts + j], p);
       }
     }
@@ -236,8 +260,8 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
   if (positions != nullptr) {
     for (int r = tid; r < capacity; r += kMixedThreads) {
       int sequence = 0;
-      for (int i = 1; i < sequences; ++i) sequence += r >= boundaries[i];
-      positions[r] = r - boundaries[sequence];
+      for (int i = 1; i < sequences; ++i) sequence += r >= bounds[i];
+      positions[r] = r - bounds[sequence];
       row_slots[r] = sequence_slots[sequence];
     }
   }
@@ -300,6 +324,10 @@ extern "C" int d3_mixed_rows(const uint8_t* occupancy, int32_t num_slots, int32_
   D3_REQUIRE(positions == nullptr ||
                  (row_slots && sequence_slots && sequences >= 1 && sequences >= prompts),
              "mixed_rows: row metadata needs row_slots, sequence_slots and sequences >= prompts");
+  if (positions == nullptr) sequences = 0;
+  D3_SUPPORTED(prompts < kMixedMaxBounds && sequences < kMixedMaxBounds,
+               "mixed_rows: %d prompts / %d sequences (max %d)", prompts, sequences,
+               kMixedMaxBounds - 1);
   if (frames != nullptr && prompts >= 2) {
     D3_SUPPORTED(prompts <= kMixedMaxPrompts, "mixed_rows: prefix reuse over %d prompts (max %d)",
                  prompts, kMixedMaxPrompts);
