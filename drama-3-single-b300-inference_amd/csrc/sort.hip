@@ -48,6 +48,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_routes_kernel(
 constexpr int kWideThreads = 256;
 constexpr int kWideChunk = 512;
 constexpr int kWideScanLds = 12288;  // chunk histogram cells staged in LDS (48 KiB)
+static_assert(kWideScanLds % kSortThreads == 0, "whole staging rounds per thread");
 
 template <bool kI64>
 __global__ __launch_bounds__(kWideThreads) void wide_rank_kernel(
@@ -119,8 +120,21 @@ __global__ __launch_bounds__(kSortThreads) void wide_scan_kernel(
   const int tid = threadIdx.x;
   const int cells = chunks * num_experts;
   const bool in_lds = cells <= kWideScanLds;
-  if (in_lds) {  // one coalesced pass instead of a chain of dependent loads
-    for (int i = tid; i < cells; i += kSortThreads) staged[i] = chunk_counts[i];
+  if (in_lds) {
+    // Every load issued before the first LDS store: one memory round trip
+    // (a loop that stores as it loads waits for each load in turn).
+    constexpr int kPerThread = kWideScanLds / kSortThreads;
+    int v[kPerThread];
+#pragma unroll
+    for (int b = 0; b < kPerThread; ++b) {
+      const int i = b * kSortThreads + tid;
+      v[b] = i < cells ? chunk_counts[i] : 0;
+    }
+#pragma unroll
+    for (int b = 0; b < kPerThread; ++b) {
+      const int i = b * kSortThreads + tid;
+      if (i < cells) staged[i] = v[b];
+    }
     __syncthreads();
   }
   // Per expert: exclusive scan of its chunk counts (offsets written back in
