@@ -70,6 +70,12 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
   return total;
 }
 
+// out = bf16(shared * bf16(sigmoid(gate)) + routed), rounded once: the
+// reference's combine_experts (kernels.py:427-445) is written as two bf16
+// roundings, but its compiled form contracts the multiply-add into one bf16
+// FMA, the result the reference then keeps in its fused residual variant
+// (kernels.py:465-474); with the same FMA here, this kernel followed by
+// add_norm gives combine_experts_add_norm's bytes.
 __global__ __launch_bounds__(kThreads) void combine_experts_kernel(
     const uint16_t* __restrict__ routed, const uint16_t* __restrict__ shared,
     const uint16_t* __restrict__ gate, int64_t gate_stride, int width,
@@ -82,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void combine_experts_kernel(
     load4(routed + base + column, r);
     load4(shared + base + column, s);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = r[i] + round_bf16(s[i] * g);
+    for (int i = 0; i < 4; ++i) v[i] = fma_bf16(s[i], g, r[i]);
     store4(out + base + column, v);
   }
 }

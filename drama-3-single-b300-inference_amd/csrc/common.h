@@ -87,8 +87,8 @@ __device__ __forceinline__ uint32_t quantize_one(float x, float scale) {
 // quantize_one of four values, packed little-endian (v[0] in the low byte).
 // The conversion is v_cvt_pk_fp8_f32 (round to nearest even into OCP e4m3),
 // which gives f32_to_e4m3's byte for every input in [-448, 448] in every
-// byte position: checked on gfx950 over all 2^32 fp32 bit patterns after
-// the clamp.
+// byte position: d3_check_e4m3_conversion (selftest.hip) compares the two
+// over all 2^32 fp32 bit patterns after the clamp.
 __device__ __forceinline__ uint32_t quantize_four(const float* v, float scale) {
   float c[4];
 #pragma unroll
@@ -134,6 +134,10 @@ struct SumF32 {
 struct MaxU32 {
   static constexpr uint32_t kIdentity = 0u;
   __device__ static uint32_t apply(uint32_t a, uint32_t b) { return a > b ? a : b; }
+};
+struct SumU32 {
+  static constexpr uint32_t kIdentity = 0u;
+  __device__ static uint32_t apply(uint32_t a, uint32_t b) { return a + b; }
 };
 
 // Every lane of each 16-lane row gets the reduction over its row.

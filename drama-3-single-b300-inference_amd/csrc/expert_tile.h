@@ -110,35 +110,22 @@ __device__ __forceinline__ floatx4 mfma_block_bf16(int32x8 a, const bf16x8 b[4])
 }
 
 // SwiGLU of one bf16-rounded gate / up pair in fp32: a = (g * sigmoid(g)) * u
-// with sigmoid(g) = 1 / (1 + exp(-g)) on the hardware exponential and
-// reciprocal (v_exp_f32, v_rcp_f32: about one ulp each).  The reference runs
-// this step in Fish's Triton silu_mul_quant kernel, whose sigmoid and
-// division are likewise the approximate hardware forms; every kernel of this
-// build that requantises FC1 outputs uses this one function, so they agree
-// bit for bit.
+// with sigmoid(g) = 1 / (1 + exp(-g)) in IEEE fp32 (the library expf, within
+// one ulp, and a correctly rounded division), the arithmetic of the
+// reference's in-repo SwiGLU (kernels.py:392-394) without its bf16 rounding
+// of silu(g).  Every kernel of this build that requantises FC1 outputs uses
+// this one function, so they agree bit for bit.
 __device__ __forceinline__ float swiglu_value(float g, float u) {
-  const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+  const float sig = 1.0f / (1.0f + expf(-g));
   return (g * sig) * u;
-}
-
-// e4m3 codes of clamp(v * inv_scale, -448, 448) for four values (v[0] in the
-// low byte): the SwiGLU requantisation multiplies by the reciprocal of its
-// group scale (one reciprocal per group; the activation quantiser of the
-// MoE input, moe_input.py:24-27, keeps the IEEE division of quantize_four).
-__device__ __forceinline__ uint32_t requantize_four(const float* v, float inv_scale) {
-  float c[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) c[i] = fminf(fmaxf(v[i] * inv_scale, -448.0f), 448.0f);
-  int word = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
-  word = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], word, true);
-  return static_cast<uint32_t>(word);
 }
 
 // SwiGLU + e4m3 requantisation of one 128-column group held by 16 lanes
 // (8 gate and 8 up bf16 values per lane): a = swiglu_value(g, u), scale =
-// max(amax, 1e-10) / 448, codes requantize_four(a, 1 / scale).  Shared by the
-// standalone kernel, the FC2 prologues and the fused FC1 epilogue, so all
-// give the same bytes.
+// max(amax, 1e-10) / 448, codes quantize_four(a, scale) (IEEE division by
+// the scale, the rule of moe_input.py:24-27).  Shared by the standalone
+// kernel, the FC2 prologues and the fused FC1 epilogue, so all give the
+// same bytes.
 __device__ __forceinline__ float swiglu_quant_group(uint4 graw, uint4 uraw, uint2* codes) {
   const uint32_t gw[4] = {graw.x, graw.y, graw.z, graw.w};
   const uint32_t uw[4] = {uraw.x, uraw.y, uraw.z, uraw.w};
@@ -153,9 +140,8 @@ __device__ __forceinline__ float swiglu_quant_group(uint4 graw, uint4 uraw, uint
   }
   amax = segment_max<16>(amax);
   const float scale = group_scale(amax);
-  const float inv = __builtin_amdgcn_rcpf(scale);
-  const uint32_t lo = requantize_four(v, inv);
-  const uint32_t hi = requantize_four(v + 4, inv);
+  const uint32_t lo = quantize_four(v, scale);
+  const uint32_t hi = quantize_four(v + 4, scale);
   *codes = make_uint2(lo, hi);
   return scale;
 }

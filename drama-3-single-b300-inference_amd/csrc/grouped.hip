@@ -308,10 +308,9 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
       for (int q = 1; q < kGgWaves; ++q) amax = fmaxf(amax, amax_part[q][route]);
       const float scale = group_scale(amax);
-      const float inv = __builtin_amdgcn_rcpf(scale);
       uint8_t* dst = out_codes + static_cast<size_t>(position) * out_cols + n0 + 32 * wave + 4 * group;
-      *reinterpret_cast<uint32_t*>(dst) = requantize_four(&v[rt][0], inv);
-      *reinterpret_cast<uint32_t*>(dst + 16) = requantize_four(&v[rt][4], inv);
+      *reinterpret_cast<uint32_t*>(dst) = quantize_four(&v[rt][0], scale);
+      *reinterpret_cast<uint32_t*>(dst + 16) = quantize_four(&v[rt][4], scale);
       if (wave == 0 && group == 0) out_scales[static_cast<size_t>(position) * groups + tile] = scale;
     }
   }

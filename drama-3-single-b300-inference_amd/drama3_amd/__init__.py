@@ -2,11 +2,13 @@
 david6666666/drama-3-single-b300-inference (``src/drama3``).
 
 Modules mirror the reference's: ``kernels`` (route, small_batch_moe,
-native_moe, combine_experts*, add_norm, silu_mul), ``moe_input``
-(prepare_moe_input), ``moe_atomic`` (atomic_down), ``packed_prefill``
-(PackedLayout, row_metadata), ``runtime_state`` (DeviceRequests).  The decode
-step over persistent slots is ``pipeline.DecodeStep``.  All compute runs in
-the HIP library ``_lib/libdrama3_moe.so``; there is no CPU fallback.
+native_moe, routed_moe, combine_experts*, add_norm, silu_mul), ``moe_input``
+(prepare_moe_input, quantize_groups), ``moe_atomic`` (atomic_down),
+``packed_prefill`` (PackedLayout, row_metadata), ``runtime_state``
+(DeviceRequests).  The decode step over persistent slots is
+``pipeline.DecodeStep``, the mixed decode + prefill step ``mixed.MixedStep``
+and one whole MoE layer ``moe_layer.MoELayer``.  All compute runs in the HIP
+library ``_lib/libdrama3_moe.so``; there is no CPU fallback.
 """
 
 from pathlib import Path

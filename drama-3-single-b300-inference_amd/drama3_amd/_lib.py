@@ -37,6 +37,7 @@ _f32 = ctypes.c_float
 SIGNATURES = {
     "d3_abi_version": (_i32, []),
     "d3_last_error": (ctypes.c_char_p, []),
+    "d3_check_e4m3_conversion": (_i32, [ctypes.c_uint64, ctypes.c_uint64, _p, _p]),
     "d3_compact_slots": (_i32, [_p, _i32, _p, _p, _p]),
     "d3_route": (_i32, [_p, _i32, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _i32, _p]),
     "d3_quantize_rows": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p, _p, _i32, _p]),
@@ -52,6 +53,8 @@ SIGNATURES = {
         _i32, [_p, _i32, _i32, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _i32, _p, _i32, _p,
                _i32, _p, _p, _p, _i64, _p]),
     "d3_sort_wide_scratch_ints": (_i64, [_i32, _i32, _i32]),
+    "d3_items_from_tiles": (_i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _p, _p, _p]),
+    "d3_gather_rows": (_i32, [_p, _i64, _i64, _p, _p, _i32, _p, _p]),
     "d3_max_sorted_rows": (_i32, [_i32, _i32, _i32]),
     "d3_max_items": (_i32, [_i32, _i32, _i32]),
     "d3_expert_gemm": (

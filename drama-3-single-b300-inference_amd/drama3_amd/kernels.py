@@ -104,8 +104,10 @@ def small_batch_moe(x, topk_ids, topk_weights, experts, up_rows=4, down_rows=4, 
 def native_moe(x, topk_ids, topk_weights, experts, block_m=16, group_m=1, atomic=False):
     """``native_moe`` (``kernels.py:702-779``): device-only routing layout
     (histogram, padded offsets, stable scatter) then the grouped FP8 GEMMs.
-    ``atomic`` selected the reference's fp32-atomic down projection; here the
-    reduction is always the deterministic rank-ordered one."""
+    ``atomic`` selected the reference's fp32-atomic down projection
+    (``moe_atomic.atomic_down``, also provided with its signature); here the
+    reduction is always the deterministic rank-ordered one, which
+    ``atomic_down`` computes as well."""
     if not isinstance(group_m, int) or group_m < 1:
         raise ValueError("group_m must be a positive integer")
     return _routed(x, topk_ids, topk_weights, experts, block_m)
@@ -172,12 +174,16 @@ def _gate_args(gate: torch.Tensor, rows: int):
 
 
 def combine_experts(routed, shared, gate):
-    """``combine_experts`` (``kernels.py:427-445``):
-    ``routed + bf16(shared * bf16(sigmoid(gate)))``."""
+    """``combine_experts`` (``kernels.py:427-445``) as the reference runs it:
+    ``bf16(shared * bf16(sigmoid(gate)) + routed)`` in one single-rounding
+    bf16 FMA (the contraction ``kernels.py:465-466`` describes), so
+    ``add_norm(combine_experts(...))`` equals ``combine_experts_add_norm``.
+    ``routed`` and ``shared`` are read as contiguous rows."""
     _check_rows(routed, "routed")
     _check_rows(shared, "shared")
     if routed.shape != shared.shape:
         raise ValueError("routed and shared must have the same shape")
+    routed, shared = routed.contiguous(), shared.contiguous()
     stride = _gate_args(gate, len(routed))
     out = torch.empty_like(routed)
     call("d3_combine_experts", ptr(routed), ptr(shared), ptr(gate), stride, routed.shape[0],
@@ -265,14 +271,12 @@ def routed_moe(x, router, experts, decode=True, *, row_slots=None, padding_start
         return out
     logits = router
     if row_slots is not None:
-        if (row_slots.shape != (rows,) or row_slots.device != x.device
-                or row_slots.dtype not in (torch.int32, torch.int64)):
-            raise ValueError("Expected one integer slot per MoE row on the same device")
-        if not isinstance(padding_start, int) or padding_start <= 0:
-            raise ValueError("padding_start must be a positive reserved-slot boundary")
-        source = torch.arange(rows, device=x.device)
-        source = torch.where(row_slots >= padding_start, torch.zeros_like(source), source)
-        logits = router.index_select(0, source)
+        # The reference's decode path (model.py:543-552): prepare_moe_input
+        # applies the padding rule to the fp32 logits in its fused launch.
+        from .moe_input import prepare_moe_input
+
+        _, _, logits = prepare_moe_input(x, router, row_slots=row_slots,
+                                         padding_start=padding_start)
     if x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
     ws = MoEWorkspace(Shape(rows, e, h, i, TOP_K), x.device,

@@ -47,6 +47,19 @@ extern "C" {
 #define D3_LAYOUT_REFERENCE 0 /* w [E, N, K] row-major, as the checkpoint stores it */
 #define D3_LAYOUT_FRAGMENT 1  /* fragment-major, produced by d3_pack_expert_weights */
 
+/*
+ * Self-check of the e4m3 conversion (no counterpart in the reference).
+ * Every quantiser of this library converts clamped fp32 values with the
+ * gfx950 instruction v_cvt_pk_fp8_f32; the reference's bytes are the
+ * round-to-nearest-even e4m3fn cast (src/drama3/moe_input.py:24-27).  For
+ * the fp32 bit patterns [first, first + count) (multiples of 4, inside
+ * 2^32), each clamped to [-448, 448], the instruction's byte is compared with
+ * the software conversion in every byte position of the packed word;
+ * result[0] += mismatches, result[1] = min(result[1], first bad pattern).
+ * The caller initialises result to {0, 0xffffffff}.
+ */
+int d3_check_e4m3_conversion(uint64_t first, uint64_t count, uint32_t *result, void *stream);
+
 /* Version of this ABI (bumped on any signature change). */
 int d3_abi_version(void);
 
@@ -180,6 +193,34 @@ int d3_sort_routes_wide(const void *ids, int32_t ids_dtype, int32_t rows, const 
 int64_t d3_sort_wide_scratch_ints(int32_t rows, int32_t top_k, int32_t num_experts);
 
 /* Capacity helpers for d3_sort_routes (host-side arithmetic only). */
+/*
+ * A7  A caller's sorted-tile layout as work items.
+ * For native_moe's layout (src/drama3/kernels.py:666-699, sized at 710-731)
+ * as moe_atomic.atomic_down receives it (src/drama3/moe_atomic.py:60-78):
+ * sorted_ids int32 [max_tiles * tile] (pair ids, sentinel `pairs` in the
+ * padding), expert_ids int32 [max_tiles] (expert of each tile), *total (a
+ * multiple of tile).  Writes items int32 [max_tiles][4] = {expert_ids[t],
+ * t * tile, routes of tile t below the sentinel, 0} for t < *total / tile
+ * (an expert id outside [0, num_experts) gives an item of 0 routes) and
+ * *num_items = *total / tile (clamped to [0, max_tiles]).  items 16-byte
+ * aligned.
+ */
+int d3_items_from_tiles(const int32_t *sorted_ids, const int32_t *expert_ids,
+                        const int32_t *total, int32_t tile, int32_t pairs, int32_t max_tiles,
+                        int32_t num_experts, int32_t *items, int32_t *num_items, void *stream);
+
+/*
+ * A8  Row gather (permute) by an index list.
+ * The gather of activation rows stored by pair into sorted order that the
+ * reference's atomic down projection does inside its GEMM
+ * (src/drama3/moe_atomic.py:38-42: X + pairs * I).  dst row r (r < *row_count,
+ * or all rows when row_count is NULL) = src row index[r] when 0 <= index[r]
+ * < src_rows, else zeros; rows at or beyond the count are left untouched.
+ * row_bytes a multiple of 4; src / dst 4-byte aligned.
+ */
+int d3_gather_rows(const void *src, int64_t row_bytes, int64_t src_rows, const int32_t *index,
+                   const int32_t *row_count, int32_t rows, void *dst, void *stream);
+
 int32_t d3_max_sorted_rows(int32_t pairs, int32_t num_experts, int32_t tile);
 int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);
 
@@ -477,8 +518,10 @@ int d3_weighted_combine(const float *down, const void *weights, int32_t weights_
 
 /*
  * A12  Routed + gated shared expert combine.
- * Replaces combine_experts (src/drama3/kernels.py:427-445):
- * out = bf16(routed + bf16(shared * bf16(sigmoid(gate[r * gate_stride])))).
+ * Replaces combine_experts (src/drama3/kernels.py:427-445) as compiled: one
+ * single-rounding bf16 FMA (kernels.py:465-474),
+ * out = bf16(shared * bf16(sigmoid(gate[r * gate_stride])) + routed), so this
+ * followed by d3_add_norm equals d3_combine_experts_add_norm byte for byte.
  */
 int d3_combine_experts(const uint16_t *routed, const uint16_t *shared, const uint16_t *gate,
                        int64_t gate_stride, int32_t rows, int32_t width, uint16_t *out,

@@ -238,31 +238,38 @@ def silu_mul(projected_bf16: np.ndarray) -> np.ndarray:
     return f32_to_bf16((activated * up).astype(np.float32))
 
 
-def swiglu_f32(gate_up_bf16: np.ndarray) -> np.ndarray:
+def swiglu_f32(gate_up_bf16: np.ndarray, silu_bf16: bool = False) -> np.ndarray:
     """fp32 SwiGLU of bf16 [gate | up] rows: ``silu(g) * u`` with
-    ``silu(g) = g * sigmoid(g)``, no intermediate rounding beyond fp32.
+    ``silu(g) = g * sigmoid(g)``; sigmoid rounded once to fp32, then two fp32
+    products.
 
-    Parity unpinned: the reference applies Fish Speech's
-    ``silu_mul_quant_kernel`` (fish-speech @ 541566932abb, ``fp8_moe.py``, not
-    vendored; called at ``kernels.py:344,748``).  Whether it rounds
-    ``silu(gate)`` to bf16 before the multiply is not visible from the
-    reference; the build keeps fp32, the form of the in-repo ``silu_mul``
-    arithmetic (``kernels.py:392-394``) without its bf16 output rounding.
+    The reference applies Fish Speech's ``silu_mul_quant_kernel``
+    (fish-speech @ 541566932abb, ``fp8_moe.py``, not vendored; called at
+    ``kernels.py:344,748``), whose source is absent.  The build keeps fp32
+    throughout, the arithmetic of the in-repo ``silu_mul``
+    (``kernels.py:392-394``) without its bf16 roundings; ``silu_bf16=True``
+    gives that kernel's other reading, ``silu(g)`` rounded to bf16 before the
+    multiply, so its effect on the MoE output can be bounded.  Pinned against
+    ``torch.nn.functional.silu`` (float32 and float64) and the mathematics'
+    special values in ``tests/test_oracle_swiglu.py``.
     """
     width = gate_up_bf16.shape[-1] // 2
     gate = bf16_to_f32(gate_up_bf16[:, :width])
     up = bf16_to_f32(gate_up_bf16[:, width:])
     sig = (1.0 / (1.0 + np.exp(-gate.astype(np.float64)))).astype(np.float32)
-    return ((gate * sig).astype(np.float32) * up).astype(np.float32)
+    silu = (gate * sig).astype(np.float32)
+    if silu_bf16:
+        silu = round_bf16(silu)
+    return (silu * up).astype(np.float32)
 
 
-def silu_mul_quant(gate_up_bf16: np.ndarray, group: int = GROUP):
+def silu_mul_quant(gate_up_bf16: np.ndarray, group: int = GROUP, silu_bf16: bool = False):
     """SwiGLU + per-128 e4m3 requantisation of the FC1 output (A10).
 
-    Quantisation rule identical to ``quantize_rows``.  Parity unpinned for the
-    SwiGLU rounding, see ``swiglu_f32``.
+    Quantisation rule identical to ``quantize_rows``; the SwiGLU is
+    ``swiglu_f32`` (``silu_bf16`` selects its bf16-rounded reading).
     """
-    return quantize_rows(swiglu_f32(gate_up_bf16), group)
+    return quantize_rows(swiglu_f32(gate_up_bf16, silu_bf16), group)
 
 
 @dataclass
@@ -335,17 +342,19 @@ def weighted_combine(down: np.ndarray, topk_weights_f32: np.ndarray) -> np.ndarr
     return f32_to_bf16(total.astype(np.float32))
 
 
-def expert_ffn(x_bf16, ids, topk_weights_bf16, weights_: ExpertWeights, trace: bool = False):
+def expert_ffn(x_bf16, ids, topk_weights_bf16, weights_: ExpertWeights, trace: bool = False,
+               silu_bf16: bool = False):
     """Routed expert FFN of ``small_batch_moe`` / ``native_moe``.
 
     ``kernels.py:325-357`` and ``:702-779``: quantise x per 128 group, FC1
     (fp32 accumulate, bf16 out), SwiGLU + FP8 requant, FC2 (fp32), routing
-    weighted sum over the K ranks in fp32, bf16 out.
+    weighted sum over the K ranks in fp32, bf16 out.  ``silu_bf16``: see
+    ``swiglu_f32``.
     """
     x = bf16_to_f32(x_bf16)
     q, scales = quantize_rows(x)
     gate_up = expert_fc1(q, scales, ids, weights_)
-    act_q, act_scales = silu_mul_quant(gate_up)
+    act_q, act_scales = silu_mul_quant(gate_up, silu_bf16=silu_bf16)
     down = expert_fc2(act_q, act_scales, ids, weights_)
     out = weighted_combine(down, bf16_to_f32(topk_weights_bf16))
     if trace:
@@ -383,13 +392,17 @@ def sigmoid_bf16(gate_f32: np.ndarray) -> np.ndarray:
 
 def combine_experts(routed_bf16, shared_bf16, gate_bf16):
     """``combine_experts`` (``kernels.py:427-445``):
-    ``out = bf16(routed + bf16(shared * bf16(sigmoid(gate))))``.
+    ``out = fma_bf16(shared, bf16(sigmoid(gate)), routed)``, one rounding.
+
+    The kernel source reads ``routed + bf16(shared * gate)``, but the
+    reference states that its compiled form contracts the multiply-add into
+    one single-rounding bf16 FMA and keeps that result in the fused residual
+    variant (``kernels.py:465-474``), so the single rounding is the contract.
     gate: bf16 [T] (one gate column per row)."""
-    routed = bf16_to_f32(routed_bf16)
-    shared = bf16_to_f32(shared_bf16)
-    gate = sigmoid_bf16(bf16_to_f32(gate_bf16))[:, None]
-    weighted = round_bf16((shared * gate).astype(np.float32))
-    return f32_to_bf16((routed + weighted).astype(np.float32))
+    routed = bf16_to_f32(routed_bf16).astype(np.float64)
+    shared = bf16_to_f32(shared_bf16).astype(np.float64)
+    gate = sigmoid_bf16(bf16_to_f32(gate_bf16)).astype(np.float64)[:, None]
+    return f64_to_bf16(shared * gate + routed)
 
 
 def _rms_norm(value: np.ndarray, weight_bf16, eps: float) -> np.ndarray:

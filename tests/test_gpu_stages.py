@@ -375,6 +375,25 @@ def test_combine_routes_add_norm_equals_two_launches(device, top_k, wdtype, with
 
 
 # --------------------------------------------------------------------------- A12
+def test_combine_then_add_norm_equals_combine_add_norm(device):
+    """d3_combine_experts followed by d3_add_norm gives the bytes of
+    d3_combine_experts_add_norm (both combine with one bf16 FMA)."""
+    from drama3_amd.kernels import add_norm, combine_experts, combine_experts_add_norm
+
+    rng = np.random.default_rng(12)
+    rows, width = 16, 2048
+    routed, shared = bf16_tensor(rng, (rows, width), device), bf16_tensor(rng, (rows, width), device)
+    gate = bf16_tensor(rng, (rows, 1), device)
+    weight = bf16_tensor(rng, (width,), device, 0.1)
+    res_a = bf16_tensor(rng, (rows, width), device)
+    res_b = res_a.clone()
+    out_a = add_norm(combine_experts(routed, shared, gate), res_a, weight, 1e-6)
+    out_b = combine_experts_add_norm(routed, shared, gate, res_b, weight, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(res_a.view(torch.int16), res_b.view(torch.int16))
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16))
+
+
 def test_combine_kernels(device):
     from drama3_amd.kernels import (add_norm, combine_experts, combine_experts_add_norm,
                                     combine_experts_add_norm_inverse, silu_mul)
@@ -386,8 +405,7 @@ def test_combine_kernels(device):
     gate = gate_storage[:, 1:2]
     out = combine_experts(routed, shared, gate)
     want = om.combine_experts(np_bf16(routed), np_bf16(shared), np_bf16(gate)[:, 0])
-    assert_bf16_close(np_bf16(out), want, ulps=1, row_floor=0.0)
-    assert np.mean(np_bf16(out) == want) > 0.999
+    assert np.array_equal(np_bf16(out), want)  # one bf16 FMA, single rounding
 
     residual = bf16_tensor(rng, (rows, width), device)
     weight = bf16_tensor(rng, (width,), device, 0.1)

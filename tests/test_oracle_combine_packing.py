@@ -18,14 +18,44 @@ def tb(bits):
     return torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16)
 
 
-def test_combine_experts_matches_torch_bf16_ops():
+def bf16_neighbours(bits):
+    """The bf16 values one ulp below and above each (finite, nonzero) value."""
+    f = bf16_to_f32(bits).astype(np.float64)
+    up = bf16_to_f32(np.where(f >= 0, bits + 1, bits - 1).astype(np.uint16)).astype(np.float64)
+    down = bf16_to_f32(np.where(f > 0, bits - 1, bits + 1).astype(np.uint16)).astype(np.float64)
+    return down, up
+
+
+def test_combine_experts_is_the_nearest_bf16_of_the_exact_fma():
+    """combine_experts (kernels.py:427-445 as compiled: one bf16 FMA,
+    kernels.py:465-474) is the bf16 value nearest to shared * bf16(sigmoid(g))
+    + routed, ties to even; the two-rounding reading of the source differs
+    from it on some elements, so this test tells the two apart."""
     rng = np.random.default_rng(0)
-    routed, shared, gate = bf16(rng, (8, 256)), bf16(rng, (8, 256)), bf16(rng, (8,))
+    routed, shared, gate = bf16(rng, (64, 256)), bf16(rng, (64, 256)), bf16(rng, (64,))
     got = om.combine_experts(routed, shared, gate)
-    g = torch.sigmoid(tb(gate).float()).to(torch.bfloat16).float()[:, None]
-    weighted = (tb(shared).float() * g).to(torch.bfloat16).float()
-    want = (tb(routed).float() + weighted).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
-    assert np.array_equal(got, want)
+    g = torch.sigmoid(tb(gate).float()).to(torch.bfloat16).double()[:, None]
+    exact = (tb(shared).double() * g + tb(routed).double()).numpy()  # exact in float64
+    value = bf16_to_f32(got).astype(np.float64)
+    down, up = bf16_neighbours(got)
+    dist = np.abs(value - exact)
+    assert np.all(dist <= np.abs(down - exact)) and np.all(dist <= np.abs(up - exact))
+    tie = (dist == np.abs(down - exact)) | (dist == np.abs(up - exact))
+    assert np.all((got[tie] & 1) == 0)
+    weighted = (tb(shared).float() * g.float()).to(torch.bfloat16).float()
+    twice = (tb(routed).float() + weighted).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    # (about a fifth of the elements differ by one ulp on N(0,1) data)
+    assert np.mean(got == twice) > 0.5 and np.mean(got != twice) > 0.05
+
+
+def test_combine_then_add_norm_equals_fused_combine_add_norm():
+    rng = np.random.default_rng(5)
+    routed, shared, gate = bf16(rng, (6, 512)), bf16(rng, (6, 512)), bf16(rng, (6,))
+    residual, weight = bf16(rng, (6, 512)), bf16(rng, (512,), 0.1)
+    combined = om.combine_experts(routed, shared, gate)
+    out_a, res_a = om.add_norm(combined, residual, weight, 1e-6)
+    out_b, res_b = om.combine_experts_add_norm(routed, shared, gate, residual, weight, 1e-6)
+    assert np.array_equal(res_a, res_b) and np.array_equal(out_a, out_b)
 
 
 def test_silu_mul_matches_torch():
