@@ -33,7 +33,8 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 # this script (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors read off
 # the 1 GiB device copy in the same runs); profiles/expert_gemm_c2_hbm_traffic.md.
 # Re-measure whenever the FC1 kernel or its tiling changes.
-FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,1,6,1>", "bytes": 401299456}
+FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,1,6,1>", "bytes": 401299456,
+                     "measured_on": "383c000 (profiles/expert_gemm_c2_hbm_traffic.md)"}
 
 
 def parse():
@@ -46,8 +47,14 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--fused", action="store_true",
                    help="time the one-launch step (d3_moe_decode_step) instead of the kernel chain")
-    p.add_argument("--cpu-sample-steps", type=int, default=3,
-                   help="oracle steps timed for cpu_baseline (about 5 s each on 8 cores)")
+    p.add_argument("--cpu-runs", type=int, default=10,
+                   help="timed runs per configuration of the CPU baseline (after 2 warm-ups)")
+    p.add_argument("--replays", type=int, default=100,
+                   help="individually timed graph replays for the per-replay statistics")
+    p.add_argument("--no-parity", action="store_true",
+                   help="skip the config-2 output check against the numpy oracle")
+    p.add_argument("--no-decode-configs", action="store_true",
+                   help="skip the config-1 and config-3 decode lines")
     p.add_argument("--no-prefill", action="store_true",
                    help="skip the config-4 packed-prefill measurement")
     p.add_argument("--prefill-only", action="store_true",
@@ -69,6 +76,7 @@ def baseline_metric():
 
 
 def time_graphs(torch, graphs, count):
+    """Mean time per replay (us) of `count` back-to-back replays."""
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
@@ -79,34 +87,156 @@ def time_graphs(torch, graphs, count):
     return start.elapsed_time(end) * 1000.0 / count  # us
 
 
-def cpu_baseline(workload, step, samples):
-    """The CPU oracle (numpy restatement of the reference step) on this host."""
+def replay_stats(torch, graph, replays, per_replay=1, warmup=10):
+    """Per-replay timing: `warmup` untimed replays, then `replays` replays,
+    each bracketed by its own events on the replay stream.  Returns the
+    median and mean per step (us; a replay holds `per_replay` steps) and the
+    mean of the whole back-to-back run."""
+    import statistics
+
+    for _ in range(warmup):
+        graph.replay()
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(replays)]
+    first, last = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    first.record()
+    for start, end in pairs:
+        start.record()
+        graph.replay()
+        end.record()
+    last.record()
+    torch.cuda.synchronize()
+    each = [s.elapsed_time(e) * 1000.0 / per_replay for s, e in pairs]
+    return {"median_us": statistics.median(each), "mean_us": statistics.fmean(each),
+            "min_us": min(each), "max_us": max(each),
+            "run_mean_us": first.elapsed_time(last) * 1000.0 / (replays * per_replay),
+            "replays": replays, "steps_per_replay": per_replay, "warmup_replays": warmup}
+
+
+def host_cpu():
+    """CPU model, usable cores and torch's intra-op thread setting of this host."""
+    import torch
+
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    info = [line.strip() for line in torch.__config__.parallel_info().splitlines()
+            if line.strip().startswith(("ATen", "at::get_num_threads", "OpenMP", "MKL", "Intra-op"))]
+    return {"cpu_model": model, "cores": cores, "threads": torch.get_num_threads(),
+            "parallel_info": info}
+
+
+def cpu_baseline(configs, runs: int = 10, warmup: int = 2) -> dict:
+    """The PyTorch-CPU restatement of the step (``oracle/cpu_step.py``,
+    pinned against the numpy oracle) on this host's cores: median of `runs`
+    after `warmup`, per configuration, on each configuration's full first
+    step (config 5: its first mixed step's 560 packed rows)."""
+    import statistics
+
+    import torch
+
+    from oracle import cpu_step
+
+    host = host_cpu()
+    out = {}
+    for name, (workload, step) in configs.items():
+        x, logits = step.packed()
+        times = []
+        for k in range(warmup + runs):
+            t0 = time.perf_counter()
+            cpu_step.moe_step(x, logits, workload.experts, workload.shared)
+            if k >= warmup:
+                times.append(time.perf_counter() - t0)
+        us = statistics.median(times) * 1e6
+        out[name] = {"us_per_step": round(us, 1), "rows": len(x),
+                     "tokens_per_s": round(len(x) / (us * 1e-6), 1), "runs": runs,
+                     "warmup": warmup}
+    return {**host, "configs": out}
+
+
+def decode_parity(workload, step, out) -> dict:
+    """The decode step's live output rows against the numpy oracle."""
     import numpy as np
     import torch
 
     from oracle import moe as om
+    from oracle.numerics import bf16_to_f32
 
-    import threadpoolctl
-
-    np.ones(2) @ np.ones(2)  # load the BLAS so its pool is listed
-    pools = [p["num_threads"] for p in threadpoolctl.threadpool_info() if p["user_api"] == "blas"]
-    threads = max(pools) if pools else 1
+    active, _ = om.compact_slots(step.occupancy.numpy())
+    x = step.x_slots.view(torch.int16).numpy().view(np.uint16)[active]
+    weights, ids = om.route(step.logits_slots.float().numpy()[active])
     wt = om.ExpertWeights(*(t.view(torch.uint8).numpy() if t.dtype.itemsize == 1 else t.numpy()
                             for t in workload.experts.tensors()))
-    occ = step.occupancy.numpy()
-    x_all = step.x_slots.view(torch.int16).numpy().view(np.uint16)
-    logits_all = step.logits_slots.float().numpy()
-    times, out = [], None
-    for _ in range(samples):
-        t0 = time.perf_counter()
-        active, _ = om.compact_slots(occ)
-        weights, ids = om.route(logits_all[active])
-        out = om.expert_ffn(x_all[active], ids, weights, wt)
-        times.append(time.perf_counter() - t0)
-    return float(np.median(times)) * 1e6, threads, out
+    expected = om.expert_ffn(x, ids, weights, wt)
+    got = out.view(torch.int16).cpu().numpy().view(np.uint16)
+    a, b = bf16_to_f32(got).astype(np.float64), bf16_to_f32(expected).astype(np.float64)
+    err = float(np.sqrt(np.mean((a - b) ** 2) / np.mean(b ** 2)))
+    return {"rrms_vs_oracle": err, "max_abs": float(np.abs(a - b).max()),
+            "exact_fraction": float(np.mean(got == expected)), "tolerance_rrms": 1e-3,
+            "ok": err < 1e-3}
 
 
-def bench_prefill(torch, steps: int, copies: int = 2) -> dict:
+def bench_decode_config(torch, config: int, replays: int, working_set: float = 6e8) -> dict:
+    """A decode configuration's step (config 1: 4 of 64 slots; config 3: all
+    64 slots under Zipf-skewed routing; E16 H1024 I256) through DecodeStep:
+    one graph holds one step per weight copy, enough copies that their bytes
+    exceed the 256 MB MALL (cold), timed per replay; hot = the same graph on
+    one copy.  Parity of the live rows against the numpy oracle.  Reported,
+    not a roofline claim: at 12.6 MB of weights the step is launch-bound."""
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.pipeline import DecodeStep
+
+    device = torch.device("cuda:0")
+    w = workloads.CONFIGS[config]()
+    step = w.steps[0]
+    rows = int(step.occupancy.sum())
+    first = w.experts.to(device)
+    n_copies = max(4, int(working_set // sum(t.numel() * t.element_size() for t in first.tensors())))
+    copies = [first] + [workloads.Experts(*(t.clone() for t in first.tensors()))
+                        for _ in range(n_copies - 1)]
+    for c in copies:
+        prepare_experts(c)
+    occ = step.occupancy.to(device)
+    x, logits = step.x_slots.to(device), step.logits_slots.to(device)
+    ds = DecodeStep(workloads.SLOTS, w.num_experts, w.hidden, w.intermediate, device=device)
+    for c in copies:
+        out = ds(occ, x, logits, c)
+    torch.cuda.synchronize()
+    parity = decode_parity(w, step, out[:rows])
+
+    def graph_of(sequence):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for c in sequence:
+                ds(occ, x, logits, c)
+        return g
+
+    cold = replay_stats(torch, graph_of(copies), replays, len(copies))
+    hot = replay_stats(torch, graph_of([copies[0]] * len(copies)), replays, len(copies))
+    used = int(torch.unique(ds.workspace.ids[:rows]).numel())
+    nbytes = workloads.algorithmic_bytes(w, step, used)
+    return {"workload": w.name, "active_rows": rows, "used_experts": used,
+            "algorithmic_bytes_per_step": nbytes,
+            "us_per_step": round(cold["median_us"], 2), "mean_us": round(cold["mean_us"], 2),
+            "GB_s": round(nbytes / cold["median_us"] / 1e3, 1),
+            "hot_us_per_step": round(hot["median_us"], 2),
+            "tokens_per_s": round(rows / (cold["median_us"] * 1e-6), 1),
+            "parity": parity,
+            "timing": f"median of {replays} replays (after 10) of a graph of {len(copies)} steps, "
+                      f"one per weight copy ({len(copies)} copies, more bytes than the 256 MB "
+                      "MALL: cold); hot: the same graph on one copy"}
+
+
+def bench_prefill(torch, steps: int, copies: int = 2, replays: int = 100) -> dict:
     """Config 4: 16 packed prompts (~3.7k rows), routed top-8 FP8 MoE (H2048,
     E128, I768) plus a dense FP8 shared expert: route + quantise, wide route
     sort, tiled grouped FC1 (SwiGLU requant in its epilogue) and FC2 with the
@@ -148,6 +278,16 @@ def bench_prefill(torch, steps: int, copies: int = 2) -> dict:
         full(routed, shared)
     torch.cuda.synchronize()
     step_us = graph_us([lambda r=r, s=s: full(r, s) for r, s in sets], 2)
+
+    def graph_of(pairs):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for routed, shared in pairs:
+                full(routed, shared)
+        return g
+
+    cold = replay_stats(torch, graph_of(sets), replays, len(sets))
+    hot = replay_stats(torch, graph_of([sets[0]] * len(sets)), replays, len(sets))
     stage_us = {
         "route_quantize": graph_us([lambda: ws.front(xd, ld)], 4),
         "sort": graph_us([ws.sort], 4),
@@ -166,6 +306,8 @@ def bench_prefill(torch, steps: int, copies: int = 2) -> dict:
     return {
         "workload": w.name, "rows": rows, "sequences": len(step.cu_seqlens) - 1,
         "us_per_step": round(step_us, 2), "tokens_per_s": round(rows / (step_us * 1e-6), 1),
+        "median_us_per_step": round(cold["median_us"], 2),
+        "hot_median_us_per_step": round(hot["median_us"], 2),
         "TFLOP_s": round(tflops, 1), "mfma_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
         "GB_s": round(nbytes / step_us / 1e3, 1), "hbm_frac": round(nbytes / step_us / 1e3 / HBM_PEAK_GBS, 4),
         "flop_per_step": flop, "algorithmic_bytes_per_step": nbytes, "used_experts": used,
@@ -300,8 +442,9 @@ def bench_mixed(torch, steps: int = 50) -> dict:
         torch.cuda.synchronize()
         kept = int(step.rows.keep_count.item())
         us = time_graphs(torch, [step.graph], steps)
-        out[name] = {"us_per_step": round(us, 2), "moe_rows": kept,
-                     "tokens_per_s": round((48 + 512) / (us * 1e-6), 1)}
+        stats = replay_stats(torch, step.graph, max(steps, 100))
+        out[name] = {"us_per_step": round(us, 2), "median_us_per_step": round(stats["median_us"], 2),
+                     "moe_rows": kept, "tokens_per_s": round((48 + 512) / (us * 1e-6), 1)}
     return {"workload": "config 5 mixed step: 48 of 64 decode slots + 2 x 256 prompt rows "
                         "(640-row suffix), E16 H1024 I256 top-8",
             "rows": full, "live_rows": 48 + 512, **out,
@@ -325,7 +468,8 @@ def main():
     from drama3_amd.pipeline import DecodeStep
 
     if args.prefill_only:
-        print(json.dumps({"prefill": bench_prefill(torch, args.prefill_steps)}), flush=True)
+        print(json.dumps({"prefill": bench_prefill(torch, args.prefill_steps, replays=args.replays)}),
+              flush=True)
         return
     if args.mixed_only:
         print(json.dumps({"mixed": bench_mixed(torch, args.mixed_steps)}), flush=True)
@@ -388,6 +532,11 @@ def main():
     time_steps(copies, args.warmup)
     step_us, out = time_steps(copies, args.steps)
     hot_us, _ = time_steps([copies[0]] * len(copies), args.steps)
+    # BASELINE protocol next to the exact-K mean: >= 100 replays of the
+    # one-step-per-copy graph after >= 10 warm-up replays, each timed alone.
+    cold_replays = replay_stats(torch, step_graph(copies)[0], args.replays, len(copies))
+    hot_replays = replay_stats(torch, step_graph([copies[0]] * len(copies))[0], args.replays,
+                               len(copies))
     used = int(torch.unique(ws.ids[:rows]).numel())  # experts with at least one route
     step_bytes = workloads.algorithmic_bytes(w, step, used)
 
@@ -444,26 +593,26 @@ def main():
     fc2_gbs = fc2_bytes / fc2_us / 1e3
     step_gbs = step_bytes / step_us / 1e3
 
-    parity = None
+    parity = None if args.no_parity else decode_parity(w, step, out[:rows])
+    decode_configs = None if args.no_decode_configs else {
+        name: bench_decode_config(torch, c, args.replays) for name, c in (("c1", 1), ("c3", 3))}
     cpu = None
     if not args.no_cpu_baseline:
-        cpu_us, threads, expected = cpu_baseline(w, step, args.cpu_sample_steps)
-        got = out[:rows].view(torch.int16).cpu().numpy().view(np.uint16)
-        from oracle.numerics import bf16_to_f32
+        sample = {f"c{c}": (lambda wl_: (wl_, wl_.steps[0]))(w if c == 2 else workloads.CONFIGS[c]())
+                  for c in (1, 2, 3, 4, 5)}
+        base = cpu_baseline(sample, args.cpu_runs)
+        c2 = base["configs"]["c2"]
+        cpu = {"value": round(step_bytes / c2["us_per_step"] / 1e3, 3), "unit": "GB/s",
+               "cores": base["threads"], "kind": "port", "us_per_step": c2["us_per_step"],
+               "sample": (f"config 2's full decode step ({rows} live rows) through the PyTorch-CPU "
+                          f"restatement of the step (oracle/cpu_step.py: routing, quantisation, "
+                          f"per-expert dequantise + FP32 FC1 / SwiGLU / FC2, combine) on "
+                          f"{base['threads']} torch threads; median of {args.cpu_runs} runs after "
+                          f"2 warm-ups; `configs` holds every configuration timed the same way"),
+               **base}
 
-        a, b = bf16_to_f32(got).astype(np.float64), bf16_to_f32(expected).astype(np.float64)
-        err = float(np.sqrt(np.mean((a - b) ** 2) / np.mean(b ** 2)))
-        parity = {"rrms_vs_oracle": err, "max_abs": float(np.abs(a - b).max()),
-                  "tolerance_rrms": 1e-3, "ok": err < 1e-3}
-        cpu = {"value": round(step_bytes / cpu_us / 1e3, 3), "unit": "GB/s", "cores": threads,
-               "kind": "port", "us_per_step": round(cpu_us, 1),
-               "sample": f"median of {args.cpu_sample_steps} full config-2 decode steps ({rows} "
-                         "rows) of the numpy oracle (compaction, routing, quantisation, "
-                         "per-expert dequantise + FC1/SwiGLU/FC2 in float64, combine); `cores` "
-                         "is the BLAS thread pool, the element-wise numpy work runs on one",
-               "host_cpus": len(os.sched_getaffinity(0))}
-
-    prefill = None if args.no_prefill else bench_prefill(torch, args.prefill_steps)
+    prefill = None if args.no_prefill else bench_prefill(torch, args.prefill_steps,
+                                                         replays=args.replays)
     reference_shape = None if args.no_reference_shape else bench_reference_shape(torch)
     mixed = None if args.no_mixed else bench_mixed(torch, args.mixed_steps)
     moe_layer = None if args.no_reference_shape else bench_moe_layer(torch)
@@ -497,13 +646,22 @@ def main():
                              "layers), replayed; cold: every step streams its copy from HBM"},
         "hot": {"us_per_step": round(hot_us, 2),
                 "GB_s": round(step_bytes / hot_us / 1e3, 1)},
+        "per_replay": {"cold": {k: round(v, 2) if isinstance(v, float) else v
+                                for k, v in cold_replays.items()},
+                       "hot": {k: round(v, 2) if isinstance(v, float) else v
+                               for k, v in hot_replays.items()},
+                       "cold_median_GB_s": round(step_bytes / cold_replays["median_us"] / 1e3, 1),
+                       "cold_median_pct_of_hbm_peak": round(
+                           100.0 * step_bytes / cold_replays["median_us"] / 1e3 / HBM_PEAK_GBS, 1)},
         "roofline": {"bound": "hbm",
                      "kernel": ("decode_route_fc1" if frontless else
                                 "decode_expert_gemm FC1" if ws.sortless else "expert_gemm FC1"),
                      "achieved": round(fc1_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(fc1_gbs / HBM_PEAK_GBS, 4),
                      "traffic": FC1_TRAFFIC_BYTES["bytes"],
-                     "traffic_kernel": FC1_TRAFFIC_BYTES["kernel"], "us_per_launch": round(fc1_us, 2),
+                     "traffic_kernel": FC1_TRAFFIC_BYTES["kernel"],
+                     "traffic_measured_on": FC1_TRAFFIC_BYTES["measured_on"],
+                     "us_per_launch": round(fc1_us, 2),
                      "algorithmic_bytes_per_launch": fc1_bytes},
         "fc2": {"kernel": ("decode_expert_gemm FC2 (SwiGLU prologue)" if ws.sortless else
                            "expert_fc2_swiglu" if ws.swiglu_in_fc2 else "expert_gemm FC2"),
@@ -512,6 +670,7 @@ def main():
         "device_copy_GB_s": round(copy_gbs, 1),
         "cpu_baseline": cpu,
         "parity": parity,
+        "decode_configs": decode_configs,
         "prefill": prefill,
         "reference_shape": reference_shape,
         "mixed": mixed,

@@ -734,17 +734,22 @@ __global__ __launch_bounds__(kRoutedCombineThreads) void routed_combine_kernel(R
   if (inside) *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(row) * a.hidden + column) = pack_bf16x4(acc);
 }
 
-}  // namespace
-}  // namespace d3
+// ---------------------------------------------------------------------------
+// Entry points: each validates its arguments into a launch description
+// first, so the whole-step entry points can check all three stages before
+// launching any.
+// ---------------------------------------------------------------------------
+struct GemmLaunch {
+  int mode;
+  int kb;
+  int num_experts;
+  DecodeArgs args;
+};
 
-using namespace d3;
-
-extern "C" int d3_decode_expert_gemm(int32_t mode, const uint8_t* w, const float* ws,
-                                     int32_t num_experts, int32_t n, int32_t k,
-                                     const int32_t* ids, const int32_t* row_count,
-                                     int32_t capacity, int32_t top_k, const void* a,
-                                     const float* a_scales, int32_t exact_routes,
-                                     uint16_t* out_bf16, float* out_f32, void* stream) {
+int check_expert_gemm(int32_t mode, const uint8_t* w, const float* ws, int32_t num_experts,
+                      int32_t n, int32_t k, const int32_t* ids, const int32_t* row_count,
+                      int32_t capacity, int32_t top_k, const void* a, const float* a_scales,
+                      int32_t exact_routes, uint16_t* out_bf16, float* out_f32, GemmLaunch* launch) {
   D3_REQUIRE(mode == 0 || mode == 2, "decode_expert_gemm: mode must be 0 (FC1) or 2 (FC2 + SwiGLU)");
   D3_REQUIRE(w && ws && ids && a && (mode == 2 || a_scales), "decode_expert_gemm: null pointer");
   D3_REQUIRE(mode == 0 ? out_bf16 != nullptr : out_f32 != nullptr, "decode_expert_gemm: null output");
@@ -774,26 +779,30 @@ extern "C" int d3_decode_expert_gemm(int32_t mode, const uint8_t* w, const float
   args.act_scales = a_scales;
   args.out_bf16 = out_bf16;
   args.out_f32 = out_f32;
-  hipStream_t s = as_stream(stream);
-  if (mode == 0) {
-    if (kb == 8) launch_decode<8, 0>(num_experts, s, args);
-    else launch_decode<16, 0>(num_experts, s, args);
-  } else {
-    if (kb == 2) launch_decode<2, 2>(num_experts, s, args);
-    else if (kb == 4) launch_decode<4, 2>(num_experts, s, args);
-    else if (kb == 6) launch_decode<6, 2>(num_experts, s, args);
-    else launch_decode<8, 2>(num_experts, s, args);
-  }
-  D3_LAUNCHED("decode_expert_gemm");
+  *launch = GemmLaunch{mode, kb, num_experts, args};
+  return D3_OK;
 }
 
-extern "C" int d3_decode_route_fc1(const uint8_t* w, const float* ws, int32_t num_experts,
-                                   int32_t n, int32_t k, const uint8_t* occupancy,
-                                   int32_t capacity, const uint16_t* x, int64_t x_stride,
-                                   const void* logits, int32_t logits_dtype,
-                                   int64_t logits_stride, int32_t top_k, int32_t exact_routes,
-                                   int32_t* ids, int32_t* count, int32_t* active,
-                                   uint16_t* gate_up, void* stream) {
+void launch_expert_gemm(const GemmLaunch& l, hipStream_t s) {
+  if (l.mode == 0) {
+    if (l.kb == 8) launch_decode<8, 0>(l.num_experts, s, l.args);
+    else launch_decode<16, 0>(l.num_experts, s, l.args);
+  } else if (l.mode == 1) {
+    if (l.kb == 8) launch_decode<8, 1>(l.num_experts, s, l.args);
+    else launch_decode<16, 1>(l.num_experts, s, l.args);
+  } else {
+    if (l.kb == 2) launch_decode<2, 2>(l.num_experts, s, l.args);
+    else if (l.kb == 4) launch_decode<4, 2>(l.num_experts, s, l.args);
+    else if (l.kb == 6) launch_decode<6, 2>(l.num_experts, s, l.args);
+    else launch_decode<8, 2>(l.num_experts, s, l.args);
+  }
+}
+
+int check_route_fc1(const uint8_t* w, const float* ws, int32_t num_experts, int32_t n, int32_t k,
+                    const uint8_t* occupancy, int32_t capacity, const uint16_t* x, int64_t x_stride,
+                    const void* logits, int32_t logits_dtype, int64_t logits_stride, int32_t top_k,
+                    int32_t exact_routes, int32_t* ids, int32_t* count, int32_t* active,
+                    uint16_t* gate_up, GemmLaunch* launch) {
   D3_REQUIRE(w && ws && occupancy && x && logits && ids && count && active && gate_up,
              "decode_route_fc1: null pointer");
   D3_REQUIRE(logits_dtype == D3_DTYPE_BF16 || logits_dtype == D3_DTYPE_F32,
@@ -837,17 +846,19 @@ extern "C" int d3_decode_route_fc1(const uint8_t* w, const float* ws, int32_t nu
   args.count_out = count;
   args.active_out = active;
   args.out_bf16 = gate_up;
-  hipStream_t s = as_stream(stream);
-  if (kb == 8) launch_decode<8, 1>(num_experts, s, args);
-  else launch_decode<16, 1>(num_experts, s, args);
-  D3_LAUNCHED("decode_route_fc1");
+  *launch = GemmLaunch{1, kb, num_experts, args};
+  return D3_OK;
 }
 
-extern "C" int d3_decode_route_combine(const uint8_t* occupancy, int32_t capacity,
-                                       const void* logits, int32_t logits_dtype,
-                                       int64_t logits_stride, int32_t num_experts, int32_t top_k,
-                                       int32_t hidden, const float* down, void* weights,
-                                       int32_t weights_dtype, uint16_t* out, void* stream) {
+struct CombineLaunch {
+  bool f32;
+  RoutedCombineArgs args;
+};
+
+int check_route_combine(const uint8_t* occupancy, int32_t capacity, const void* logits,
+                        int32_t logits_dtype, int64_t logits_stride, int32_t num_experts,
+                        int32_t top_k, int32_t hidden, const float* down, void* weights,
+                        int32_t weights_dtype, uint16_t* out, CombineLaunch* launch) {
   D3_REQUIRE(occupancy && logits && down && weights && out, "decode_route_combine: null pointer");
   D3_REQUIRE(logits_dtype == D3_DTYPE_BF16 || logits_dtype == D3_DTYPE_F32,
              "decode_route_combine: logits must be bf16 or f32");
@@ -860,24 +871,120 @@ extern "C" int d3_decode_route_combine(const uint8_t* occupancy, int32_t capacit
                "decode_route_combine: capacity %d (<= %d), top_k %d (<= 8), E %d (<= 256)",
                capacity, kMaxSlots, top_k, num_experts);
   D3_REQUIRE(aligned(down, 16) && aligned(out, 8), "decode_route_combine: alignment");
-  RoutedCombineArgs args{occupancy, capacity, logits, logits_stride, num_experts, top_k,
-                         hidden, down, weights, weights_dtype == D3_DTYPE_F32 ? 1 : 0, out};
-  const int slices = (hidden + kRoutedCombineColumns - 1) / kRoutedCombineColumns;
-  const dim3 grid(capacity * slices), block(kRoutedCombineThreads);
-  hipStream_t s = as_stream(stream);
-  const bool f32 = logits_dtype == D3_DTYPE_F32;
-#define D3_COMBINE(NPL)                                                            \
-  if (f32)                                                                         \
-    hipLaunchKernelGGL((routed_combine_kernel<NPL, true>), grid, block, 0, s, args); \
-  else                                                                             \
-    hipLaunchKernelGGL((routed_combine_kernel<NPL, false>), grid, block, 0, s, args);
-  if (num_experts <= 64) {
+  *launch = CombineLaunch{logits_dtype == D3_DTYPE_F32,
+                          RoutedCombineArgs{occupancy, capacity, logits, logits_stride, num_experts,
+                                            top_k, hidden, down, weights,
+                                            weights_dtype == D3_DTYPE_F32 ? 1 : 0, out}};
+  return D3_OK;
+}
+
+void launch_route_combine(const CombineLaunch& l, hipStream_t s) {
+  const int slices = (l.args.hidden + kRoutedCombineColumns - 1) / kRoutedCombineColumns;
+  const dim3 grid(l.args.capacity * slices), block(kRoutedCombineThreads);
+#define D3_COMBINE(NPL)                                                                  \
+  if (l.f32)                                                                             \
+    hipLaunchKernelGGL((routed_combine_kernel<NPL, true>), grid, block, 0, s, l.args);  \
+  else                                                                                   \
+    hipLaunchKernelGGL((routed_combine_kernel<NPL, false>), grid, block, 0, s, l.args);
+  if (l.args.num_experts <= 64) {
     D3_COMBINE(1)
-  } else if (num_experts <= 128) {
+  } else if (l.args.num_experts <= 128) {
     D3_COMBINE(2)
   } else {
     D3_COMBINE(4)
   }
 #undef D3_COMBINE
+}
+
+// The three launches of the decode step on the given intermediate buffers:
+// FC1 from the slots (ids, count, active, gate_up), FC2 with the SwiGLU
+// requant (down), the routed combine (weights, out).  Everything is checked
+// before the first launch.
+int decode_step(const uint8_t* w13, const float* s13, const uint8_t* w2, const float* s2,
+                int32_t num_experts, int32_t hidden, int32_t intermediate, const uint8_t* occupancy,
+                int32_t capacity, const uint16_t* x, int64_t x_stride, const void* logits,
+                int32_t logits_dtype, int64_t logits_stride, int32_t top_k, int32_t exact_routes,
+                int32_t* ids, void* weights, int32_t weights_dtype, uint16_t* gate_up, float* down,
+                int32_t* active, int32_t* count, uint16_t* out, void* stream) {
+  D3_REQUIRE(hidden > 0 && intermediate > 0, "decode_step: hidden %d, intermediate %d", hidden,
+             intermediate);
+  GemmLaunch fc1{}, fc2{};
+  CombineLaunch combine{};
+  int status = check_route_fc1(w13, s13, num_experts, 2 * intermediate, hidden, occupancy, capacity,
+                               x, x_stride, logits, logits_dtype, logits_stride, top_k,
+                               exact_routes, ids, count, active, gate_up, &fc1);
+  if (status != D3_OK) return status;
+  status = check_expert_gemm(2, w2, s2, num_experts, hidden, intermediate, ids, count, capacity,
+                             top_k, gate_up, nullptr, exact_routes, nullptr, down, &fc2);
+  if (status != D3_OK) return status;
+  status = check_route_combine(occupancy, capacity, logits, logits_dtype, logits_stride, num_experts,
+                               top_k, hidden, down, weights, weights_dtype, out, &combine);
+  if (status != D3_OK) return status;
+  hipStream_t s = as_stream(stream);
+  launch_expert_gemm(fc1, s);
+  launch_expert_gemm(fc2, s);
+  launch_route_combine(combine, s);
+  D3_LAUNCHED("decode_step");
+}
+
+}  // namespace
+}  // namespace d3
+
+using namespace d3;
+
+extern "C" int d3_decode_expert_gemm(int32_t mode, const uint8_t* w, const float* ws,
+                                     int32_t num_experts, int32_t n, int32_t k,
+                                     const int32_t* ids, const int32_t* row_count,
+                                     int32_t capacity, int32_t top_k, const void* a,
+                                     const float* a_scales, int32_t exact_routes,
+                                     uint16_t* out_bf16, float* out_f32, void* stream) {
+  GemmLaunch launch{};
+  const int status = check_expert_gemm(mode, w, ws, num_experts, n, k, ids, row_count, capacity,
+                                       top_k, a, a_scales, exact_routes, out_bf16, out_f32, &launch);
+  if (status != D3_OK) return status;
+  launch_expert_gemm(launch, as_stream(stream));
+  D3_LAUNCHED("decode_expert_gemm");
+}
+
+extern "C" int d3_decode_route_fc1(const uint8_t* w, const float* ws, int32_t num_experts,
+                                   int32_t n, int32_t k, const uint8_t* occupancy,
+                                   int32_t capacity, const uint16_t* x, int64_t x_stride,
+                                   const void* logits, int32_t logits_dtype,
+                                   int64_t logits_stride, int32_t top_k, int32_t exact_routes,
+                                   int32_t* ids, int32_t* count, int32_t* active,
+                                   uint16_t* gate_up, void* stream) {
+  GemmLaunch launch{};
+  const int status = check_route_fc1(w, ws, num_experts, n, k, occupancy, capacity, x, x_stride,
+                                     logits, logits_dtype, logits_stride, top_k, exact_routes, ids,
+                                     count, active, gate_up, &launch);
+  if (status != D3_OK) return status;
+  launch_expert_gemm(launch, as_stream(stream));
+  D3_LAUNCHED("decode_route_fc1");
+}
+
+extern "C" int d3_decode_route_combine(const uint8_t* occupancy, int32_t capacity,
+                                       const void* logits, int32_t logits_dtype,
+                                       int64_t logits_stride, int32_t num_experts, int32_t top_k,
+                                       int32_t hidden, const float* down, void* weights,
+                                       int32_t weights_dtype, uint16_t* out, void* stream) {
+  CombineLaunch launch{};
+  const int status = check_route_combine(occupancy, capacity, logits, logits_dtype, logits_stride,
+                                         num_experts, top_k, hidden, down, weights, weights_dtype,
+                                         out, &launch);
+  if (status != D3_OK) return status;
+  launch_route_combine(launch, as_stream(stream));
   D3_LAUNCHED("decode_route_combine");
+}
+
+extern "C" int d3_decode_step(const uint8_t* w13, const float* s13, const uint8_t* w2,
+                              const float* s2, int32_t num_experts, int32_t hidden,
+                              int32_t intermediate, const uint8_t* occupancy, int32_t capacity,
+                              const uint16_t* x, int64_t x_stride, const void* logits,
+                              int32_t logits_dtype, int64_t logits_stride, int32_t top_k,
+                              int32_t exact_routes, int32_t* ids, void* weights,
+                              int32_t weights_dtype, uint16_t* gate_up, float* down,
+                              int32_t* active, int32_t* count, uint16_t* out, void* stream) {
+  return decode_step(w13, s13, w2, s2, num_experts, hidden, intermediate, occupancy, capacity, x,
+                     x_stride, logits, logits_dtype, logits_stride, top_k, exact_routes, ids,
+                     weights, weights_dtype, gate_up, down, active, count, out, stream);
 }

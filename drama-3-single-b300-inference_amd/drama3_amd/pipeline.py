@@ -412,6 +412,23 @@ class MoEWorkspace:
              logits.stride(0), s.top_k, self.exact_routes, ptr(self.ids), ptr(count),
              ptr(active), ptr(self.gate_up), stream)
 
+    def decode_step(self, experts, occupancy, x, logits, active, count, out=None,
+                    stream=None) -> torch.Tensor:
+        """decode_route_fc1 + decode_fc2 + decode_route_combine as one C call
+        (``d3_decode_step``: every stage checked before the first launch)."""
+        s, stream = self.shape, self._stream(stream)
+        out = self.out if out is None else out
+        w13, s13, l13 = fc1_operands(experts)
+        w2, s2, l2 = fc2_operands(experts)
+        if l13 != LAYOUT_FRAGMENT or l2 != LAYOUT_FRAGMENT:
+            raise ValueError("sortless decode needs fragment-major weights (prepare_experts)")
+        call("d3_decode_step", ptr(w13), ptr(s13), ptr(w2), ptr(s2), s.num_experts, s.hidden,
+             s.intermediate, ptr(occupancy), s.rows, ptr(x), x.stride(0), ptr(logits),
+             dtype_code(logits.dtype), logits.stride(0), s.top_k, self.exact_routes,
+             ptr(self.ids), ptr(self.weights), dtype_code(self.weights.dtype), ptr(self.gate_up),
+             ptr(self.down), ptr(active), ptr(count), ptr(out), stream)
+        return out
+
     def decode_route_combine(self, occupancy, logits, out=None, stream=None) -> torch.Tensor:
         """Combine of the step started by decode_route_fc1: the routing weights
         are recomputed from the logits (and stored in ``weights``)."""
@@ -663,10 +680,8 @@ class DecodeStep:
             return self._fused(occupancy, x_slots, logits_slots, experts, stream)
         ws.sortless = self.sortless and self.uses_sortless(experts)
         if ws.sortless and self.uses_frontless(occupancy, x_slots, logits_slots):
-            ws.decode_route_fc1(experts, occupancy, x_slots, logits_slots, self.active,
-                                self.count, stream)
-            ws.decode_fc2(experts, self.count, stream)
-            return ws.decode_route_combine(occupancy, logits_slots, stream=stream)
+            return ws.decode_step(experts, occupancy, x_slots, logits_slots, self.active,
+                                  self.count, stream=stream)
         ws.front(x_slots, logits_slots, occupancy=occupancy, active=self.active,
                  count=self.count, stream=stream)
         return ws.experts(experts, self.count, stream=stream)

@@ -448,6 +448,30 @@ int d3_decode_route_combine(const uint8_t *occupancy, int32_t capacity, const vo
                             int32_t weights_dtype, uint16_t *out, void *stream);
 
 /*
+ * A1-A12  The decode MoE step over persistent slots (three launches).
+ * Replaces DramaModel.routed_moe's decode path (src/drama3/model.py:520-583:
+ * the slot filter engine.py:637-647, route kernels.py:360-383, the per-128
+ * quantisation moe_input.py:24-27, expert_up_kernel / silu_mul_quant /
+ * expert_down_kernel and the combine kernels.py:290-322, 344) for one
+ * step: d3_decode_route_fc1 (ids int32 [capacity, top_k], *count, active
+ * int32 [capacity], gate_up bf16 [capacity * top_k, 2I] by pair), then
+ * d3_decode_expert_gemm mode 2 (down f32 [capacity * top_k, hidden] by pair)
+ * with row_count = count, then d3_decode_route_combine (weights [capacity,
+ * top_k] in weights_dtype, out bf16 [capacity, hidden]: row r < *count
+ * belongs to slot active[r]).  Every stage's arguments are checked before
+ * the first launch; the limits are those of the three entry points
+ * (fragment-major weights, hidden in {1024, 2048}, intermediate in {256,
+ * 512, 768, 1024}, capacity <= 256, top_k <= 8).
+ */
+int d3_decode_step(const uint8_t *w13, const float *s13, const uint8_t *w2, const float *s2,
+                   int32_t num_experts, int32_t hidden, int32_t intermediate,
+                   const uint8_t *occupancy, int32_t capacity, const uint16_t *x,
+                   int64_t x_stride, const void *logits, int32_t logits_dtype,
+                   int64_t logits_stride, int32_t top_k, int32_t exact_routes, int32_t *ids,
+                   void *weights, int32_t weights_dtype, uint16_t *gate_up, float *down,
+                   int32_t *active, int32_t *count, uint16_t *out, void *stream);
+
+/*
  * A1-A12  The whole decode MoE step in one launch.
  * Replaces DramaModel.routed_moe's decode path (src/drama3/model.py:520-583:
  * slot filter engine.py:637-647, route kernels.py:360-383, quantise

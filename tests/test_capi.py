@@ -146,6 +146,19 @@ def test_contract_violations_raise_value_error(lib):
                   16, 16, 16, 16, None)
 
 
+def test_decode_step_entry_points_check_before_launching(lib):
+    """The decode-step entry point rejects bad shapes with no GPU call,
+    checking every stage before it launches any."""
+    from drama3_amd import _lib
+
+    with pytest.raises(ValueError, match="K=1536 not in the compiled set"):
+        _lib.call("d3_decode_step", 16, 16, 16, 16, 16, 1536, 256, 16, 64, 16, 1536, 16, 0, 16,
+                  8, 64, 16, 16, 0, 16, 16, 16, 16, 16, None)
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.call("d3_decode_step", 16, 16, 16, 16, 16, 1024, 256, 16, 64, 16, 1024, 16, 0, 16,
+                  8, 64, None, 16, 0, 16, 16, 16, 16, 16, None)
+
+
 def test_product_code_does_not_import_the_oracle():
     package = ROOT / "drama-3-single-b300-inference_amd"
     for path in package.rglob("*.py"):
