@@ -28,6 +28,8 @@
 // front's per-128 rule.  The routing weights are then computed by the
 // combine (routed_combine_kernel) from the same logits with the front's
 // function, so every byte matches the chain that runs the front.
+#include <mutex>
+
 #include "common.h"
 #include "expert_tile.h"
 #include "front_rows.h"
@@ -927,6 +929,65 @@ int decode_step(const uint8_t* w13, const float* s13, const uint8_t* w2, const f
   D3_LAUNCHED("decode_step");
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free decode step: the intermediate buffers of decode_step live
+// in one device array of this file, `scratch`, for callers that cannot
+// allocate (code under graph capture, serving loops that forbid it).  Its
+// layout: ids int32 [pairs], route weights [pairs] (the logits' dtype),
+// gate_up bf16 [pairs, 2I], down f32 [pairs, H], pairs = capacity * top_k,
+// each region at a fixed offset sized for the maximum below.  Nothing in it
+// needs clearing: every buffer is written before it is read within a call
+// (ids and gate_up for every live route, down for every live route, the
+// weights of every live row).  The array is per GPU (each device holds its
+// own copy at its own address, found with hipGetSymbolAddress with that
+// device current) and every call on a GPU shares it: calls that overlap on
+// one GPU race.
+// ---------------------------------------------------------------------------
+constexpr int kStaticPairs = 512;     // capacity * top_k (64 slots x top-8)
+constexpr int kStaticGateUp = 2048;   // 2I
+constexpr int kStaticHidden = 2048;   // H
+constexpr size_t kScratchIds = 0;
+constexpr size_t kScratchWeights = kScratchIds + size_t{kStaticPairs} * 4;
+constexpr size_t kScratchGateUp = kScratchWeights + size_t{kStaticPairs} * 4;
+constexpr size_t kScratchDown = kScratchGateUp + size_t{kStaticPairs} * kStaticGateUp * 2;
+constexpr size_t kScratchBytes = kScratchDown + size_t{kStaticPairs} * kStaticHidden * 4;
+static_assert(kScratchWeights % 256 == 0 && kScratchGateUp % 256 == 0 && kScratchDown % 256 == 0,
+              "scratch regions keep 256-byte alignment");
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+uint8_t* g_scratch_address[kMaxDevices] = {};
+
+}  // namespace
+}  // namespace d3
+
+// The allocation-free decode step's device scratch (6 MiB + 4 KiB per GPU).
+static __device__ __align__(256) uint8_t scratch[d3::kScratchBytes];
+
+namespace d3 {
+namespace {
+
+// Address of `scratch` on the current device, looked up once per device.
+int scratch_address(uint8_t** address) {
+  int device = -1;
+  hipError_t status = hipGetDevice(&device);
+  if (status != hipSuccess)
+    return set_error(D3_ERR_HIP, "decode_step_static: hipGetDevice failed: %s", hipGetErrorString(status));
+  D3_SUPPORTED(device >= 0 && device < kMaxDevices, "decode_step_static: device %d beyond %d", device,
+               kMaxDevices);
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch_address[device] == nullptr) {
+    void* p = nullptr;
+    status = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (status != hipSuccess || p == nullptr)
+      return set_error(D3_ERR_HIP, "decode_step_static: hipGetSymbolAddress(scratch) failed: %s",
+                       hipGetErrorString(status));
+    g_scratch_address[device] = static_cast<uint8_t*>(p);
+  }
+  *address = g_scratch_address[device];
+  return D3_OK;
+}
+
 }  // namespace
 }  // namespace d3
 
@@ -987,4 +1048,32 @@ extern "C" int d3_decode_step(const uint8_t* w13, const float* s13, const uint8_
   return decode_step(w13, s13, w2, s2, num_experts, hidden, intermediate, occupancy, capacity, x,
                      x_stride, logits, logits_dtype, logits_stride, top_k, exact_routes, ids,
                      weights, weights_dtype, gate_up, down, active, count, out, stream);
+}
+
+extern "C" int d3_decode_step_static(const uint8_t* w13, const float* s13, const uint8_t* w2,
+                                     const float* s2, int32_t num_experts, int32_t hidden,
+                                     int32_t intermediate, const uint8_t* occupancy,
+                                     int32_t capacity, const uint16_t* x, int64_t x_stride,
+                                     const void* logits, int32_t logits_dtype,
+                                     int64_t logits_stride, int32_t top_k, int32_t exact_routes,
+                                     int32_t* active, int32_t* count, uint16_t* out,
+                                     void* stream) {
+  D3_REQUIRE(capacity >= 1 && top_k >= 1 && hidden > 0 && intermediate > 0,
+             "decode_step_static: capacity %d, top_k %d, hidden %d, intermediate %d", capacity,
+             top_k, hidden, intermediate);
+  D3_SUPPORTED(static_cast<int64_t>(capacity) * top_k <= kStaticPairs,
+               "decode_step_static: capacity %d x top_k %d = %lld routes exceeds the static "
+               "scratch's %d",
+               capacity, top_k, static_cast<long long>(capacity) * top_k, kStaticPairs);
+  D3_SUPPORTED(2 * intermediate <= kStaticGateUp && hidden <= kStaticHidden,
+               "decode_step_static: intermediate %d / hidden %d exceed the static scratch's %d / %d",
+               intermediate, hidden, kStaticGateUp / 2, kStaticHidden);
+  uint8_t* base = nullptr;
+  const int status = scratch_address(&base);
+  if (status != D3_OK) return status;
+  return decode_step(w13, s13, w2, s2, num_experts, hidden, intermediate, occupancy, capacity, x,
+                     x_stride, logits, logits_dtype, logits_stride, top_k, exact_routes,
+                     reinterpret_cast<int32_t*>(base + kScratchIds), base + kScratchWeights,
+                     logits_dtype, reinterpret_cast<uint16_t*>(base + kScratchGateUp),
+                     reinterpret_cast<float*>(base + kScratchDown), active, count, out, stream);
 }

@@ -86,6 +86,9 @@ SIGNATURES = {
     "d3_decode_step": (
         _i32, [_p, _p, _p, _p, _i32, _i32, _i32, _p, _i32, _p, _i64, _p, _i32, _i64, _i32, _i32,
                _p, _p, _i32, _p, _p, _p, _p, _p, _p]),
+    "d3_decode_step_static": (
+        _i32, [_p, _p, _p, _p, _i32, _i32, _i32, _p, _i32, _p, _i64, _p, _i32, _i64, _i32, _i32,
+               _p, _p, _p, _p]),
     "d3_moe_step_sync_ints": (_i32, [_i32, _i32, _i32, _i32]),
     "d3_moe_decode_step": (
         _i32, [_p, _i32, _p, _p, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32,

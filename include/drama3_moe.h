@@ -6,7 +6,8 @@
  * stream).  Nothing here allocates or frees memory, synchronises the stream
  * or copies device data to the host, so every call is hipGraph-capturable.
  * Calls are re-entrant: the library keeps no mutable global state besides a
- * thread-local error message.
+ * thread-local error message, except d3_decode_step_static, whose static
+ * device scratch is shared by every call on a GPU.
  *
  * Data types:   bf16 = uint16_t bit patterns;  fp8 = uint8_t OCP e4m3fn codes;
  *               fp32 block scales = float, one per 128 x 128 weight block or
@@ -470,6 +471,29 @@ int d3_decode_step(const uint8_t *w13, const float *s13, const uint8_t *w2, cons
                    int64_t logits_stride, int32_t top_k, int32_t exact_routes, int32_t *ids,
                    void *weights, int32_t weights_dtype, uint16_t *gate_up, float *down,
                    int32_t *active, int32_t *count, uint16_t *out, void *stream);
+
+/*
+ * A1-A12  d3_decode_step without a caller workspace, for callers that
+ * cannot allocate device memory (code under graph capture, serving loops
+ * that forbid allocation); it has no counterpart in the reference.  The
+ * intermediate buffers (ids, route weights in the logits' dtype, gate_up,
+ * down) live in a static device array of the library, 6 MiB + 4 KiB per
+ * GPU, held by each GPU it runs on until the process ends; the caller
+ * passes only inputs and outputs (active, count, out: as d3_decode_step).
+ * Limits of that array: capacity * top_k <= 512 routes, 2I <= 2048,
+ * hidden <= 2048; larger calls return D3_ERR_UNSUPPORTED and launch
+ * nothing.  Allocates nothing (no hipMalloc / hipFree).  Every call on one
+ * GPU shares the array: calls that overlap on one GPU (other streams, other
+ * threads) race and must be serialised by the caller.  Results equal
+ * d3_decode_step's byte for byte.
+ */
+int d3_decode_step_static(const uint8_t *w13, const float *s13, const uint8_t *w2,
+                          const float *s2, int32_t num_experts, int32_t hidden,
+                          int32_t intermediate, const uint8_t *occupancy, int32_t capacity,
+                          const uint16_t *x, int64_t x_stride, const void *logits,
+                          int32_t logits_dtype, int64_t logits_stride, int32_t top_k,
+                          int32_t exact_routes, int32_t *active, int32_t *count, uint16_t *out,
+                          void *stream);
 
 /*
  * A1-A12  The whole decode MoE step in one launch.

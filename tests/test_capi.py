@@ -147,10 +147,16 @@ def test_contract_violations_raise_value_error(lib):
 
 
 def test_decode_step_entry_points_check_before_launching(lib):
-    """The decode-step entry point rejects bad shapes with no GPU call,
-    checking every stage before it launches any."""
+    """Both decode-step entry points reject bad shapes with no GPU call: the
+    static variant its scratch limits first, the workspace one every stage."""
     from drama3_amd import _lib
 
+    args = (16, 16, 16, 16, 16, 1024, 256, 16, 128, 16, 1024, 16, 0, 16, 8, 64)
+    with pytest.raises(ValueError, match="exceeds the static scratch"):
+        _lib.call("d3_decode_step_static", *args, 16, 16, 16, None)
+    with pytest.raises(ValueError, match="exceed the static scratch"):
+        _lib.call("d3_decode_step_static", 16, 16, 16, 16, 16, 4096, 256, 16, 64, 16, 4096, 16,
+                  0, 16, 8, 64, 16, 16, 16, None)
     with pytest.raises(ValueError, match="K=1536 not in the compiled set"):
         _lib.call("d3_decode_step", 16, 16, 16, 16, 16, 1536, 256, 16, 64, 16, 1536, 16, 0, 16,
                   8, 64, 16, 16, 0, 16, 16, 16, 16, 16, None)
