@@ -398,8 +398,9 @@ def bench_moe_layer(torch, steps: int = 30, copies: int = 3) -> dict:
     return {"workload": "one MoE layer, 64 rows, H2048 E256 I512 top-8 + bf16 shared expert "
                         "(I512), packed input projection (the reference model's layer)",
             "us_per_layer": out,
-            "step": "bf16 projection GEMM -> [routed experts (decode step) || SwiGLU + bf16 "
-                    "down GEMM] -> combine_experts",
+            "step": "d3_dense_bf16 projection (SwiGLU activation in its epilogue) -> routed "
+                    "FC1 / FC2 (decode step) || d3_dense_bf16 shared down projection -> "
+                    "d3_combine_route_logits (routing weights, routed sum, gated shared add)",
             "timing": f"hipGraph, {copies} rotated weight copies"}
 
 

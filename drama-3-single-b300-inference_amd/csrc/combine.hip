@@ -10,6 +10,7 @@
 
 #include "common.h"
 #include "expert_tile.h"
+#include "front_rows.h"
 #include "status.h"
 
 namespace d3 {
@@ -166,6 +167,152 @@ __global__ __launch_bounds__(kThreads) void add_norm_kernel(
   }
 }
 
+// The decode layer's epilogue in one launch: for row r (a live slot of a
+// decode step whose FC1 ranked the experts itself, so no routing weights
+// are stored yet), wave 0 routes the row's logits with the front's function
+// (route_top_k) and rounds the weights to the stored dtype, while every
+// thread loads its columns' eight down rows (by pair r * top_k + rank), the
+// shared expert row and (kNorm) the residual row; then
+//   routed   = bf16(sum_rank w[rank] * down[rank])   (rank order, fp32 FMAs)
+//   combined = bf16 FMA(shared, bf16(sigmoid(gate)), routed)
+// and out = combined (combine_experts), or (kNorm) residual <- bf16(combined
+// + residual), out = bf16(residual * rsqrt(mean(residual^2) + eps) * (1 + w))
+// (combine_experts_add_norm).  The bytes equal d3_decode_route_combine
+// followed by d3_combine_experts (+ d3_add_norm): the same arithmetic in the
+// same order.
+struct RouteLogitArgs {
+  const float* down;
+  const void* logits;
+  int64_t logits_stride;  // elements
+  int num_experts;
+  int top_k;
+  void* weights;  // [rows, top_k] stored routing weights, or nullptr
+  int weights_f32;
+  const uint16_t* shared;
+  const uint16_t* gate;
+  int64_t gate_stride;
+  uint16_t* residual;
+  const uint16_t* norm;
+  float eps;
+  int width;
+  uint16_t* out;
+};
+
+template <int NPL, bool kF32, bool kNorm, int kChunks>
+__global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLogitArgs a) {
+  __shared__ float route_w[8];
+  __shared__ float scratch[kThreads / kWave];
+  const int row = blockIdx.x;
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int width = a.width;
+  const int64_t base = static_cast<int64_t>(row) * width;
+  RouteLogits<NPL> logits;
+  if (wave == 0)
+    load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
+                                     static_cast<int64_t>(row) * a.logits_stride * (kF32 ? 4 : 2),
+                                 a.num_experts, logits);
+  float4 y[kChunks][8];
+  float s[kChunks][4], res[kChunks][4];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int column = threadIdx.x * 4 + c * kThreads * 4;
+    const bool inside = column < width;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      y[c][r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (inside && r < a.top_k)
+        y[c][r] = *reinterpret_cast<const float4*>(a.down + (static_cast<int64_t>(row) * a.top_k + r) * width +
+                                                   column);
+    }
+    if (inside) {
+      load4(a.shared + base + column, s[c]);
+      if constexpr (kNorm) load4(a.residual + base + column, res[c]);
+    }
+  }
+  const float g = gate_bf16(a.gate, a.gate_stride, row);
+  if (wave == 0) {
+    const RouteChoice choice = route_top_k<NPL>(logits, a.num_experts, a.top_k);
+    if (lane < a.top_k) {
+      route_w[lane] = stored_weight(choice.weight, a.weights_f32);
+      if (a.weights != nullptr) {
+        const int64_t index = static_cast<int64_t>(row) * a.top_k + lane;
+        if (a.weights_f32)
+          static_cast<float*>(a.weights)[index] = choice.weight;
+        else
+          static_cast<uint16_t*>(a.weights)[index] = f32_to_bf16(choice.weight);
+      }
+    }
+  }
+  __syncthreads();
+  float values[kChunks][4];
+  float squares = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int column = threadIdx.x * 4 + c * kThreads * 4;
+    if (column >= width) continue;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      if (r < a.top_k) {
+        const float wr = route_w[r];
+        acc.x = fmaf(wr, y[c][r].x, acc.x);
+        acc.y = fmaf(wr, y[c][r].y, acc.y);
+        acc.z = fmaf(wr, y[c][r].z, acc.z);
+        acc.w = fmaf(wr, y[c][r].w, acc.w);
+      }
+    }
+    const float routed[4] = {round_bf16(acc.x), round_bf16(acc.y), round_bf16(acc.z), round_bf16(acc.w)};
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = fma_bf16(s[c][i], g, routed[i]);
+    if constexpr (kNorm) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = round_bf16(v[i] + res[c][i]);
+        squares += v[i] * v[i];
+        values[c][i] = v[i];
+      }
+      store4(a.residual + base + column, v);
+    } else {
+      store4(a.out + base + column, v);
+    }
+  }
+  if constexpr (kNorm) {
+    const float total = block_sum(squares, scratch);
+    const float inv = 1.0f / sqrtf(total / static_cast<float>(width) + a.eps);
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const int column = threadIdx.x * 4 + c * kThreads * 4;
+      if (column >= width) continue;
+      float w[4], v[4];
+      load4(a.norm + column, w);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = values[c][i] * inv * (1.0f + w[i]);
+      store4(a.out + base + column, v);
+    }
+  }
+}
+
+template <int NPL, bool kF32, bool kNorm>
+void launch_route_logits(const RouteLogitArgs& a, int rows, hipStream_t s) {
+  if (a.width <= kThreads * 4)
+    hipLaunchKernelGGL((combine_route_logits_kernel<NPL, kF32, kNorm, 1>), dim3(rows), dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((combine_route_logits_kernel<NPL, kF32, kNorm, 2>), dim3(rows), dim3(kThreads), 0, s, a);
+}
+
+template <int NPL>
+void launch_route_logits(const RouteLogitArgs& a, int rows, bool f32, bool norm, hipStream_t s) {
+  if (f32) {
+    if (norm) launch_route_logits<NPL, true, true>(a, rows, s);
+    else launch_route_logits<NPL, true, false>(a, rows, s);
+  } else {
+    if (norm) launch_route_logits<NPL, false, true>(a, rows, s);
+    else launch_route_logits<NPL, false, false>(a, rows, s);
+  }
+}
+
 // silu_mul (kernels.py:386-395): bf16(bf16(g * sigmoid(g)) * u).
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ x,
                                                             int64_t stride, int width,
@@ -177,7 +324,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
     load4(in + column, g);
     load4(in + width + column, u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = round_bf16(g[i] * (1.0f / (1.0f + expf(-g[i])))) * u[i];
+    for (int i = 0; i < 4; ++i) v[i] = silu_mul_value(g[i], u[i]);
     store4(out + static_cast<int64_t>(row) * width + column, v);
   }
 }
@@ -284,4 +431,45 @@ extern "C" int d3_silu_mul(const uint16_t* projected, int64_t row_stride, int32_
   hipLaunchKernelGGL(silu_mul_kernel, dim3(rows), dim3(kThreads), 0, as_stream(stream), projected,
                      row_stride, width, out);
   D3_LAUNCHED("silu_mul");
+}
+
+extern "C" int d3_combine_route_logits(const float* down, const void* logits, int32_t logits_dtype,
+                                       int64_t logits_stride, int32_t num_experts, int32_t top_k,
+                                       void* route_weights, int32_t weights_dtype,
+                                       const uint16_t* shared, const uint16_t* gate,
+                                       int64_t gate_stride, uint16_t* residual,
+                                       const uint16_t* weight, float eps, int32_t rows,
+                                       int32_t width, uint16_t* out, void* stream) {
+  D3_REQUIRE(down && logits && shared && gate && out && (residual == nullptr || weight != nullptr),
+             "combine_route_logits: null pointer");
+  D3_REQUIRE(logits_dtype == D3_DTYPE_BF16 || logits_dtype == D3_DTYPE_F32,
+             "combine_route_logits: logits must be bf16 or f32");
+  D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
+             "combine_route_logits: weights must be bf16 or f32");
+  D3_REQUIRE(num_experts >= 1 && top_k >= 1 && top_k <= num_experts && logits_stride >= num_experts,
+             "combine_route_logits: bad routing shape (E=%d, top_k=%d)", num_experts, top_k);
+  D3_SUPPORTED(top_k <= 8 && num_experts <= 256,
+               "combine_route_logits: top_k %d (<= 8), E %d (<= 256)", top_k, num_experts);
+  D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0, "combine_route_logits: width %d", width);
+  D3_SUPPORTED(width <= 2 * kThreads * 4, "combine_route_logits: width %d above %d", width,
+               2 * kThreads * 4);
+  D3_REQUIRE((reinterpret_cast<uintptr_t>(down) & 15u) == 0 && aligned8(shared) && aligned8(out) &&
+                 (residual == nullptr || (aligned8(residual) && aligned8(weight))),
+             "combine_route_logits: alignment");
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  const RouteLogitArgs args{down, logits, logits_stride, num_experts, top_k, route_weights,
+                            weights_dtype == D3_DTYPE_F32 ? 1 : 0, shared, gate, gate_stride,
+                            residual, weight, eps, width, out};
+  const bool f32 = logits_dtype == D3_DTYPE_F32, norm = residual != nullptr;
+  hipStream_t s = as_stream(stream);
+  if (num_experts <= 64)
+    launch_route_logits<1>(args, rows, f32, norm, s);
+  else if (num_experts <= 128)
+    launch_route_logits<2>(args, rows, f32, norm, s);
+  else
+    launch_route_logits<4>(args, rows, f32, norm, s);
+  D3_LAUNCHED("combine_route_logits");
 }

@@ -1,0 +1,223 @@
+// Dense bf16 GEMM of the MoE layer's small-batch projections (decode-sized
+// row counts): out[M, N] = x[M, K] . W[N, K]^T, fp32 accumulation, one bf16
+// rounding.  Used for the packed input projection (model.py:230-245,
+// 495-501: shared gate / up rows, router, shared-expert gate), whose
+// epilogue also forms the shared expert's activation silu_mul(gate, up)
+// (kernels.py:386-395), and for the shared expert's down projection.
+//
+// Design (gfx950, wave64, mfma_f32_16x16x32_bf16):
+//   * A workgroup owns two 16-row tiles of W and up to 64 rows of x per
+//     pass.  K is walked in chunks of 256 columns: the workgroup copies the
+//     chunk of both operands (64 x rows, 32 W rows; 48 KB) into LDS with
+//     coalesced 16-byte loads (each wave instruction reads 1 KB of
+//     contiguous row), the next two chunks' loads in flight (registers)
+//     while the current chunk is multiplied.
+//   * LDS rows are 512 bytes; the 16-byte part p of row r is stored at
+//     position p ^ (r & 31), so the 16 rows an MFMA fragment read touches
+//     land on distinct banks.
+//   * Wave w computes weight tile w / 4 against token tile w % 4 over the
+//     whole K, so no cross-wave reduction is needed.
+//   * Paired tiles (the projection's first 2I rows are the shared expert's
+//     gate rows then its up rows): a workgroup takes gate tile j and up tile
+//     j, so it holds both halves of 16 activation columns and writes
+//     act = bf16(bf16(silu(gate)) * up) from the rounded outputs, the bytes
+//     of d3_silu_mul.
+#include "common.h"
+#include "expert_tile.h"
+#include "status.h"
+
+namespace d3 {
+namespace {
+
+constexpr int kDenseWaves = 8;
+constexpr int kDenseThreads = kDenseWaves * kWave;
+constexpr int kDenseTokens = 64;   // x rows per pass (4 token tiles)
+constexpr int kDenseChunk = 256;   // K columns per LDS chunk (512 bytes of a row)
+constexpr int kDenseParts = kDenseChunk * 2 / 16;  // 16-byte parts per chunk row (32)
+constexpr int kXLoads = kDenseTokens * kDenseParts / kDenseThreads;  // 4 per thread
+constexpr int kWLoads = 32 * kDenseParts / kDenseThreads;            // 2 per thread
+
+struct DenseArgs {
+  const uint16_t* x;
+  int64_t x_stride;  // elements
+  int rows;
+  const uint16_t* w;  // [n, k]
+  int n;
+  int k;
+  uint16_t* out;
+  int64_t out_stride;  // elements
+  int pairs;           // workgroups 0 .. pairs-1 take gate tile j and up tile j
+  int pair_offset;     // rows between a gate tile and its up tile (I)
+  uint16_t* act;       // [rows, act_stride] silu_mul of each pair, or nullptr
+  int64_t act_stride;
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(int32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Byte offset of 16-byte part p of LDS row r (512-byte rows, XOR swizzle).
+__device__ __forceinline__ int lds_part(int r, int p) { return r * 512 + ((p ^ (r & 31)) << 4); }
+
+// CHUNKS = K / 256 (compile time, so the register sets of the chunk loop
+// are indexed statically).
+template <int CHUNKS>
+__global__ __launch_bounds__(kDenseThreads) void dense_bf16_kernel(DenseArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kDenseTokens * 512];
+  __shared__ __attribute__((aligned(16))) uint8_t wsm[2][32 * 512];
+  __shared__ floatx4 up_sum[4][kWave];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int row16 = lane & 15;
+  const int quarter = lane >> 4;
+  const int tiles = a.n / 16;
+  const int b = blockIdx.x;
+  int t0, t1;
+  if (b < a.pairs) {  // gate tile j and its up tile
+    t0 = b;
+    t1 = b + a.pair_offset / 16;
+  } else {  // two consecutive tiles after the pairs (the second clamped)
+    t0 = 2 * a.pairs + 2 * (b - a.pairs);
+    t1 = min(t0 + 1, tiles - 1);
+  }
+  const bool second = t1 != t0;
+  constexpr int chunks = CHUNKS;
+  const BufferView w_view(a.w, static_cast<uint32_t>(static_cast<int64_t>(a.n) * a.k * 2));
+  const BufferView x_view(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.rows) * a.x_stride * 2));
+  const int r_tile = wave >> 2;  // this wave's weight tile (0: t0, 1: t1)
+  const int t_tile = wave & 3;   // and token tile
+
+  for (int m0 = 0; m0 < a.rows; m0 += kDenseTokens) {
+    // staging of chunk c: thread loads x parts q = tid + 512 i (row q / 32,
+    // part q % 32) and W parts likewise (rows 0-15: tile t0, 16-31: t1);
+    // the next two chunks are in flight in registers (set c % 2) while chunk
+    // c is multiplied from LDS (a third measured no faster).
+    constexpr int kSets = chunks < 2 ? chunks : 2;
+    int4 xr[kSets][kXLoads], wr[kSets][kWLoads];
+    auto load_chunk = [&](int c, int set) {
+#pragma unroll
+      for (int i = 0; i < kXLoads; ++i) {
+        const int q = tid + kDenseThreads * i, r = q >> 5, p = q & 31;
+        const int token = m0 + r;
+        xr[set][i] = x_view.load16(token < a.rows ? static_cast<uint32_t>((static_cast<int64_t>(token) * a.x_stride +
+                                                                             c * kDenseChunk + p * 8) * 2)
+                                                  : kNoRow);
+      }
+#pragma unroll
+      for (int i = 0; i < kWLoads; ++i) {
+        const int q = tid + kDenseThreads * i, r = q >> 5, p = q & 31;
+        const int row = (r < 16 ? t0 : t1) * 16 + (r & 15);
+        wr[set][i] = w_view.load16(static_cast<uint32_t>((static_cast<int64_t>(row) * a.k + c * kDenseChunk + p * 8) * 2));
+      }
+    };
+    auto store_chunk = [&](int set, int slot) {
+#pragma unroll
+      for (int i = 0; i < kXLoads; ++i) {
+        const int q = tid + kDenseThreads * i;
+        *reinterpret_cast<int4*>(&xs[slot][lds_part(q >> 5, q & 31)]) = xr[set][i];
+      }
+#pragma unroll
+      for (int i = 0; i < kWLoads; ++i) {
+        const int q = tid + kDenseThreads * i;
+        *reinterpret_cast<int4*>(&wsm[slot][lds_part(q >> 5, q & 31)]) = wr[set][i];
+      }
+    };
+#pragma unroll
+    for (int c = 0; c < kSets; ++c) load_chunk(c, c);
+    store_chunk(0, 0);
+    __syncthreads();
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < chunks; ++c) {
+      // set c % 2 was stored; reuse it for chunk c + 2
+      if (c + kSets < chunks) load_chunk(c + kSets, c % kSets);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint8_t* xb = xs[c & 1];
+      const uint8_t* wb = wsm[c & 1];
+      const int xrow = 16 * t_tile + row16, wrow = 16 * r_tile + row16;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int p = 4 * s + quarter;  // k = 32 s + 8 quarter .. + 8
+        const int32x4 av = *reinterpret_cast<const int32x4*>(&wb[lds_part(wrow, p)]);
+        const int32x4 bv = *reinterpret_cast<const int32x4*>(&xb[lds_part(xrow, p)]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), acc, 0, 0, 0);
+      }
+      if (c + 1 < chunks) store_chunk((c + 1) % kSets, (c + 1) & 1);
+      __syncthreads();
+    }
+    // lane holds rows 16 tile + 4 quarter .. + 3 of token m0 + 16 t_tile + row16
+    const int token = m0 + 16 * t_tile + row16;
+    const int tile = r_tile ? t1 : t0;
+    float rounded[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rounded[i] = bf16_to_f32(f32_to_bf16(acc[i]));
+    if (token < a.rows && (r_tile == 0 || second)) {
+      const uint32_t lo = f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
+      const uint32_t hi = f32_to_bf16(acc[2]) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16);
+      *reinterpret_cast<uint2*>(a.out + static_cast<int64_t>(token) * a.out_stride + tile * 16 + 4 * quarter) =
+          make_uint2(lo, hi);
+    }
+    if (b < a.pairs && a.act != nullptr) {  // uniform over the workgroup
+      if (r_tile == 1) up_sum[t_tile][lane] = floatx4{rounded[0], rounded[1], rounded[2], rounded[3]};
+      __syncthreads();
+      if (r_tile == 0 && token < a.rows) {
+        const floatx4 up = up_sum[t_tile][lane];
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = silu_mul_value(rounded[i], up[i]);
+        const uint32_t lo = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+        const uint32_t hi = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+        *reinterpret_cast<uint2*>(a.act + static_cast<int64_t>(token) * a.act_stride + t0 * 16 + 4 * quarter) =
+            make_uint2(lo, hi);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+bool aligned_to(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+}  // namespace
+}  // namespace d3
+
+using namespace d3;
+
+extern "C" int d3_dense_bf16(const uint16_t* x, int64_t x_stride, int32_t rows, const uint16_t* w,
+                             int32_t n, int32_t k, int32_t pair_rows, uint16_t* out,
+                             int64_t out_stride, uint16_t* act, int64_t act_stride, void* stream) {
+  D3_REQUIRE(x && w && out, "dense_bf16: null pointer");
+  D3_REQUIRE(rows >= 0 && n > 0 && k > 0 && pair_rows >= 0 && 2 * pair_rows <= n,
+             "dense_bf16: rows %d, N %d, K %d, pair_rows %d", rows, n, k, pair_rows);
+  const int chunks = k / kDenseChunk;
+  D3_SUPPORTED(k % kDenseChunk == 0 && (chunks == 1 || chunks == 2 || chunks == 3 || chunks == 4 ||
+                                        chunks == 6 || chunks == 8),
+               "dense_bf16: K=%d not in {256, 512, 768, 1024, 1536, 2048}", k);
+  D3_SUPPORTED(n % 16 == 0 && pair_rows % 16 == 0, "dense_bf16: N=%d and pair_rows %d must be multiples of 16",
+               n, pair_rows);
+  D3_SUPPORTED(rows <= 1024, "dense_bf16: %d rows above the 1024 of the small-batch kernel", rows);
+  D3_REQUIRE(x_stride >= k && out_stride >= n && (act == nullptr || act_stride >= pair_rows),
+             "dense_bf16: row strides");
+  D3_REQUIRE(aligned_to(x, 16) && x_stride % 8 == 0 && aligned_to(w, 16) && aligned_to(out, 8) &&
+                 out_stride % 4 == 0 && (act == nullptr || (aligned_to(act, 8) && act_stride % 4 == 0)),
+             "dense_bf16: x / w rows must be 16-byte aligned, out / act rows 8-byte");
+  D3_SUPPORTED(static_cast<int64_t>(rows) * x_stride * 2 < (int64_t{1} << 31) &&
+                   static_cast<int64_t>(n) * k * 2 < (int64_t{1} << 31),
+               "dense_bf16: operands above 2 GiB");
+  if (rows == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  const int pairs = pair_rows / 16;
+  const int rest = n / 16 - 2 * pairs;
+  const DenseArgs args{x, x_stride, rows, w, n, k, out, out_stride, pairs, pair_rows, act, act_stride};
+  const dim3 grid(pairs + (rest + 1) / 2), block(kDenseThreads);
+  hipStream_t s = as_stream(stream);
+  switch (k / kDenseChunk) {
+    case 1: hipLaunchKernelGGL(dense_bf16_kernel<1>, grid, block, 0, s, args); break;
+    case 2: hipLaunchKernelGGL(dense_bf16_kernel<2>, grid, block, 0, s, args); break;
+    case 3: hipLaunchKernelGGL(dense_bf16_kernel<3>, grid, block, 0, s, args); break;
+    case 4: hipLaunchKernelGGL(dense_bf16_kernel<4>, grid, block, 0, s, args); break;
+    case 6: hipLaunchKernelGGL(dense_bf16_kernel<6>, grid, block, 0, s, args); break;
+    default: hipLaunchKernelGGL(dense_bf16_kernel<8>, grid, block, 0, s, args); break;
+  }
+  D3_LAUNCHED("dense_bf16");
+}

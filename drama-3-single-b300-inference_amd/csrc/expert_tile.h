@@ -120,6 +120,13 @@ __device__ __forceinline__ float swiglu_value(float g, float u) {
   return (g * sig) * u;
 }
 
+// The reference's bf16 SwiGLU, silu_mul (kernels.py:392-394): silu(g)
+// rounded to bf16, times u; the caller rounds the product to bf16 as it
+// stores it.
+__device__ __forceinline__ float silu_mul_value(float g, float u) {
+  return bf16_to_f32(f32_to_bf16(g * (1.0f / (1.0f + expf(-g))))) * u;
+}
+
 // SwiGLU + e4m3 requantisation of one 128-column group held by 16 lanes
 // (8 gate and 8 up bf16 values per lane): a = swiglu_value(g, u), scale =
 // max(amax, 1e-10) / 448, codes quantize_four(a, scale) (IEEE division by

@@ -102,6 +102,9 @@ SIGNATURES = {
                                           _i32, _i32, _p, _p]),
     "d3_add_norm": (_i32, [_p, _p, _p, _f32, _i32, _i32, _p, _p]),
     "d3_silu_mul": (_i32, [_p, _i64, _i32, _i32, _p, _p]),
+    "d3_dense_bf16": (_i32, [_p, _i64, _i32, _p, _i32, _i32, _i32, _p, _i64, _p, _i64, _p]),
+    "d3_combine_route_logits": (_i32, [_p, _p, _i32, _i64, _i32, _i32, _p, _i32, _p, _p, _i64, _p,
+                                       _p, _f32, _i32, _i32, _p, _p]),
     "d3_row_metadata": (_i32, [_p, _p, _i32, _i32, _p, _i32, _i64, _p, _p, _p, _p]),
     "d3_mixed_rows": (_i32, [_p, _i32, _i32, _i64, _p, _i32, _i32, _p, _i32, _p, _i32, _p, _p, _p,
                              _p, _p, _p, _p, _p, _p]),

@@ -7,11 +7,19 @@ The reference projects the layer input once through a packed bf16 matrix
 gate and up rows, the router, the shared-expert gate, zero-padded by 127
 rows), runs the bf16 shared expert (``silu_mul`` then ``down_proj``) on a
 side stream while the routed top-8 FP8 experts run on the main stream, and
-joins before the combine (``model.py:506-518``).  Here the two bf16 GEMMs
-are plain library GEMMs (``torch.mm``, two-dimensional: hipBLASLt), the
-SwiGLU, the routed experts and the combine are this package's kernels, and
-the side stream is a default-priority stream forked after the projection
-and joined before the routed rows are read.
+joins before the combine (``model.py:506-518``).
+
+Here, for decode-sized batches (up to 1024 rows), both bf16 GEMMs are this
+package's MFMA kernel (``d3_dense_bf16``: the projection, whose epilogue
+also writes the shared expert's ``silu_mul`` activation, and the shared
+down projection), and with
+at most 256 rows the routed experts are the decode step, whose combine is
+folded into the layer's (``d3_combine_route_logits``: routing weights,
+rank-order routed sum, gated shared add and optionally the residual +
+RMSNorm of ``combine_experts_add_norm``, one launch).  Larger batches run
+the projections as library GEMMs (``torch.mm``, hipBLASLt) and the prefill
+path.  ``overlap`` puts the shared expert on a default-priority side stream
+forked after the projection and joined before the combine.
 """
 
 from __future__ import annotations
@@ -21,9 +29,11 @@ import torch.nn.functional as F
 
 from . import _lib
 from ._lib import call, ptr
-from .pipeline import DecodeStep, MoEWorkspace, Shape, require_cuda
+from .pipeline import DTYPE_BF16, DecodeStep, MoEWorkspace, Shape, dtype_code, require_cuda
 
 PROJECTION_PADDING = 127  # zero rows the reference appends (model.py:236-245)
+DENSE_ROWS = 1024  # most rows of d3_dense_bf16
+DENSE_K = (256, 512, 768, 1024, 1536, 2048)
 
 
 def pack_input_projection(gate_proj: torch.Tensor, up_proj: torch.Tensor, router: torch.Tensor,
@@ -40,18 +50,39 @@ def pack_input_projection(gate_proj: torch.Tensor, up_proj: torch.Tensor, router
     return F.pad(torch.cat(parts), (0, 0, 0, PROJECTION_PADDING))
 
 
+def dense_bf16(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, pair_rows: int = 0,
+               act: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """``out = x @ weight.T`` on the MFMA kernel (``d3_dense_bf16``).  With
+    ``pair_rows`` P and ``act``, weight rows [0, P) / [P, 2P) are a gate /
+    up pair and ``act`` receives ``silu_mul`` of the rounded outputs."""
+    require_cuda(x, weight, out, act)
+    if any(t is not None and t.dtype != torch.bfloat16 for t in (x, weight, out, act)):
+        raise TypeError("dense_bf16 takes bf16 operands")
+    n, k = weight.shape
+    if weight.stride(1) != 1 or weight.stride(0) != k or x.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError("weight must be contiguous, x and out rows unit-stride")
+    if x.shape[1] != k or out.shape != (x.shape[0], n):
+        raise ValueError("shapes do not match the projection")
+    if act is not None and (act.shape != (x.shape[0], pair_rows) or act.stride(1) != 1):
+        raise ValueError("act must be [rows, pair_rows] with unit column stride")
+    stream = _lib.stream(x.device) if stream is None else stream
+    call("d3_dense_bf16", ptr(x), x.stride(0), x.shape[0], ptr(weight), n, k, pair_rows, ptr(out),
+         out.stride(0), ptr(act), act.stride(0) if act is not None else 0, stream)
+    return out
+
+
 class MoELayer:
     """``moe_parts`` / ``moe`` of one layer for up to ``rows`` rows.
 
     ``parts(x, ...)`` returns (routed, shared, shared_gate) views into the
-    layer's buffers; ``__call__`` adds ``combine_experts``.  Routed experts:
-    with ``rows <= 256`` the decode step (``DecodeStep`` with every row a
-    live slot), otherwise the prefill path (``MoEWorkspace``: routes sorted,
-    tiled grouped GEMMs when the shapes allow).  ``overlap`` runs the shared
-    expert on a side stream; off by default: on MI355X the in-line order
-    measured faster (one reference-shape layer, 64 rows: 147.4 us in line,
-    158.7 us with the side stream), the routed GEMMs already filling the
-    device while they stream their weights.
+    layer's buffers; ``__call__`` returns ``combine_experts`` of them and
+    ``add_norm`` the residual + RMSNorm form (``combine_experts_add_norm``).
+    Routed experts: with ``rows <= 256`` the decode step (``DecodeStep``
+    with every row a live slot), otherwise the prefill path
+    (``MoEWorkspace``: routes sorted, tiled grouped GEMMs when the shapes
+    allow).  ``overlap`` runs the shared expert on a side stream; off by
+    default: on MI355X the in-line order measured faster, the routed GEMMs
+    already filling the device while they stream their weights.
     """
 
     def __init__(self, rows: int, num_experts: int, hidden: int, intermediate: int,
@@ -69,6 +100,10 @@ class MoELayer:
         self.act = torch.empty((rows, shared_intermediate), **bf16)
         self.shared = torch.empty((rows, hidden), **bf16)
         self.out = torch.empty((rows, hidden), **bf16)
+        self.norm_out = torch.empty((rows, hidden), **bf16)
+        # own MFMA GEMMs for decode-sized batches whose shapes the kernel covers
+        self.dense = (rows <= DENSE_ROWS and hidden in DENSE_K and shared_intermediate in DENSE_K
+                      and width % 16 == 0 and width % 8 == 0 and hidden % 16 == 0)
         self.decode = rows <= 256
         if self.decode:
             self.step = DecodeStep(rows, num_experts, hidden, intermediate, top_k, device=dev)
@@ -86,16 +121,7 @@ class MoELayer:
         shared_gate = self.projected[:, 2 * s + self.num_experts:2 * s + self.num_experts + 1]
         return gate_up, router, shared_gate
 
-    def _shared_expert(self, gate_up, down_proj) -> None:
-        stream = _lib.stream(self.device)
-        call("d3_silu_mul", ptr(gate_up), gate_up.stride(0), self.rows, self.shared_intermediate,
-             ptr(self.act), stream)
-        torch.mm(self.act, down_proj.t(), out=self.shared)
-
-    def parts(self, x: torch.Tensor, projection: torch.Tensor, down_proj: torch.Tensor, experts):
-        """x bf16 [rows, H]; projection = ``pack_input_projection(...)``;
-        down_proj bf16 [H, shared_intermediate].  Returns (routed [rows, H],
-        shared [rows, H], shared_gate [rows, 1])."""
+    def _check(self, x, projection, down_proj) -> None:
         require_cuda(x, projection, down_proj)
         if x.shape != (self.rows, self.hidden) or x.dtype != torch.bfloat16:
             raise ValueError(f"x must be bf16 [{self.rows}, {self.hidden}]")
@@ -103,29 +129,103 @@ class MoELayer:
             raise ValueError("projection must be pack_input_projection's [N, H]")
         if down_proj.shape != (self.hidden, self.shared_intermediate):
             raise ValueError("down_proj must be [H, shared_intermediate]")
+
+    def _project(self, x, projection) -> None:
+        """The packed projection; the own kernel also writes the shared
+        expert's activation ``silu_mul(gate | up)`` from its epilogue."""
+        if self.dense:
+            dense_bf16(x, projection.contiguous(), self.projected, self.shared_intermediate,
+                       self.act)
+        else:
+            torch.mm(x, projection.t(), out=self.projected)
+
+    def _shared_expert(self, gate_up, down_proj) -> None:
+        if self.dense:
+            dense_bf16(self.act, down_proj.contiguous(), self.shared)
+            return
+        call("d3_silu_mul", ptr(gate_up), gate_up.stride(0), self.rows, self.shared_intermediate,
+             ptr(self.act), _lib.stream(self.device))
+        torch.mm(self.act, down_proj.t(), out=self.shared)
+
+    def _fused(self, experts, x, router) -> bool:
+        """Whether the routed combine folds into the layer's combine: the
+        decode step's three-launch path (routes ranked inside FC1)."""
+        step = self.step if self.decode else None
+        return (step is not None and step.sortless and step.uses_sortless(experts)
+                and step.uses_frontless(self.all_rows, x, router) and self.hidden <= 2048
+                and self.num_experts <= 256)
+
+    def _routed_and_shared(self, x, projection, down_proj, experts, fuse: bool):
+        """Projection, routed experts (without their combine when ``fuse``)
+        and shared expert; returns the router logits view."""
+        self._check(x, projection, down_proj)
         main = torch.cuda.current_stream(self.device)
-        torch.mm(x, projection.t(), out=self.projected)
-        gate_up, router, shared_gate = self._views()
+        self._project(x, projection)
+        gate_up, router, _ = self._views()
         if self.side is not None:
             # Fork after the projection; join before the outputs are read
             # (the reference's moe_shared_stream, model.py:506-517).
             self.side.wait_stream(main)
             with torch.cuda.stream(self.side):
                 self._shared_expert(gate_up, down_proj)
-        if self.decode:
-            routed = self.step(self.all_rows, x, router, experts)
-            self.routed = routed  # the decode step's output buffer
+        if fuse:
+            ws, stream = self.step.workspace, _lib.stream(self.device)
+            ws.decode_route_fc1(experts, self.all_rows, x, router, self.step.active,
+                                self.step.count, stream)
+            ws.decode_fc2(experts, self.step.count, stream)
+        elif self.decode:
+            self.routed = self.step(self.all_rows, x, router, experts)
         else:
-            routed = self.workspace.forward(x, router, experts, out=self.routed)
+            self.workspace.forward(x, router, experts, out=self.routed)
         if self.side is None:
             self._shared_expert(gate_up, down_proj)
         else:
             main.wait_stream(self.side)
-        return routed, self.shared, shared_gate
+        return router
+
+    def parts(self, x: torch.Tensor, projection: torch.Tensor, down_proj: torch.Tensor, experts):
+        """x bf16 [rows, H]; projection = ``pack_input_projection(...)``;
+        down_proj bf16 [H, shared_intermediate].  Returns (routed [rows, H],
+        shared [rows, H], shared_gate [rows, 1])."""
+        self._routed_and_shared(x, projection, down_proj, experts, fuse=False)
+        _, _, shared_gate = self._views()
+        return self.routed, self.shared, shared_gate
+
+    def _combine(self, x, projection, down_proj, experts, residual=None, norm_weight=None,
+                 eps=0.0, out=None) -> torch.Tensor:
+        fuse = self._fused(experts, x, self._views()[1])
+        router = self._routed_and_shared(x, projection, down_proj, experts, fuse)
+        _, _, gate = self._views()
+        stream = _lib.stream(self.device)
+        if fuse:
+            ws = self.step.workspace
+            call("d3_combine_route_logits", ptr(ws.down), ptr(router), DTYPE_BF16, router.stride(0),
+                 self.num_experts, ws.shape.top_k, ptr(ws.weights), dtype_code(ws.weights.dtype),
+                 ptr(self.shared), ptr(gate), gate.stride(0), ptr(residual), ptr(norm_weight),
+                 float(eps), self.rows, self.hidden, ptr(out), stream)
+        elif residual is None:
+            call("d3_combine_experts", ptr(self.routed), ptr(self.shared), ptr(gate),
+                 gate.stride(0), self.rows, self.hidden, ptr(out), stream)
+        else:
+            call("d3_combine_experts_add_norm", ptr(self.routed), ptr(self.shared), ptr(gate),
+                 gate.stride(0), None, ptr(residual), ptr(norm_weight), float(eps), self.rows,
+                 self.hidden, ptr(out), stream)
+        return out
 
     def __call__(self, x, projection, down_proj, experts) -> torch.Tensor:
         """``moe``: combine_experts(routed, shared, shared_gate) -> bf16 [rows, H]."""
-        routed, shared, gate = self.parts(x, projection, down_proj, experts)
-        call("d3_combine_experts", ptr(routed), ptr(shared), ptr(gate), gate.stride(0), self.rows,
-             self.hidden, ptr(self.out), _lib.stream(self.device))
-        return self.out
+        return self._combine(x, projection, down_proj, experts, out=self.out)
+
+    def add_norm(self, x, projection, down_proj, experts, residual: torch.Tensor,
+                 norm_weight: torch.Tensor, eps: float) -> torch.Tensor:
+        """``combine_experts_add_norm`` of the layer (``kernels.py:448-499``,
+        as the backbone applies it, ``model.py:596-606``): residual is
+        updated in place, the (1 + w) RMS-normalised rows are returned."""
+        require_cuda(residual, norm_weight)
+        if (residual.shape != (self.rows, self.hidden) or residual.dtype != torch.bfloat16
+                or not residual.is_contiguous()):
+            raise ValueError("residual must be contiguous bf16 [rows, hidden]")
+        if norm_weight.shape != (self.hidden,) or norm_weight.dtype != torch.bfloat16:
+            raise ValueError("norm weight must be bf16 [hidden]")
+        return self._combine(x, projection, down_proj, experts, residual,
+                             norm_weight.contiguous(), eps, out=self.norm_out)

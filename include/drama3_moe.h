@@ -624,6 +624,51 @@ int d3_silu_mul(const uint16_t *projected, int64_t row_stride, int32_t rows, int
                 uint16_t *out, void *stream);
 
 /*
+ * A11, A12  The decode layer's epilogue in one launch.
+ * Replaces route_kernel's weights (src/drama3/kernels.py:360-383), the
+ * routed combine (kernels.py:319-322) and combine_experts /
+ * combine_experts_add_norm (kernels.py:427-499) after a decode step whose
+ * FC1 ranked the experts itself (d3_decode_route_fc1: rows = live slots,
+ * down f32 [rows * top_k, width] by pair, no weights stored).  Row r: the
+ * routing weights of logits row r (bf16 or f32, logits_stride) rounded to
+ * weights_dtype (also stored in route_weights [rows, top_k] when non-NULL),
+ * routed = bf16(sum_rank w * down[r * top_k + rank]) in rank order,
+ * combined = single-rounding bf16 FMA shared * bf16(sigmoid(gate)) +
+ * routed; with residual == NULL out[r] = combined, otherwise residual[r] <-
+ * bf16(combined + residual[r]) and out[r] = bf16(residual * rsqrt(mean(
+ * residual^2) + eps) * (1 + weight)).  Bytes equal d3_decode_route_combine
+ * then d3_combine_experts (then d3_add_norm).  top_k <= 8, E <= 256,
+ * width <= 2048.
+ */
+int d3_combine_route_logits(const float *down, const void *logits, int32_t logits_dtype,
+                            int64_t logits_stride, int32_t num_experts, int32_t top_k,
+                            void *route_weights, int32_t weights_dtype, const uint16_t *shared,
+                            const uint16_t *gate, int64_t gate_stride, uint16_t *residual,
+                            const uint16_t *weight, float eps, int32_t rows, int32_t width,
+                            uint16_t *out, void *stream);
+
+/*
+ * f4  Dense bf16 GEMM of the MoE layer's small-batch projections.
+ * Replaces the two bf16 linear layers around the routed experts in
+ * DramaModel.moe_parts (src/drama3/model.py:495-518): the packed input
+ * projection (shared gate / up rows, router, shared-expert gate;
+ * model.py:230-245) with the shared expert's silu_mul (kernels.py:386-402)
+ * in its epilogue, and the shared expert's down projection.
+ * out[r, j] = bf16(sum_c x[r, c] w[j, c]) for r < rows, j < n, c < k, fp32
+ * accumulation.  With pair_rows = P > 0, rows [0, P) of w are gate rows and
+ * rows [P, 2P) the matching up rows; when act != NULL it also receives
+ * act[r, c] = bf16(bf16(silu(out[r, c])) * out[r, P + c]) for c < P (the
+ * bytes of d3_silu_mul on out).  x bf16 [rows, x_stride], w bf16 [n, k]
+ * row-major (a torch Linear weight), out bf16 [rows, out_stride], act bf16
+ * [rows, act_stride].  k in {256, 512, 768, 1024, 1536, 2048}, n and P
+ * multiples of 16, rows <= 1024; x / w rows 16-byte aligned, out / act rows
+ * 8-byte.
+ */
+int d3_dense_bf16(const uint16_t *x, int64_t x_stride, int32_t rows, const uint16_t *w, int32_t n,
+                  int32_t k, int32_t pair_rows, uint16_t *out, int64_t out_stride, uint16_t *act,
+                  int64_t act_stride, void *stream);
+
+/*
  * A13  Ragged packed-row metadata.
  * Replaces row_metadata (src/drama3/packed_prefill.py:51-78).
  * cu_seqlens int32 [sequences + 1], sequence_slots int64 [sequences] ->
