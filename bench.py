@@ -45,8 +45,6 @@ def parse():
     p.add_argument("--copies", type=int, default=6, help="rotated weight copies (cold cache)")
     p.add_argument("--kernel-reps", type=int, default=8, help="FC1/FC2 graph repetitions per copy")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--fused", action="store_true",
-                   help="time the one-launch step (d3_moe_decode_step) instead of the kernel chain")
     p.add_argument("--cpu-runs", type=int, default=10,
                    help="timed runs per configuration of the CPU baseline (after 2 warm-ups)")
     p.add_argument("--replays", type=int, default=100,
@@ -489,8 +487,7 @@ def main():
         prepare_experts(c)
     occ = step.occupancy.to(device)
     x_slots, logits_slots = step.x_slots.to(device), step.logits_slots.to(device)
-    ds = DecodeStep(workloads.SLOTS, w.num_experts, w.hidden, w.intermediate, device=device,
-                    fused=args.fused)
+    ds = DecodeStep(workloads.SLOTS, w.num_experts, w.hidden, w.intermediate, device=device)
 
     # eager warm-up run, then one graph per weight copy
     side = torch.cuda.Stream()
@@ -638,8 +635,7 @@ def main():
                    "experts": e, "hidden": h, "intermediate": i, "top_k": workloads.TOP_K,
                    "used_experts": used, "algorithmic_bytes_per_step": step_bytes,
                    "weight_copies": len(copies),
-                   "step": ("one launch (d3_moe_decode_step)" if args.fused else
-                            "FC1 routing + quantising the slots itself, sortless FC2, routed "
+                   "step": ("FC1 routing + quantising the slots itself, sortless FC2, routed "
                             "combine (3 launches)" if frontless else
                             "front + sortless decode GEMMs + combine" if ws.sortless else
                             "front + sorted expert GEMMs + combine"),

@@ -47,37 +47,13 @@
 namespace d3 {
 namespace {
 
-// Fused epilogues of the expert GEMM.  Each output group is finished by the
-// last workgroup that contributes to it: contributors publish their tile
-// (coherent stores, waited for), take a ticket with one atomic add, and the
-// one holding the final ticket reads every contribution back with coherent
-// loads, finishes the group and resets its ticket to 0 for the next launch.
-// Nobody waits on another workgroup.
-enum Fuse : int {
-  kFuseNone = 0,
-  kFuseSwiglu = 1,   // FC1: SwiGLU + requant of each (route, 128-column) group
-  kFuseCombine = 2,  // FC2: weighted top-k combine of each (token, column tile)
-};
-
-struct EpilogueArgs {
-  int32_t* tickets;
-  // kFuseSwiglu
-  int intermediate;
-  uint8_t* act_out;
-  float* act_scales_out;
-  // kFuseCombine
-  const void* route_weights;
-  int route_weights_f32;
-  uint16_t* combined;
-};
-
-template <int KB, int RT, int MODE, int FUSE, bool kPacked, int TILES>
+template <int KB, int RT, int MODE, bool kPacked, int TILES>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void expert_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows,
     const uint8_t* __restrict__ act, const float* __restrict__ act_scales,
     const int32_t* __restrict__ sorted_ids, int top_k, const int4* __restrict__ items,
     const int32_t* __restrict__ num_items, int exact_routes, uint16_t* __restrict__ out_bf16,
-    float* __restrict__ out_f32, EpilogueArgs epi) {
+    float* __restrict__ out_f32) {
   constexpr int K = KB * kGroup;
   constexpr int kRowsPerWave = RT * 16;
   constexpr int kRowsPerGroup = kGemmWaves * kRowsPerWave;
@@ -87,9 +63,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   __shared__ __attribute__((aligned(16))) uint8_t b_tile[16 * kStride];
   __shared__ float b_scales[16 * KB];
   __shared__ int b_target[16];  // FC1: sorted position, FC2: pair id; -1 = no route
-  __shared__ int finish[16];    // fused epilogue: group this workgroup finishes, or -1
 
-  static_assert(TILES == 1 || FUSE == kFuseNone, "fused epilogues take one weight tile per workgroup");
   const int tiles = n_rows / kRowsPerGroup;
   const int groups = tiles / TILES;  // workgroups per item
   const int item_index = blockIdx.x / groups;
@@ -266,81 +240,10 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
           const uint32_t lo = f32_to_bf16(acc[rt][0]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][1])) << 16);
           const uint32_t hi = f32_to_bf16(acc[rt][2]) | (static_cast<uint32_t>(f32_to_bf16(acc[rt][3])) << 16);
           uint16_t* dst = out_bf16 + static_cast<size_t>(target) * n_rows + n;
-          if constexpr (FUSE == kFuseSwiglu)
-            publish_u64(dst, (static_cast<uint64_t>(hi) << 32) | lo);
-          else
-            *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+          *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
         } else {
           float* dst = out_f32 + static_cast<size_t>(target) * n_rows + n;
-          if constexpr (FUSE == kFuseCombine) {
-            publish_u64(dst, (static_cast<uint64_t>(__float_as_uint(acc[rt][1])) << 32) |
-                                 __float_as_uint(acc[rt][0]));
-            publish_u64(dst + 2, (static_cast<uint64_t>(__float_as_uint(acc[rt][3])) << 32) |
-                                     __float_as_uint(acc[rt][2]));
-          } else {
-            *reinterpret_cast<float4*>(dst) = make_float4(acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]);
-          }
-        }
-      }
-    }
-    if constexpr (FUSE != kFuseNone) {
-      const int tile_n0 = tile * kRowsPerGroup;
-      wait_stores();  // this tile's published outputs are visible device-wide
-      __syncthreads();
-      if (threadIdx.x < 16) {
-        const int c = threadIdx.x;
-        const int t = b_target[c];
-        int done = -1;
-        if (t >= 0) {
-          if constexpr (FUSE == kFuseSwiglu) {
-            // (sorted row, act group): 128 / tile gate tiles + as many up tiles
-            const bool up = tile_n0 >= epi.intermediate;
-            const int g = (up ? tile_n0 - epi.intermediate : tile_n0) / kGroup;
-            const int contributors = 2 * (kGroup / kRowsPerGroup);
-            const int index = t * (epi.intermediate / kGroup) + g;
-            if (take_ticket(&epi.tickets[index]) == contributors - 1) done = index;
-          } else {
-            // (token, column tile): one contribution per routed expert
-            const int index = (t / top_k) * tiles + tile;
-            if (take_ticket(&epi.tickets[index]) == top_k - 1) done = index;
-          }
-        }
-        finish[c] = done;
-      }
-      __syncthreads();
-      const int seg = threadIdx.x >> 4;  // one 16-thread segment per route column
-      const int part = threadIdx.x & 15;
-      const int index = finish[seg];
-      if (index >= 0) {
-        if constexpr (FUSE == kFuseSwiglu) {
-          const int groups = epi.intermediate / kGroup;
-          const int row = index / groups;
-          const int g = index % groups;
-          const uint16_t* gate = out_bf16 + static_cast<size_t>(row) * n_rows + g * kGroup + part * 8;
-          const uint64_t g0 = collect_u64(gate), g1 = collect_u64(gate + 4);
-          const uint64_t u0 = collect_u64(gate + epi.intermediate);
-          const uint64_t u1 = collect_u64(gate + epi.intermediate + 4);
-          const uint4 graw = make_uint4(static_cast<uint32_t>(g0), static_cast<uint32_t>(g0 >> 32),
-                                        static_cast<uint32_t>(g1), static_cast<uint32_t>(g1 >> 32));
-          const uint4 uraw = make_uint4(static_cast<uint32_t>(u0), static_cast<uint32_t>(u0 >> 32),
-                                        static_cast<uint32_t>(u1), static_cast<uint32_t>(u1 >> 32));
-          uint2 codes;
-          const float scale = swiglu_quant_group(graw, uraw, &codes);
-          *reinterpret_cast<uint2*>(epi.act_out + static_cast<size_t>(row) * epi.intermediate +
-                                    g * kGroup + part * 8) = codes;
-          if (part == 0) {
-            epi.act_scales_out[static_cast<size_t>(row) * groups + g] = scale;
-            reset_ticket(&epi.tickets[index]);
-          }
-        } else {
-          const int token = index / tiles;
-          for (int column = tile_n0 + part * 4; column < tile_n0 + kRowsPerGroup; column += 64) {
-            const float4 v = combine4<true>(out_f32, epi.route_weights, epi.route_weights_f32,
-                                            token, top_k, n_rows, column);
-            *reinterpret_cast<uint2*>(epi.combined + static_cast<size_t>(token) * n_rows + column) =
-                pack_bf16x4(v);
-          }
-          if (part == 0) reset_ticket(&epi.tickets[index]);
+          *reinterpret_cast<float4*>(dst) = make_float4(acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]);
         }
       }
     }
@@ -473,7 +376,6 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint8_t* __rest
 
 struct GemmLaunch {
   int mode;
-  int fuse;
   int packed;  // weight layout: 0 reference [E, N, K], 1 fragment-major
   const uint8_t* w;
   const float* ws;
@@ -489,7 +391,6 @@ struct GemmLaunch {
   int exact_routes;
   uint16_t* out_bf16;
   float* out_f32;
-  EpilogueArgs epi;
 };
 
 // Weight tiles per workgroup: FC2 takes two when every item is one route
@@ -498,27 +399,25 @@ struct GemmLaunch {
 // the SwiGLU requant - is done once, and the two-tile kernel fits three
 // workgroups per CU).  FC1 keeps one: its tiles are 128 KiB, and longer
 // workgroups leave a longer partial last round (measured on c2: 65.5 us
-// with two tiles against 62.5 us with one).  Fused epilogues take one.
-template <int KB, int RT, int MODE, int FUSE>
+// with two tiles against 62.5 us with one).
+template <int KB, int RT, int MODE>
 void launch_gemm(int tiles, hipStream_t s, const GemmLaunch& g) {
-  const bool pair = FUSE == kFuseNone && MODE != 0 && tiles % 2 == 0 && g.item_rows <= 16;
+  const bool pair = MODE != 0 && tiles % 2 == 0 && g.item_rows <= 16;
   const dim3 grid(g.max_items * (pair ? tiles / 2 : tiles));
 #define D3_GEMM_ARGS                                                                          \
   grid, dim3(kGemmThreads), 0, s, g.w, g.ws, g.n, g.a, g.as, g.sorted_ids, g.top_k, g.items, \
-      g.num_items, g.exact_routes, g.out_bf16, g.out_f32, g.epi
-  if constexpr (FUSE == kFuseNone) {
-    if (pair) {
-      if (g.packed)
-        hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, true, 2>), D3_GEMM_ARGS);
-      else
-        hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, false, 2>), D3_GEMM_ARGS);
-      return;
-    }
+      g.num_items, g.exact_routes, g.out_bf16, g.out_f32
+  if (pair) {
+    if (g.packed)
+      hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, true, 2>), D3_GEMM_ARGS);
+    else
+      hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, false, 2>), D3_GEMM_ARGS);
+    return;
   }
   if (g.packed)
-    hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, true, 1>), D3_GEMM_ARGS);
+    hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, true, 1>), D3_GEMM_ARGS);
   else
-    hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, FUSE, false, 1>), D3_GEMM_ARGS);
+    hipLaunchKernelGGL((expert_gemm_kernel<KB, RT, MODE, false, 1>), D3_GEMM_ARGS);
 #undef D3_GEMM_ARGS
 }
 
@@ -534,22 +433,12 @@ int dispatch_gemm(const GemmLaunch& g, hipStream_t s) {
   D3_SUPPORTED(g.n % rows_per_group == 0, "expert_gemm: N=%d must be a multiple of %d for K=%d",
                g.n, rows_per_group, KB * kGroup);
   const int tiles = g.n / rows_per_group;
-  if (g.fuse == kFuseSwiglu) {
-    if constexpr (rows_per_group <= kGroup) {
-      launch_gemm<KB, RT, 0, kFuseSwiglu>(tiles, s, g);
-      return D3_OK;
-    }
-    return set_error(D3_ERR_UNSUPPORTED, "expert_fc1_swiglu: K=%d tiles %d rows (> 128)",
-                     KB * kGroup, rows_per_group);
-  }
-  if (g.fuse == kFuseCombine)
-    launch_gemm<KB, RT, 1, kFuseCombine>(tiles, s, g);
-  else if (g.mode == 0)
-    launch_gemm<KB, RT, 0, kFuseNone>(tiles, s, g);
+  if (g.mode == 0)
+    launch_gemm<KB, RT, 0>(tiles, s, g);
   else if (g.mode == 1)
-    launch_gemm<KB, RT, 1, kFuseNone>(tiles, s, g);
+    launch_gemm<KB, RT, 1>(tiles, s, g);
   else if constexpr (KB <= kMaxSwigluKB)
-    launch_gemm<KB, RT, 2, kFuseNone>(tiles, s, g);
+    launch_gemm<KB, RT, 2>(tiles, s, g);
   else
     return set_error(D3_ERR_UNSUPPORTED, "expert_fc2_swiglu: intermediate %d > %d", KB * kGroup,
                      kMaxSwigluKB * kGroup);
@@ -614,9 +503,9 @@ extern "C" int d3_expert_gemm(int32_t mode, const uint8_t* w, const float* ws,
   D3_REQUIRE(mode == 0 ? aligned(out_bf16, 8) : aligned(out_f32, 16),
              "expert_gemm: output alignment");
   D3_REQUIRE(item_rows >= 1, "expert_gemm: item_rows must be positive");
-  const GemmLaunch g{mode, kFuseNone, weight_layout, w, ws, n, a, a_scales, sorted_ids, top_k,
+  const GemmLaunch g{mode, weight_layout, w, ws, n, a, a_scales, sorted_ids, top_k,
                      reinterpret_cast<const int4*>(items), num_items, max_items, item_rows,
-                     exact_routes, out_bf16, out_f32, EpilogueArgs{}};
+                     exact_routes, out_bf16, out_f32};
   int status = check_gemm(g, num_experts, k, "expert_gemm");
   if (status != D3_OK) return status;
   if (max_items == 0) {
@@ -628,71 +517,6 @@ extern "C" int d3_expert_gemm(int32_t mode, const uint8_t* w, const float* ws,
   D3_LAUNCHED("expert_gemm");
 }
 
-extern "C" int d3_expert_fc1_swiglu(const uint8_t* w13, const float* s13, int32_t weight_layout,
-                                    int32_t num_experts, int32_t intermediate, int32_t hidden,
-                                    const uint8_t* q,
-                                    const float* x_scales, const int32_t* sorted_ids,
-                                    int32_t top_k, const int32_t* items,
-                                    const int32_t* num_items, int32_t max_items,
-                                    int32_t exact_routes, uint16_t* gate_up, uint8_t* act,
-                                    float* act_scales, int32_t* tickets, void* stream) {
-  D3_REQUIRE(gate_up && act && act_scales && tickets, "expert_fc1_swiglu: null output");
-  D3_REQUIRE(intermediate > 0 && intermediate % kGroup == 0,
-             "expert_fc1_swiglu: intermediate %d must be a multiple of 128", intermediate);
-  D3_REQUIRE(aligned(gate_up, 16) && aligned(act, 8), "expert_fc1_swiglu: output alignment");
-  EpilogueArgs epi{};
-  epi.tickets = tickets;
-  epi.intermediate = intermediate;
-  epi.act_out = act;
-  epi.act_scales_out = act_scales;
-  const GemmLaunch g{0, kFuseSwiglu, weight_layout, w13, s13, 2 * intermediate, q, x_scales,
-                     sorted_ids, top_k,
-                     reinterpret_cast<const int4*>(items), num_items, max_items, 1 << 30,
-                     exact_routes, gate_up, nullptr, epi};
-  int status = check_gemm(g, num_experts, hidden, "expert_fc1_swiglu");
-  if (status != D3_OK) return status;
-  if (max_items == 0) {
-    clear_error();
-    return D3_OK;
-  }
-  status = run_gemm(g, hidden, as_stream(stream));
-  if (status != D3_OK) return status;
-  D3_LAUNCHED("expert_fc1_swiglu");
-}
-
-extern "C" int d3_expert_fc2_combine(const uint8_t* w2, const float* s2, int32_t weight_layout,
-                                     int32_t num_experts, int32_t hidden, int32_t intermediate,
-                                     const uint8_t* act,
-                                     const float* act_scales, const int32_t* sorted_ids,
-                                     int32_t top_k, const int32_t* items,
-                                     const int32_t* num_items, int32_t max_items,
-                                     int32_t exact_routes, float* down, const void* weights,
-                                     int32_t weights_dtype, uint16_t* out, int32_t* tickets,
-                                     void* stream) {
-  D3_REQUIRE(down && weights && out && tickets, "expert_fc2_combine: null output");
-  D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
-             "expert_fc2_combine: weights must be bf16 or f32");
-  D3_REQUIRE(aligned(down, 16) && aligned(out, 8), "expert_fc2_combine: output alignment");
-  EpilogueArgs epi{};
-  epi.tickets = tickets;
-  epi.route_weights = weights;
-  epi.route_weights_f32 = weights_dtype == D3_DTYPE_F32 ? 1 : 0;
-  epi.combined = out;
-  const GemmLaunch g{1, kFuseCombine, weight_layout, w2, s2, hidden, act, act_scales, sorted_ids,
-                     top_k,
-                     reinterpret_cast<const int4*>(items), num_items, max_items, 1 << 30,
-                     exact_routes, nullptr, down, epi};
-  int status = check_gemm(g, num_experts, intermediate, "expert_fc2_combine");
-  if (status != D3_OK) return status;
-  if (max_items == 0) {
-    clear_error();
-    return D3_OK;
-  }
-  status = run_gemm(g, intermediate, as_stream(stream));
-  if (status != D3_OK) return status;
-  D3_LAUNCHED("expert_fc2_combine");
-}
-
 extern "C" int d3_expert_fc2_swiglu(const uint8_t* w2, const float* s2, int32_t weight_layout,
                                     int32_t num_experts, int32_t hidden, int32_t intermediate,
                                     const uint16_t* gate_up, const int32_t* sorted_ids,
@@ -702,10 +526,10 @@ extern "C" int d3_expert_fc2_swiglu(const uint8_t* w2, const float* s2, int32_t 
   D3_REQUIRE(gate_up && down, "expert_fc2_swiglu: null pointer");
   D3_REQUIRE(item_rows >= 1, "expert_fc2_swiglu: item_rows must be positive");
   D3_REQUIRE(aligned(gate_up, 16) && aligned(down, 16), "expert_fc2_swiglu: alignment");
-  const GemmLaunch g{2, kFuseNone, weight_layout, w2, s2, hidden,
+  const GemmLaunch g{2, weight_layout, w2, s2, hidden,
                      reinterpret_cast<const uint8_t*>(gate_up), nullptr, sorted_ids, top_k,
                      reinterpret_cast<const int4*>(items), num_items, max_items, item_rows,
-                     exact_routes, nullptr, down, EpilogueArgs{}};
+                     exact_routes, nullptr, down};
   int status = check_gemm(g, num_experts, intermediate, "expert_fc2_swiglu");
   if (status != D3_OK) return status;
   if (max_items == 0) {

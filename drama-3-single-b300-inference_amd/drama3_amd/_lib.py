@@ -68,12 +68,6 @@ SIGNATURES = {
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p,
                _i32, _i32, _i32, _p, _p]),
     "d3_pack_expert_weights": (_i32, [_p, _i32, _i32, _i32, _p, _p]),
-    "d3_expert_fc1_swiglu": (
-        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _p, _p,
-               _p]),
-    "d3_expert_fc2_combine": (
-        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p, _i32, _p,
-               _p, _p]),
     "d3_expert_fc2_swiglu": (
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _p, _p]),
     "d3_decode_expert_gemm": (
@@ -89,10 +83,6 @@ SIGNATURES = {
     "d3_decode_step_static": (
         _i32, [_p, _p, _p, _p, _i32, _i32, _i32, _p, _i32, _p, _i64, _p, _i32, _i64, _i32, _i32,
                _p, _p, _p, _p]),
-    "d3_moe_step_sync_ints": (_i32, [_i32, _i32, _i32, _i32]),
-    "d3_moe_decode_step": (
-        _i32, [_p, _i32, _p, _p, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32,
-               _p, _p, _i32, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p]),
     "d3_silu_mul_quant": (_i32, [_p, _i32, _i32, _p, _p, _p, _i32, _p, _p, _p]),
     "d3_weighted_combine": (_i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
     "d3_combine_experts": (_i32, [_p, _p, _p, _i64, _i32, _i32, _p, _p]),

@@ -107,7 +107,7 @@ class MoEWorkspace:
 
     def __init__(self, shape: Shape, device: torch.device | str = "cuda", tile: int = SORT_TILE,
                  item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
-                 exact_routes: int = EXACT_ROUTES, fused_epilogues: bool = False,
+                 exact_routes: int = EXACT_ROUTES,
                  swiglu_in_fc2: bool | None = None, sortless: bool = False,
                  grouped: bool | None = None, shared_rows: int = 0, fused_sort: bool = False):
         lib = _lib.load()
@@ -126,7 +126,7 @@ class MoEWorkspace:
         contraction = self.item_rows > EXACT_ROUTES
         h, i = shape.hidden, shape.intermediate
         if grouped is None:
-            grouped = contraction and grouped_supported(h, i) and not fused_epilogues and not sortless
+            grouped = contraction and grouped_supported(h, i) and not sortless
         if grouped and item_rows is None and shape.rows > 128:
             self.item_rows = GROUPED_ITEM_ROUTES
         if self.item_rows % tile:
@@ -161,21 +161,12 @@ class MoEWorkspace:
                                       device=dev)
         self.down = torch.empty((pairs + shared_rows, h), dtype=torch.float32, device=dev)
         self.out = torch.empty((t, h), dtype=torch.bfloat16, device=dev)
-        # Optional fused epilogues (SwiGLU requant in FC1, combine in FC2)
-        # when the tiling allows; their tickets start at 0 and every launch
-        # leaves 0.  Off by default: with one short workgroup per 16-row tile
-        # the hand-off tail (coherent stores, ticket, finisher) costs more
-        # than the two small kernels it replaces (c2 decode: 90 + 49 us fused
-        # against 71.5 + 7 + 38.4 + 7 us unfused).
-        fc1_tile, fc2_tile = lib.d3_expert_tile_rows(h), lib.d3_expert_tile_rows(i)
-        self.fuse_fc1 = fused_epilogues and 0 < fc1_tile <= 128
-        self.fuse_fc2 = fused_epilogues and fc2_tile > 0
         # SwiGLU requant in FC2's prologue: every FC2 workgroup of an item
         # recomputes the item's activations, which is free while its weights
         # stream in as long as items are a few route tiles (decode).
         if swiglu_in_fc2 is None:
             swiglu_in_fc2 = self.item_rows <= EXACT_ROUTES and i <= 1024
-        self.swiglu_in_fc2 = swiglu_in_fc2 and not self.fuse_fc1 and not self.fuse_fc2
+        self.swiglu_in_fc2 = bool(swiglu_in_fc2)
         # Sortless decode: the front skips the route sort and the expert GEMMs
         # (d3_decode_expert_gemm, fragment-major weights) find each expert's
         # routes themselves; gate_up / down rows are indexed by pair.
@@ -188,12 +179,10 @@ class MoEWorkspace:
             raise ValueError(f"tiled grouped GEMMs need item_rows <= {GROUPED_ROUTES}, hidden and "
                              f"intermediate in {GROUPED_K}, hidden % 256 == 0")
         self.grouped = bool(grouped) and not sortless
-        self.fc1_tickets = torch.zeros(self.max_rows * (i // 128) if self.fuse_fc1 else 1, **i32)
         # Scratch of the wide route sort (prefill-sized batches).
         self.wide_sort = pairs > WIDE_SORT_PAIRS
         self.sort_scratch = torch.empty(
             lib.d3_sort_wide_scratch_ints(t, shape.top_k, e) if self.wide_sort else 1, **i32)
-        self.fc2_tickets = torch.zeros(t * (h // fc2_tile) if self.fuse_fc2 else 1, **i32)
 
     # -- stages ---------------------------------------------------------------
     def _stream(self, stream):
@@ -359,24 +348,6 @@ class MoEWorkspace:
         self.front(x, logits, row_index, row_count, stream=stream)
         return self.experts(experts, row_count, shared, out, stream)
 
-    def fc1_swiglu(self, experts, stream=None) -> None:
-        s, stream = self.shape, self._stream(stream)
-        w, ws, layout = fc1_operands(experts)
-        call("d3_expert_fc1_swiglu", ptr(w), ptr(ws), layout, s.num_experts, s.intermediate, s.hidden, ptr(self.q), ptr(self.x_scales),
-             ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
-             self.exact_routes, ptr(self.gate_up), ptr(self.act), ptr(self.act_scales),
-             ptr(self.fc1_tickets), stream)
-
-    def fc2_combine(self, experts, out=None, stream=None) -> torch.Tensor:
-        s, stream = self.shape, self._stream(stream)
-        out = self.out if out is None else out
-        w, ws, layout = fc2_operands(experts)
-        call("d3_expert_fc2_combine", ptr(w), ptr(ws), layout, s.num_experts, s.hidden, s.intermediate, ptr(self.act), ptr(self.act_scales),
-             ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
-             self.exact_routes, ptr(self.down), ptr(self.weights), dtype_code(self.weights.dtype),
-             ptr(out), ptr(self.fc2_tickets), stream)
-        return out
-
     def decode_fc1(self, experts, row_count=None, stream=None) -> None:
         """Sortless FC1: gate_up[pair] for every live route (fragment-major W13)."""
         s, stream = self.shape, self._stream(stream)
@@ -440,17 +411,9 @@ class MoEWorkspace:
         return out
 
     def experts(self, experts, row_count=None, shared=None, out=None, stream=None):
-        """FC1, SwiGLU requant, FC2 and combine over the routes sorted by front().
-        With ``fused_epilogues`` two launches replace four; a dense shared
-        expert is always added by the separate combine."""
+        """FC1, SwiGLU requant, FC2 and combine over the routes sorted by
+        front(); a dense shared expert is added by the combine."""
         stream = _lib.stream(self.device) if stream is None else stream
-        if self.fuse_fc2 and shared is None and not (self.sortless or self.grouped):
-            if self.fuse_fc1:
-                self.fc1_swiglu(experts, stream)
-            else:
-                self.fc1(experts, stream)
-                self.activation(stream)
-            return self.fc2_combine(experts, out, stream)
         self.routes_down(experts, row_count, stream)
         return self.combine(None, row_count, shared, out, stream)
 
@@ -464,9 +427,6 @@ class MoEWorkspace:
         elif self.grouped:
             self.grouped_fc1(experts, stream=stream)
             self.grouped_fc2(experts, stream=stream)
-        elif self.fuse_fc1:
-            self.fc1_swiglu(experts, stream)
-            self.fc2(experts, stream)
         else:
             self.fc1(experts, stream)
             self._fc2_stage(experts, stream)
@@ -585,8 +545,6 @@ def moe_with_shared(ws: MoEWorkspace, dense: DenseExpert | None, x, logits, expe
     if ws.grouped:
         ws.grouped_fc1(experts, stream=stream)
         ws.grouped_fc2(experts, stream=stream)
-    elif ws.fuse_fc1 or ws.fuse_fc2:
-        raise ValueError("moe_with_shared runs the unfused chain")
     else:
         ws.fc1(experts, stream)
         ws._fc2_stage(experts, stream)
@@ -616,11 +574,6 @@ class DecodeStep:
 
     Output row r belongs to slot ``active[r]`` for r < ``count``.
 
-    ``fused=True`` runs the whole step as one launch (``d3_moe_decode_step``)
-    on fragment-major weights (``prepare_experts``) and bf16 logits, with the
-    same buffers and results as the multi-kernel chain; other calls (and the
-    default) use the chain, which is currently the faster of the two.
-
     The sortless chain (``sortless``) normally starts with the front launch;
     with ``frontless`` (default: whenever the sortless chain runs and the
     inputs fit ``d3_decode_route_fc1``) the FC1 routes and quantises the
@@ -632,7 +585,7 @@ class DecodeStep:
 
     def __init__(self, slots: int, num_experts: int, hidden: int, intermediate: int,
                  top_k: int = 8, device="cuda", item_rows: int | None = None,
-                 fused: bool | None = None, sortless: bool | None = None,
+                 sortless: bool | None = None,
                  frontless: bool | None = None):
         dev = torch.device(device)
         self.slots = slots
@@ -659,25 +612,10 @@ class DecodeStep:
         self.frontless = self.sortless if frontless is None else bool(frontless)
         if self.frontless and not self.sortless:
             raise ValueError("frontless runs the sortless chain (sortless=True)")
-        sync_ints = lib.d3_moe_step_sync_ints(slots, num_experts, hidden, intermediate)
-        supported = sync_ints > 0 and slots <= 256 and num_experts <= 256
-        if fused and not supported:
-            raise ValueError(f"the one-launch step does not cover slots={slots}, "
-                             f"E={num_experts}, H={hidden}, I={intermediate}")
-        self.fused = bool(fused)
-        # Hand-off counters of the one-launch step: zero between launches.
-        self.sync = torch.zeros(max(sync_ints, 4), dtype=torch.int32, device=dev)
-
-    def uses_fused(self, logits_slots, experts) -> bool:
-        return (self.fused and logits_slots.dtype == torch.bfloat16
-                and fc1_operands(experts)[2] == LAYOUT_FRAGMENT
-                and fc2_operands(experts)[2] == LAYOUT_FRAGMENT)
 
     def __call__(self, occupancy, x_slots, logits_slots, experts, stream=None) -> torch.Tensor:
         stream = _lib.stream(x_slots.device) if stream is None else stream
         ws = self.workspace
-        if self.uses_fused(logits_slots, experts):
-            return self._fused(occupancy, x_slots, logits_slots, experts, stream)
         ws.sortless = self.sortless and self.uses_sortless(experts)
         if ws.sortless and self.uses_frontless(occupancy, x_slots, logits_slots):
             return ws.decode_step(experts, occupancy, x_slots, logits_slots, self.active,
@@ -714,23 +652,3 @@ class DecodeStep:
 
     def uses_sortless(self, experts) -> bool:
         return self.sortless and self.uses_sortless_layout(experts)
-
-    def _fused(self, occupancy, x_slots, logits_slots, experts, stream) -> torch.Tensor:
-        ws, s = self.workspace, self.workspace.shape
-        require_cuda(occupancy, x_slots, logits_slots)
-        if occupancy.numel() != self.slots or x_slots.shape[0] < self.slots:
-            raise ValueError("occupancy / x_slots must cover every slot")
-        w13, s13, _ = fc1_operands(experts)
-        w2, s2, _ = fc2_operands(experts)
-        call("d3_moe_decode_step", ptr(occupancy), self.slots, ptr(self.active), ptr(self.count),
-             ptr(x_slots), x_slots.stride(0), ptr(logits_slots), logits_slots.stride(0), s.hidden,
-             s.num_experts, s.intermediate, s.top_k, ptr(w13), ptr(s13), ptr(w2), ptr(s2),
-             ws.exact_routes, ptr(ws.ids), ptr(ws.weights), dtype_code(ws.weights.dtype),
-             ptr(ws.q), ptr(ws.x_scales), ptr(ws.sorted_ids), ws.max_rows, ptr(ws.gate_up),
-             ptr(ws.act), ptr(ws.act_scales), ptr(ws.down), ptr(ws.out), ptr(self.sync), stream)
-        return ws.out
-
-    def wait_failed(self) -> bool:
-        """True if a wait inside a one-launch step gave up (output invalid);
-        synchronises with the device."""
-        return int(self.sync[0].item()) != 0

@@ -330,39 +330,6 @@ int d3_pack_expert_weights(const uint8_t *w, int32_t num_experts, int32_t n, int
                            uint8_t *packed, void *stream);
 
 /*
- * A9 + A10  FC1 with the SwiGLU requantisation fused into its epilogue.
- * d3_expert_gemm mode 0 (gate_up bf16 at sorted positions, n = 2I, k = H)
- * after which, for every (sorted row, 128-column activation group), the last
- * workgroup to write one of the group's gate / up tiles computes the group
- * exactly as d3_silu_mul_quant: act fp8 [rows, I], act_scales [rows, I/128].
- * tickets: int32 [max sorted rows * I/128], all 0 before the first launch and
- * left at 0.  Needs d3_expert_tile_rows(hidden) <= 128.
- */
-int d3_expert_fc1_swiglu(const uint8_t *w13, const float *s13, int32_t weight_layout,
-                         int32_t num_experts, int32_t intermediate, int32_t hidden, const uint8_t *q,
-                         const float *x_scales, const int32_t *sorted_ids, int32_t top_k,
-                         const int32_t *items, const int32_t *num_items, int32_t max_items,
-                         int32_t exact_routes, uint16_t *gate_up, uint8_t *act, float *act_scales,
-                         int32_t *tickets, void *stream);
-
-/*
- * A11  FC2 with the weighted top-k combine fused into its epilogue.
- * d3_expert_gemm mode 1 (down fp32 by pair, n = H, k = I) after which, for
- * every (token, column tile), the last of its top_k contributing workgroups
- * writes out[token, tile] = bf16(sum_r w[t,r] down[t*top_k+r, tile]) in rank
- * order, exactly as d3_weighted_combine without a shared expert.
- * tickets: int32 [tokens * hidden / d3_expert_tile_rows(intermediate)], all
- * 0 before the first launch and left at 0.
- */
-int d3_expert_fc2_combine(const uint8_t *w2, const float *s2, int32_t weight_layout,
-                          int32_t num_experts, int32_t hidden, int32_t intermediate,
-                          const uint8_t *act, const float *act_scales,
-                          const int32_t *sorted_ids, int32_t top_k, const int32_t *items,
-                          const int32_t *num_items, int32_t max_items, int32_t exact_routes,
-                          float *down, const void *weights, int32_t weights_dtype, uint16_t *out,
-                          int32_t *tickets, void *stream);
-
-/*
  * A10 + A11  FC2 with the SwiGLU requantisation done in its prologue.
  * Replaces Fish silu_mul_quant (src/drama3/kernels.py:344) followed by the
  * FC2 GEMM (kernels.py:304-318).  d3_expert_gemm mode 1 (down fp32 by pair,
@@ -494,49 +461,6 @@ int d3_decode_step_static(const uint8_t *w13, const float *s13, const uint8_t *w
                           int32_t logits_dtype, int64_t logits_stride, int32_t top_k,
                           int32_t exact_routes, int32_t *active, int32_t *count, uint16_t *out,
                           void *stream);
-
-/*
- * A1-A12  The whole decode MoE step in one launch.
- * Replaces DramaModel.routed_moe's decode path (src/drama3/model.py:520-583:
- * slot filter engine.py:637-647, route kernels.py:360-383, quantise
- * moe_input.py:24-27, small_batch_moe kernels.py:325-357 with the route sort
- * kernels.py:658-731, FC1 / silu_mul_quant / FC2 / combine kernels.py:290-322,
- * 344).  Same results as d3_moe_front + d3_expert_gemm (FC1) +
- * d3_silu_mul_quant + d3_expert_gemm (FC2) + d3_weighted_combine on the same
- * buffers (bit for bit, every intermediate included), in one kernel whose
- * expert-GEMM workgroups start streaming their weights before routing is
- * known; the route sort, the SwiGLU requant of an expert and the combine of
- * a token are done by the workgroup that completes their inputs.
- *   occupancy u8 [num_slots] -> active_slots int32 [num_slots] (ascending,
- *   -1 padded), *count = live rows; output row r (r < *count) of out
- *   bf16 [num_slots, hidden] belongs to slot active_slots[r].
- *   x bf16 [num_slots rows, x_row_stride], logits bf16 [num_slots rows,
- *   logits_row_stride] (slot-indexed); w13 / w2 in the fragment-major layout
- *   (d3_pack_expert_weights) with their block scales s13 / s2.
- *   ids, weights (route weights, bf16 or f32), q, x_scales, sorted_ids
- *   (max_rows >= d3_max_sorted_rows(num_slots * top_k, num_experts, 16)),
- *   gate_up, act, act_scales, down: the same buffers as the multi-kernel
- *   step, written with the same contents.
- *   sync: int32 [d3_moe_step_sync_ints(...)], 16-byte aligned, all zero
- *   before the first launch; every launch leaves it zero except sync[0],
- *   which becomes nonzero if a wait inside the kernel gave up (a launch that
- *   was not given the GPU to itself for ~1 s); the output is then invalid.
- * Launches on one sync buffer must not overlap.  Items of at most
- * exact_routes routes use the exact bf16-MFMA path (as d3_expert_gemm).
- * Supported: (hidden, intermediate) in {(1024, 256), (1024, 512),
- * (2048, 512), (2048, 768)}, num_experts <= 256, num_slots <= 256, bf16 logits.
- */
-int32_t d3_moe_step_sync_ints(int32_t num_slots, int32_t num_experts, int32_t hidden,
-                              int32_t intermediate);
-int d3_moe_decode_step(const uint8_t *occupancy, int32_t num_slots, int32_t *active_slots,
-                       int32_t *count, const uint16_t *x, int64_t x_row_stride,
-                       const uint16_t *logits, int64_t logits_row_stride, int32_t hidden,
-                       int32_t num_experts, int32_t intermediate, int32_t top_k,
-                       const uint8_t *w13, const float *s13, const uint8_t *w2, const float *s2,
-                       int32_t exact_routes, int32_t *ids, void *weights, int32_t weights_dtype,
-                       uint8_t *q, float *x_scales, int32_t *sorted_ids, int32_t max_rows,
-                       uint16_t *gate_up, uint8_t *act, float *act_scales, float *down,
-                       uint16_t *out, int32_t *sync, void *stream);
 
 /*
  * A10  SwiGLU + per-128 FP8 requantisation of FC1 rows.

@@ -122,10 +122,9 @@ def test_fused_front_row_mode_with_index(device, rows, experts, live, fused):
 
 
 @pytest.mark.parametrize("config", [1, 2, 3])
-def test_fused_epilogues_match_unfused_chain(device, config):
-    """FC1 + fused SwiGLU requant and FC2 + fused combine give exactly the
-    bytes of the four-kernel chain, and leave every ticket at 0; FC2 with the
-    SwiGLU requant in its prologue (three kernels) gives the same output."""
+def test_swiglu_prologue_matches_chain(device, config):
+    """FC2 with the SwiGLU requant in its prologue (three kernels) gives
+    exactly the bytes of the four-kernel chain."""
     from drama3_amd import workloads
     from drama3_amd.pipeline import MoEWorkspace, Shape
 
@@ -134,26 +133,17 @@ def test_fused_epilogues_match_unfused_chain(device, config):
     experts = w.experts.to(device)
     occ = step.occupancy.to(device)
     xs, ls = step.x_slots.to(device), step.logits_slots.to(device)
-    variants = {"chain": dict(swiglu_in_fc2=False), "fused": dict(fused_epilogues=True),
-                "prologue": dict(swiglu_in_fc2=True)}
     outs = {}
-    for name, options in variants.items():
-        ws = MoEWorkspace(Shape(64, w.num_experts, w.hidden, w.intermediate), device, **options)
+    for name in ("chain", "prologue"):
+        ws = MoEWorkspace(Shape(64, w.num_experts, w.hidden, w.intermediate), device,
+                          swiglu_in_fc2=name == "prologue")
         active = torch.empty(64, dtype=torch.int32, device=device)
         count = torch.empty(1, dtype=torch.int32, device=device)
-        for _ in range(2):  # second launch proves the tickets were reset
+        for _ in range(2):
             ws.front(xs, ls, occupancy=occ, active=active, count=count)
             out = ws.experts(experts, count)
         torch.cuda.synchronize()
         n = int(count.item())
-        total = int(ws.total.item())
-        valid = ws.sorted_ids.cpu().numpy()[:total] < n * 8
-        outs[name] = (out[:n].cpu(), np_u8(ws.act)[:total][valid], np_f32(ws.act_scales)[:total][valid])
-        if name == "fused":
-            assert ws.fuse_fc1 and ws.fuse_fc2 and not ws.swiglu_in_fc2
-            assert int(ws.fc1_tickets.abs().sum()) == 0 and int(ws.fc2_tickets.abs().sum()) == 0
+        outs[name] = out[:n].cpu()
         assert ws.swiglu_in_fc2 == (name == "prologue")
-    for name in ("fused", "prologue"):
-        assert torch.equal(outs[name][0], outs["chain"][0]), name
-    assert np.array_equal(outs["fused"][1], outs["chain"][1])
-    assert np.array_equal(outs["fused"][2], outs["chain"][2])
+    assert torch.equal(outs["prologue"], outs["chain"])
