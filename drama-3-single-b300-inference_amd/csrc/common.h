@@ -31,6 +31,19 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>((b & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
+// Two values rounded to bf16 by v_cvt_pk_bf16_f32 (round to nearest even),
+// `lo` in the low half.  d3_check_epilogue_arithmetic (selftest.hip) shows
+// it gives f32_to_bf16's bits for every non-NaN fp32 input in both halves.
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+typedef float floatx2_hw __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const floatx2_hw v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_hw));
+}
+// The two halves of a pack_bf16x2 word as fp32.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 // ---------------------------------------------------------------------------
 // OCP e4m3fn
 // ---------------------------------------------------------------------------
@@ -84,15 +97,33 @@ __device__ __forceinline__ uint32_t quantize_one(float x, float scale) {
   return f32_to_e4m3(v);
 }
 
+// x / s rounded to nearest even, given inv = 1.0f / s (IEEE): q0 = x * inv,
+// then one correction with the exact residual x - q0 * s (Markstein's
+// division step: with inv the correctly rounded reciprocal, q0 lies within
+// one ulp of x / s, the residual is exact and q0 + r * inv rounds to the
+// correctly rounded quotient).  copysign keeps the sign of a zero quotient
+// (x = -0).  Equal to the IEEE division for every quotient in the fp32
+// normal range; below it (|x / s| < 2^-126, an e4m3 zero either way) it may
+// differ in the last place.  d3_check_epilogue_arithmetic (selftest.hip)
+// compares the quantised codes with quantize_one's on the device.
+__device__ __forceinline__ float div_rn(float x, float s, float inv) {
+  const float q0 = x * inv;
+  const float r = fmaf(-q0, s, x);
+  return copysignf(fmaf(r, inv, q0), x);
+}
+
 // quantize_one of four values, packed little-endian (v[0] in the low byte).
-// The conversion is v_cvt_pk_fp8_f32 (round to nearest even into OCP e4m3),
-// which gives f32_to_e4m3's byte for every input in [-448, 448] in every
-// byte position: d3_check_e4m3_conversion (selftest.hip) compares the two
-// over all 2^32 fp32 bit patterns after the clamp.
+// The division is div_rn (one reciprocal per call: callers that quantise
+// several words with one scale share it after inlining).  The conversion is
+// v_cvt_pk_fp8_f32 (round to nearest even into OCP e4m3), which gives
+// f32_to_e4m3's byte for every input in [-448, 448] in every byte position:
+// d3_check_e4m3_conversion (selftest.hip) compares the two over all 2^32
+// fp32 bit patterns after the clamp.
 __device__ __forceinline__ uint32_t quantize_four(const float* v, float scale) {
+  const float inv = 1.0f / scale;
   float c[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) c[i] = fminf(fmaxf(v[i] / scale, -448.0f), 448.0f);
+  for (int i = 0; i < 4; ++i) c[i] = fminf(fmaxf(div_rn(v[i], scale, inv), -448.0f), 448.0f);
   int word = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
   word = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], word, true);
   return static_cast<uint32_t>(word);

@@ -109,28 +109,45 @@ __device__ __forceinline__ floatx4 mfma_block_bf16(int32x8 a, const bf16x8 b[4])
   return acc;
 }
 
+// 1 / d rounded to nearest even for d in [1, 2^126): the hardware
+// reciprocal (v_rcp_f32, within one ulp) and one Newton-Raphson correction
+// with the exact residual 1 - d * y (Markstein's reciprocal step).
+// d3_check_epilogue_arithmetic (selftest.hip) compares it with the IEEE
+// division 1.0f / d for every fp32 d in that range on the device.
+__device__ __forceinline__ float recip_rn(float d) {
+  const float y = __builtin_amdgcn_rcpf(d);
+  const float e = fmaf(-d, y, 1.0f);
+  return fmaf(e, y, y);
+}
+
 // SwiGLU of one bf16-rounded gate / up pair in fp32: a = (g * sigmoid(g)) * u
 // with sigmoid(g) = 1 / (1 + exp(-g)) in IEEE fp32 (the library expf, within
-// one ulp, and a correctly rounded division), the arithmetic of the
+// one ulp, and a correctly rounded reciprocal, recip_rn), the arithmetic of the
 // reference's in-repo SwiGLU (kernels.py:392-394) without its bf16 rounding
 // of silu(g).  Every kernel of this build that requantises FC1 outputs uses
 // this one function, so they agree bit for bit.
-__device__ __forceinline__ float swiglu_value(float g, float u) {
-  const float sig = 1.0f / (1.0f + expf(-g));
-  return (g * sig) * u;
+__device__ __forceinline__ float sigmoid_rn(float g) {
+  const float d = 1.0f + expf(-g);
+  float sig = recip_rn(d);
+  // d >= 2^126 (g < -87.3, the reciprocal subnormal or zero): the IEEE
+  // division, behind a wave-uniform branch that real data never takes.
+  const bool tiny = !(d < 0x1p126f);
+  if (__builtin_amdgcn_ballot_w64(tiny)) sig = tiny ? 1.0f / d : sig;
+  return sig;
 }
+__device__ __forceinline__ float swiglu_value(float g, float u) { return (g * sigmoid_rn(g)) * u; }
 
 // The reference's bf16 SwiGLU, silu_mul (kernels.py:392-394): silu(g)
 // rounded to bf16, times u; the caller rounds the product to bf16 as it
 // stores it.
 __device__ __forceinline__ float silu_mul_value(float g, float u) {
-  return bf16_to_f32(f32_to_bf16(g * (1.0f / (1.0f + expf(-g))))) * u;
+  return bf16_to_f32(f32_to_bf16(g * sigmoid_rn(g))) * u;
 }
 
 // SwiGLU + e4m3 requantisation of one 128-column group held by 16 lanes
 // (8 gate and 8 up bf16 values per lane): a = swiglu_value(g, u), scale =
-// max(amax, 1e-10) / 448, codes quantize_four(a, scale) (IEEE division by
-// the scale, the rule of moe_input.py:24-27).  Shared by the standalone
+// max(amax, 1e-10) / 448, codes quantize_four(a, scale) (the correctly
+// rounded division by the scale, the rule of moe_input.py:24-27).  Shared by the standalone
 // kernel, the FC2 prologues and the fused FC1 epilogue, so all give the
 // same bytes.
 __device__ __forceinline__ float swiglu_quant_group(uint4 graw, uint4 uraw, uint2* codes) {

@@ -286,12 +286,14 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
       for (int p = 0; p < 2; ++p)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float g = bf16_to_f32(f32_to_bf16(acc[p][rt][i]));
-          const float u = bf16_to_f32(f32_to_bf16(acc[2 + p][rt][i]));
-          const float a = swiglu_value(g, u);
-          v[rt][4 * p + i] = a;
-          amax = fmaxf(amax, fabsf(a));
+        for (int i = 0; i < 4; i += 2) {
+          const uint32_t gw = pack_bf16x2(acc[p][rt][i], acc[p][rt][i + 1]);
+          const uint32_t uw = pack_bf16x2(acc[2 + p][rt][i], acc[2 + p][rt][i + 1]);
+          const float a0 = swiglu_value(bf16_lo(gw), bf16_lo(uw));
+          const float a1 = swiglu_value(bf16_hi(gw), bf16_hi(uw));
+          v[rt][4 * p + i] = a0;
+          v[rt][4 * p + i + 1] = a1;
+          amax = fmaxf(amax, fmaxf(fabsf(a0), fabsf(a1)));
         }
       amax = fmaxf(amax, __shfl_xor(amax, 16));
       amax = fmaxf(amax, __shfl_xor(amax, 32));

@@ -1,4 +1,4 @@
-// Device self-check of the e4m3 conversion every quantiser relies on.
+// Device self-checks of the arithmetic every quantiser relies on.
 //
 // The quantisers (quantize_four in common.h: the MoE input, FC1 staging and
 // the SwiGLU requantisation) convert with v_cvt_pk_fp8_f32, which rounds to
@@ -7,7 +7,15 @@
 // f32_to_e4m3 byte (the rule torch's float8_e4m3fn cast implements) for
 // every clamped fp32 input and in every byte position of the packed word.
 // This kernel compares the two over a range of fp32 bit patterns.
+//
+// The SwiGLU requantisation also takes three shortcuts that must give the
+// IEEE results: pack_bf16x2 (hardware bf16 rounding), recip_rn (hardware
+// reciprocal + one Newton-Raphson step) inside sigmoid_rn, and div_rn
+// (reciprocal of the scale + one residual correction) inside quantize_four.
+// check_arithmetic_kernel compares each with its IEEE / software form over a
+// range of fp32 bit patterns.
 #include "common.h"
+#include "expert_tile.h"
 #include "status.h"
 
 namespace d3 {
@@ -17,13 +25,41 @@ constexpr int kCheckThreads = 256;
 
 __device__ __forceinline__ float clamp448(float v) { return fminf(fmaxf(v, -448.0f), 448.0f); }
 
+// Mismatch counting shared by the checks: per wave, per workgroup, then one
+// atomic add / min into result.
+__device__ void report_mismatches(uint32_t mismatches, uint32_t first_bad, uint32_t* result) {
+  __shared__ uint32_t bad_count[kCheckThreads / kWave];
+  __shared__ uint32_t bad_first[kCheckThreads / kWave];
+  const uint32_t wave_count = wave_reduce<SumU32>(mismatches);
+  uint32_t wave_first = first_bad;
+#pragma unroll
+  for (int offset = 32; offset >= 1; offset >>= 1)
+    wave_first = min(wave_first, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wave_first), offset)));
+  const int wave = threadIdx.x / kWave;
+  if (lane_id() == 0) {
+    bad_count[wave] = wave_count;
+    bad_first[wave] = wave_first;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t total = 0, least = 0xffffffffu;
+#pragma unroll
+    for (int w = 0; w < kCheckThreads / kWave; ++w) {
+      total += bad_count[w];
+      least = min(least, bad_first[w]);
+    }
+    if (total) {
+      atomicAdd(&result[0], total);
+      atomicMin(&result[1], least);
+    }
+  }
+}
+
 // Each thread takes groups of four consecutive patterns; each group is
 // converted four times, rotated so that every pattern lands in every byte
 // position of the packed word once.
 __global__ __launch_bounds__(kCheckThreads) void check_e4m3_kernel(uint64_t first, uint64_t groups,
                                                                    uint32_t* __restrict__ result) {
-  __shared__ uint32_t bad_count[kCheckThreads / kWave];
-  __shared__ uint32_t bad_first[kCheckThreads / kWave];
   uint32_t mismatches = 0;
   uint32_t first_bad = 0xffffffffu;
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kCheckThreads;
@@ -52,29 +88,56 @@ __global__ __launch_bounds__(kCheckThreads) void check_e4m3_kernel(uint64_t firs
       }
     }
   }
-  // per wave, then per workgroup, then one atomic each
-  const uint32_t wave_count = wave_reduce<SumU32>(mismatches);
-  uint32_t wave_first = first_bad;
+  report_mismatches(mismatches, first_bad, result);
+}
+
+// kind 0: pack_bf16x2 against f32_to_bf16 (NaN patterns skipped), pattern
+//   p in the low half next to p ^ 0x80000000 in the high half and the
+//   other way round;
+// kind 1: recip_rn(d) against 1.0f / d, d = pattern (inside [1, 2^126));
+// kind 2: the code and the quotient of div_rn(v, s, 1.0f / s) against
+//   v / s for v = +-pattern, s = scale (quotients from 2^-12 up compared
+//   bit for bit, smaller ones by their e4m3 code after the clamp);
+// kind 3: sigmoid_rn(g) against 1.0f / (1.0f + expf(-g)), g = pattern
+//   (NaN patterns skipped).
+__global__ __launch_bounds__(kCheckThreads) void check_arithmetic_kernel(int kind, uint64_t first, uint64_t count,
+                                                                         float scale, uint32_t* __restrict__ result) {
+  uint32_t mismatches = 0;
+  uint32_t first_bad = 0xffffffffu;
+  const float inv = 1.0f / scale;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kCheckThreads;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kCheckThreads + threadIdx.x; i < count; i += stride) {
+    const uint32_t p = static_cast<uint32_t>(first + i);
+    const float x = __uint_as_float(p);
+    bool bad = false;
+    if (kind == 0) {
+      if ((p & 0x7fffffffu) <= 0x7f800000u) {
+        const float y = __uint_as_float(p ^ 0x80000000u);
+        const uint32_t a = pack_bf16x2(x, y), b = pack_bf16x2(y, x);
+        const uint32_t want_x = f32_to_bf16(x), want_y = f32_to_bf16(y);
+        bad = (a & 0xffffu) != want_x || (a >> 16) != want_y || (b & 0xffffu) != want_y || (b >> 16) != want_x;
+      }
+    } else if (kind == 1) {
+      bad = __float_as_uint(recip_rn(x)) != __float_as_uint(1.0f / x);
+    } else if (kind == 2) {
 #pragma unroll
-  for (int offset = 32; offset >= 1; offset >>= 1) wave_first = min(wave_first, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wave_first), offset)));
-  const int wave = threadIdx.x / kWave;
-  if (lane_id() == 0) {
-    bad_count[wave] = wave_count;
-    bad_first[wave] = wave_first;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t total = 0, least = 0xffffffffu;
-#pragma unroll
-    for (int w = 0; w < kCheckThreads / kWave; ++w) {
-      total += bad_count[w];
-      least = min(least, bad_first[w]);
+      for (int sign = 0; sign < 2; ++sign) {
+        const float v = sign ? -x : x;
+        const float want = v / scale, got = div_rn(v, scale, inv);
+        const float cw = fminf(fmaxf(want, -448.0f), 448.0f), cg = fminf(fmaxf(got, -448.0f), 448.0f);
+        if (fabsf(want) >= 0x1p-12f) bad |= __float_as_uint(got) != __float_as_uint(want);
+        bad |= f32_to_e4m3(cw) != f32_to_e4m3(cg);
+      }
+    } else {
+      if ((p & 0x7fffffffu) <= 0x7f800000u)
+        bad = __float_as_uint(sigmoid_rn(x)) != __float_as_uint(1.0f / (1.0f + expf(-x)));
     }
-    if (total) {
-      atomicAdd(&result[0], total);
-      atomicMin(&result[1], least);
+    if (bad) {
+      ++mismatches;
+      first_bad = min(first_bad, p);
     }
   }
+  report_mismatches(mismatches, first_bad, result);
 }
 
 }  // namespace
@@ -96,4 +159,23 @@ extern "C" int d3_check_e4m3_conversion(uint64_t first, uint64_t count, uint32_t
   hipLaunchKernelGGL(check_e4m3_kernel, dim3(blocks), dim3(kCheckThreads), 0, as_stream(stream), first,
                      groups, result);
   D3_LAUNCHED("check_e4m3_conversion");
+}
+
+extern "C" int d3_check_epilogue_arithmetic(int32_t kind, uint64_t first, uint64_t count, float scale,
+                                            uint32_t* result, void* stream) {
+  D3_REQUIRE(result != nullptr, "check_epilogue_arithmetic: null result");
+  D3_REQUIRE(kind >= 0 && kind <= 3, "check_epilogue_arithmetic: kind must be 0-3");
+  D3_REQUIRE(first + count <= (uint64_t{1} << 32), "check_epilogue_arithmetic: range beyond 2^32");
+  D3_REQUIRE(kind != 1 || (first >= 0x3f800000u && first + count <= 0x7e800000u),
+             "check_epilogue_arithmetic: reciprocal inputs must lie in [1, 2^126)");
+  D3_REQUIRE(kind != 2 || (scale > 0.0f && first + count <= 0x7f800000u),
+             "check_epilogue_arithmetic: division needs a positive scale and finite patterns");
+  if (count == 0) {
+    clear_error();
+    return D3_OK;
+  }
+  const int blocks = static_cast<int>(std::min<uint64_t>((count + kCheckThreads - 1) / kCheckThreads, 8192));
+  hipLaunchKernelGGL(check_arithmetic_kernel, dim3(blocks), dim3(kCheckThreads), 0, as_stream(stream), kind,
+                     first, count, scale, result);
+  D3_LAUNCHED("check_epilogue_arithmetic");
 }

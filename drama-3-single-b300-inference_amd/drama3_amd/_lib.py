@@ -38,6 +38,7 @@ SIGNATURES = {
     "d3_abi_version": (_i32, []),
     "d3_last_error": (ctypes.c_char_p, []),
     "d3_check_e4m3_conversion": (_i32, [ctypes.c_uint64, ctypes.c_uint64, _p, _p]),
+    "d3_check_epilogue_arithmetic": (_i32, [_i32, ctypes.c_uint64, ctypes.c_uint64, _f32, _p, _p]),
     "d3_compact_slots": (_i32, [_p, _i32, _p, _p, _p]),
     "d3_route": (_i32, [_p, _i32, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _i32, _p]),
     "d3_quantize_rows": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p, _p, _i32, _p]),

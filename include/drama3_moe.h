@@ -61,6 +61,27 @@ extern "C" {
  */
 int d3_check_e4m3_conversion(uint64_t first, uint64_t count, uint32_t *result, void *stream);
 
+/*
+ * Device self-check of the arithmetic shortcuts of the SwiGLU requantisation
+ * (no counterpart in the reference: it shows that the shortcuts give the
+ * IEEE results the reference's rule moe_input.py:24-27 and silu
+ * (kernels.py:392-394) ask for).  Over the fp32 bit patterns
+ * [first, first + count):
+ *   kind 0: hardware bf16 rounding (v_cvt_pk_bf16_f32) against the software
+ *           round-to-nearest-even (NaN patterns skipped);
+ *   kind 1: hardware reciprocal + one Newton-Raphson step against 1.0f / d
+ *           (patterns inside [1, 2^126));
+ *   kind 2: division by `scale` through its reciprocal + one residual
+ *           correction against v / scale, for +v and -v (finite patterns):
+ *           quotients from 2^-12 up bit for bit, all by e4m3 code;
+ *   kind 3: the sigmoid 1 / (1 + expf(-g)) of the requantisation against
+ *           its IEEE form (NaN patterns skipped).
+ * result[0] += mismatches, result[1] = min(result[1], first bad pattern);
+ * the caller initialises result to {0, 0xffffffff}.
+ */
+int d3_check_epilogue_arithmetic(int32_t kind, uint64_t first, uint64_t count, float scale,
+                                 uint32_t *result, void *stream);
+
 /* Version of this ABI (bumped on any signature change). */
 int d3_abi_version(void);
 
