@@ -355,7 +355,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   int live_units = 0;
   // MODE 1: unit rows [base, base + kStageUnits) of route tile stage_m0.
   int stage_m0 = 0;
-  auto fetch_units = [&](int base) {
+  auto fetch_units = [&](int base) __attribute__((always_inline)) {
     if constexpr (MODE == 1) {
       const BufferView x_view(a.x, static_cast<uint32_t>(capacity * a.x_stride * 2));
 #pragma unroll
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   // Per-128 e4m3 quantisation of the staged units: the arithmetic and lane
   // layout of quantize_row_part, so the tile holds the front's q bytes and
   // scales.
-  auto quantize_units = [&](int base) {
+  auto quantize_units = [&](int base) __attribute__((always_inline)) {
     if constexpr (MODE == 1) {
 #pragma unroll
       for (int i = 0; i < kStageUnits; ++i) {
