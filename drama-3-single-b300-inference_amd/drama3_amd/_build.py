@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import concurrent.futures
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -47,11 +48,38 @@ def sources() -> list[Path]:
     return sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp")])
 
 
+# The compiler's per-kernel resource report; every kernel must run without
+# per-lane scratch (a register spill or an outlined call that the compiler
+# chose not to inline costs the hot loops several microseconds).
+RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"
+_FUNCTION = re.compile(r"remark: Function Name: (\S+)")
+_SCRATCH = re.compile(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)")
+
+
+def scratch_users(remarks: str) -> list[tuple[str, int]]:
+    """(function, bytes per lane) for every function the resource remarks
+    report with a nonzero scratch size."""
+    users, name = [], None
+    for line in remarks.splitlines():
+        m = _FUNCTION.search(line)
+        if m:
+            name = m.group(1)
+            continue
+        m = _SCRATCH.search(line)
+        if m and name is not None and int(m.group(1)) > 0:
+            users.append((name, int(m.group(1))))
+    return users
+
+
 def _compile(src: Path, obj: Path, extra: list[str]) -> None:
-    cmd = [hipcc(), *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, RESOURCE_REMARKS, *extra, "-c", str(src), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{result.stdout}\n{result.stderr}")
+    users = scratch_users(result.stderr)
+    if users:
+        listing = "\n".join(f"  {name}: {size} bytes/lane" for name, size in users)
+        raise RuntimeError(f"{src.name}: kernels use per-lane scratch (spills or outlined calls):\n{listing}")
 
 
 def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
