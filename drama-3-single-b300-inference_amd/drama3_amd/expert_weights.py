@@ -38,18 +38,31 @@ def pack_expert_weights(weight: torch.Tensor, stream=None) -> torch.Tensor:
     return packed
 
 
-def prepare_experts(experts, stream=None):
+def prepare_experts(experts, stream=None, keep_reference: bool = True):
     """Attach ``d3_w13_packed`` / ``d3_w2_packed`` (fragment-major codes) to an
     experts object; the MoE ops use them from then on.  Returns ``experts``.
 
     The packed copies are tied to the tensors they were made from (pointer,
     shape and version counter); ``fc1_operands``/``fc2_operands`` fall back
     to the checkpoint layout if the source weights were replaced or modified.
+
+    ``keep_reference=False`` keeps one copy of the codes: ``w13_weight`` /
+    ``w2_weight`` are replaced by their fragment-major copies (same shape and
+    dtype, half the expert bytes of keeping both).  The object then holds no
+    checkpoint-layout codes: anything that reads those tensors as checkpoint
+    rows (a CPU reference, a copy handed to other code) must not be given
+    it.  Calling ``prepare_experts`` again on such an object does nothing.
     """
     for name in ("w13", "w2"):
+        if getattr(experts, f"d3_{name}_fragment_only", False):
+            continue  # already holds only the fragment-major codes
         weight = getattr(experts, f"{name}_weight")
-        setattr(experts, f"d3_{name}_packed", pack_expert_weights(weight, stream))
-        setattr(experts, f"d3_{name}_source", _identity(weight))
+        packed = pack_expert_weights(weight, stream)
+        if not keep_reference:
+            setattr(experts, f"{name}_weight", packed)
+            setattr(experts, f"d3_{name}_fragment_only", True)
+        setattr(experts, f"d3_{name}_packed", packed)
+        setattr(experts, f"d3_{name}_source", _identity(packed if not keep_reference else weight))
     return experts
 
 

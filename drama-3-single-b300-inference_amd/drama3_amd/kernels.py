@@ -18,6 +18,25 @@ from .pipeline import WIDE_SORT_PAIRS, MoEWorkspace, Shape, dtype_code, require_
 
 TOP_K = 8
 
+# Workspaces of the eager entry points, reused across calls with the same
+# shape, options, device and current stream (calls on one stream run in
+# order, so they never share buffers concurrently); the oldest is dropped
+# past _MAX_WORKSPACES.  Outputs are always fresh tensors.
+_MAX_WORKSPACES = 16
+_workspaces: dict = {}
+
+
+def _workspace(shape: Shape, device: torch.device, **options) -> MoEWorkspace:
+    stream = torch.cuda.current_stream(device).cuda_stream if device.type == "cuda" else 0
+    key = (str(device), stream, shape.rows, shape.num_experts, shape.hidden, shape.intermediate,
+           shape.top_k, tuple(sorted(options.items())))
+    ws = _workspaces.get(key)
+    if ws is None:
+        if len(_workspaces) >= _MAX_WORKSPACES:
+            _workspaces.pop(next(iter(_workspaces)))
+        ws = _workspaces[key] = MoEWorkspace(shape, device, **options)
+    return ws
+
 
 def check_experts(experts, hidden: int | None = None):
     """``experts`` exposes w13_weight [E,2I,H] e4m3, w13_scale_inv [E,2I/128,H/128],
@@ -83,8 +102,8 @@ def _routed(x, topk_ids, topk_weights, experts, block_m: int = 16):
     out = torch.empty((rows, h), dtype=torch.bfloat16, device=x.device)
     if rows == 0:
         return out
-    ws = MoEWorkspace(Shape(rows, e, h, i, top_k), x.device, tile=block_m,
-                      item_rows=max(block_m, 128) if rows > 128 else None)
+    ws = _workspace(Shape(rows, e, h, i, top_k), x.device, tile=block_m,
+                    item_rows=max(block_m, 128) if rows > 128 else None)
     ids, weights = topk_ids.contiguous(), topk_weights.contiguous()
     if x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
@@ -279,6 +298,6 @@ def routed_moe(x, router, experts, decode=True, *, row_slots=None, padding_start
                                          padding_start=padding_start)
     if x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
-    ws = MoEWorkspace(Shape(rows, e, h, i, TOP_K), x.device,
-                      item_rows=128 if rows > 128 else None)
+    ws = _workspace(Shape(rows, e, h, i, TOP_K), x.device,
+                    item_rows=128 if rows > 128 else None)
     return ws.forward(x, logits, experts, out=out)

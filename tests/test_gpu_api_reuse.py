@@ -1,0 +1,57 @@
+"""Eager reference-API calls reuse one workspace per (shape, options,
+device, stream) and return fresh outputs; ``prepare_experts`` with
+``keep_reference=False`` keeps only the fragment-major codes and gives the
+same bytes as the two-layout object (decode, prefill-sized batch)."""
+
+import torch
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def test_native_moe_reuses_its_workspace_per_stream(device):
+    from drama3_amd import kernels, workloads
+    from drama3_amd.kernels import native_moe, route
+
+    w = workloads.config1()
+    x, logits = w.steps[0].packed()
+    experts = w.experts.to(device)
+    xd = x.to(device)
+    weights, ids = route(logits.to(device))
+    kernels._workspaces.clear()
+    a = native_moe(xd, ids, weights, experts, block_m=64)
+    b = native_moe(xd, ids, weights, experts, block_m=64)
+    assert len(kernels._workspaces) == 1
+    assert a.data_ptr() != b.data_ptr()
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        c = native_moe(xd, ids, weights, experts, block_m=64)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    assert len(kernels._workspaces) == 2  # another stream, another workspace
+    assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.parametrize("config", [2, 4])
+def test_fragment_only_experts_match_two_layouts(device, config):
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import LAYOUT_FRAGMENT, fc1_operands, fc2_operands, prepare_experts
+    from drama3_amd.kernels import routed_moe
+
+    w = workloads.CONFIGS[config]()
+    x, logits = w.steps[0].packed()
+    rows = min(len(x), 1024)
+    xd, ld = x[:rows].to(device), logits[:rows].to(device)
+    both = prepare_experts(w.experts.to(device))
+    single = prepare_experts(w.experts.to(device), keep_reference=False)
+    w13 = single.w13_weight
+    prepare_experts(single)  # a second call keeps the single copy as it is
+    assert single.w13_weight is w13
+    assert fc1_operands(single)[2] == LAYOUT_FRAGMENT and fc2_operands(single)[2] == LAYOUT_FRAGMENT
+    assert torch.equal(single.w13_weight, both.d3_w13_packed)
+    assert torch.equal(single.w2_weight, both.d3_w2_packed)
+    got = routed_moe(xd, ld, single, True)
+    want = routed_moe(xd, ld, both, True)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
