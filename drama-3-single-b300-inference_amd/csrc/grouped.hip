@@ -54,6 +54,11 @@ constexpr int kGgStride = kGroup + 16;             // LDS bytes per staged route
 constexpr int kGgStage = kGgRoutes * kGgStride;
 constexpr int kGgStaged = kGgRoutes * kGroup / (16 * kGgThreads);  // 16-byte copies per thread and K block
 constexpr int kGgXcds = 8;
+// Routes found by the workgroups themselves (by-pair launches): at most this
+// many (row, rank) pairs, read in chunks of one id per thread.
+constexpr int kGgMaxPairChunks = 32;
+constexpr int kGgMaxPairs = kGgMaxPairChunks * kGgThreads;  // 8192
+static_assert(kGgMaxPairChunks * kGgWaves == 2 * kWave, "one wave scans the (chunk, wave) counts, two per lane");
 
 // A dense shared expert folded into the routed launch: items after the
 // routed ones cover its rows [128 j, 128 j + 128) with identity routes and
@@ -67,18 +72,28 @@ struct SharedItems {
   int pair;
 };
 
-template <int KB, int MODE, bool kPacked>
+// kByPair (small batches): no sorted route list.  Work item i is part i % parts (routes
+// [128 part, 128 part + 128) in pair order) of expert i / parts; the
+// workgroup finds those routes itself in `sorted_ids`, which then holds the
+// routed expert of every (row, rank) pair, the live row count being
+// *num_items.  FC1 writes act rows by pair and FC2 reads them by pair, so
+// both match the sorted launches value for value.
+template <int KB, int MODE, bool kPacked, bool kByPair>
 __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2))) void grouped_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows, int out_cols,
     const uint8_t* __restrict__ act, uint32_t act_bytes, const float* __restrict__ act_scales,
     const int32_t* __restrict__ sorted_ids, int top_k, const int4* __restrict__ items,
     const int32_t* __restrict__ num_items, int max_items, SharedItems shared, int n_tiles, int chunk,
-    uint8_t* __restrict__ out_codes, float* __restrict__ out_scales, float* __restrict__ out_f32) {
+    int parts, int capacity, uint8_t* __restrict__ out_codes, float* __restrict__ out_scales,
+    float* __restrict__ out_f32) {
   constexpr int K = KB * kGroup;
   __shared__ __attribute__((aligned(16))) uint8_t stage[2][kGgStage];
   __shared__ float a_scale[KB][kGgRoutes];
-  __shared__ int target[kGgRoutes];  // FC1: sorted position, FC2: pair; -1 = no route
+  __shared__ int target[kGgRoutes];  // FC1: sorted position (by pair: the pair), FC2: pair; -1 = no route
   __shared__ float amax_part[MODE == 0 ? kGgWaves : 1][kGgRoutes];
+  __shared__ int route_pair[kByPair ? kGgRoutes : 1];
+  __shared__ uint64_t chunk_masks[kByPair ? kGgMaxPairChunks * kGgWaves : 1];
+  __shared__ int chunk_base[kByPair ? kGgMaxPairChunks * kGgWaves + 1 : 1];
 
   // XCD-aware order: workgroup b runs on XCD b % 8; logical index L gives
   // each XCD runs of `chunk` consecutive (item, tile) pairs.
@@ -88,8 +103,11 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   const int item_index = logical / n_tiles;
   const int tile = logical % n_tiles;
   const bool dense = item_index >= max_items;  // a shared-expert item (uniform)
-  int expert = 0, first, routes;
-  if (!dense) {
+  int expert = 0, first = 0, routes = 0;
+  if constexpr (kByPair) {
+    if (item_index >= max_items) return;
+    expert = item_index / parts;
+  } else if (!dense) {
     if (item_index >= *num_items) return;
     const int4 item = items[item_index];
     expert = item.x;
@@ -147,11 +165,67 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   };
   load_weights(0);  // depends on the item only
 
+  if constexpr (kByPair) {
+    // The expert's routes in pair order: pair p = 256 j + thread.  Each
+    // wave's ballot of chunk j goes to LDS; one wave turns their counts into
+    // exclusive bases (in pair order: chunk, then wave); each thread then
+    // ranks only its own matches (a few of its 32 chunks).
+    const int part_first = (item_index % parts) * kGgRoutes;
+    const int live_rows = min(*num_items, capacity);
+    const int pairs = live_rows * top_k;
+    const BufferView id_view(sorted_ids, static_cast<uint32_t>(capacity * top_k) * 4);
+    const int my_wave = static_cast<int>(threadIdx.x) / kWave;
+    uint32_t mine = 0;  // bit j: this thread's pair of chunk j routes to the expert
+    {
+      int idv[kGgMaxPairChunks];
+#pragma unroll
+      for (int j = 0; j < kGgMaxPairChunks; ++j) {
+        const int p = j * kGgThreads + static_cast<int>(threadIdx.x);
+        idv[j] = p < pairs ? static_cast<int>(id_view.load4(static_cast<uint32_t>(p) * 4)) : -1;
+      }
+#pragma unroll
+      for (int j = 0; j < kGgMaxPairChunks; ++j) {
+        mine |= (idv[j] == expert ? 1u : 0u) << j;
+        const uint64_t hits = __ballot(idv[j] == expert);
+        if (lane_id() == 0) chunk_masks[j * kGgWaves + my_wave] = hits;
+      }
+    }
+    __syncthreads();
+    if (my_wave == 0) {
+      // exclusive scan of the 128 (chunk, wave) counts: two per lane
+      constexpr int kCells = kGgMaxPairChunks * kGgWaves;
+      const int c0 = __popcll(chunk_masks[2 * lane_id()]);
+      const int c1 = __popcll(chunk_masks[2 * lane_id() + 1]);
+      int incl = c0 + c1;
+#pragma unroll
+      for (int offset = 1; offset < kWave; offset <<= 1) {
+        const int up = __shfl_up(incl, offset);
+        if (lane_id() >= offset) incl += up;
+      }
+      const int excl = incl - c0 - c1;
+      chunk_base[2 * lane_id()] = excl;
+      chunk_base[2 * lane_id() + 1] = excl + c0;
+      if (lane_id() == kWave - 1) chunk_base[kCells] = incl;
+    }
+    __syncthreads();
+    for (uint32_t m = mine; m != 0; m &= m - 1) {
+      const int j = __builtin_ctz(m);
+      const int cell = j * kGgWaves + my_wave;
+      const int r = chunk_base[cell] + __popcll(chunk_masks[cell] & lanemask_lt()) - part_first;
+      if (r >= 0 && r < kGgRoutes) route_pair[r] = j * kGgThreads + static_cast<int>(threadIdx.x);
+    }
+    const int base = chunk_base[kGgMaxPairChunks * kGgWaves];
+    routes = __builtin_amdgcn_readfirstlane(min(max(base - part_first, 0), kGgRoutes));
+    if (routes == 0) return;  // uniform: this part of the expert is empty
+    __syncthreads();
+  }
+
   // Route rows of the item, loaded branch-free (a dead route reads the
   // item's first id and is masked afterwards): one round trip.  Shared-expert
   // items map row r of the item to token first + r.
   auto route_row = [&](int r, int id) {
     if (dense) return MODE == 0 ? first + r : shared.pos + first + r;
+    if constexpr (kByPair) return MODE == 0 ? id / top_k : id;
     return MODE == 0 ? id / top_k : first + r;
   };
   const int part = tid & 7;
@@ -160,11 +234,15 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
   for (int i = 0; i < kGgStaged; ++i) {
     const int r = r0 + (kGgThreads / 8) * i;
-    ids[i] = dense ? 0 : sorted_ids[first + (r < routes ? r : 0)];
+    if constexpr (kByPair)
+      ids[i] = route_pair[r < routes ? r : 0];
+    else
+      ids[i] = dense ? 0 : sorted_ids[first + (r < routes ? r : 0)];
   }
   const int rs = tid % kGgRoutes;       // route of this thread's scales / target
   const int k0 = tid / kGgRoutes;       // first K block of its scales
-  const int id_s = dense ? 0 : sorted_ids[first + (rs < routes ? rs : 0)];
+  const int id_s = kByPair ? route_pair[rs < routes ? rs : 0]
+                           : (dense ? 0 : sorted_ids[first + (rs < routes ? rs : 0)]);
 
   // Staging: thread t copies 16 bytes (chunk t % 8 of the K block) of routes
   // t / 8 + 32 i.  Dead routes read past the buffer (zeros).
@@ -198,7 +276,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     for (int q = 0; q * kSplit + k0 < KB; ++q) sc[q] = srow[q * kSplit + k0];
 #pragma unroll
     for (int q = 0; q * kSplit + k0 < KB; ++q) a_scale[q * kSplit + k0][rs] = live ? sc[q] : 0.0f;
-    int t = MODE == 0 ? first + rs : id_s;
+    int t = MODE == 0 && !kByPair ? first + rs : id_s;
     if (dense) t = (MODE == 0 ? shared.pos : shared.pair) + first + rs;
     if (k0 == 0) target[rs] = live ? t : -1;
   }
@@ -338,6 +416,8 @@ struct GroupedLaunch {
   uint8_t* codes;
   float* scales;
   float* out;
+  int parts = 0;     // by-pair launches: work items per expert (0: sorted items)
+  int capacity = 0;  // by-pair launches: slot rows of the ids
 };
 
 template <int KB, int MODE>
@@ -351,11 +431,17 @@ void launch_grouped(const GroupedLaunch& g, hipStream_t s) {
   const int blocks = static_cast<int>((logical + per_round - 1) / per_round * per_round);
 #define D3_GG_ARGS dim3(blocks), dim3(kGgThreads), 0, s, g.w, g.ws, g.n_rows, g.out_cols, g.a, \
                    g.a_bytes, g.as, g.sorted_ids, g.top_k, g.items, g.num_items, g.max_items, \
-                   g.shared, n_tiles, chunk, g.codes, g.scales, g.out
-  if (g.layout == D3_LAYOUT_FRAGMENT)
-    hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true>), D3_GG_ARGS);
-  else
-    hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, false>), D3_GG_ARGS);
+                   g.shared, n_tiles, chunk, g.parts, g.capacity, g.codes, g.scales, g.out
+  if (g.parts > 0) {
+    if (g.layout == D3_LAYOUT_FRAGMENT)
+      hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true, true>), D3_GG_ARGS);
+    else
+      hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, false, true>), D3_GG_ARGS);
+  } else if (g.layout == D3_LAYOUT_FRAGMENT) {
+    hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true, false>), D3_GG_ARGS);
+  } else {
+    hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, false, false>), D3_GG_ARGS);
+  }
 #undef D3_GG_ARGS
 }
 
@@ -375,8 +461,9 @@ int dispatch_grouped(const GroupedLaunch& g, int k, hipStream_t s) {
 
 bool aligned_to(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
-int check_grouped(const GroupedLaunch& g, int num_experts, int k, int64_t a_rows, const char* name) {
-  D3_REQUIRE(g.w && g.ws && g.a && g.as && g.sorted_ids && g.items && g.num_items,
+int check_grouped(const GroupedLaunch& g, int num_experts, int k, int64_t a_rows, const char* name,
+                  bool need_items = true) {
+  D3_REQUIRE(g.w && g.ws && g.a && g.as && g.sorted_ids && (g.items || !need_items) && g.num_items,
              "%s: null pointer", name);
   D3_REQUIRE(g.layout == D3_LAYOUT_REFERENCE || g.layout == D3_LAYOUT_FRAGMENT,
              "%s: weight_layout must be D3_LAYOUT_REFERENCE or D3_LAYOUT_FRAGMENT", name);
@@ -459,4 +546,66 @@ extern "C" int d3_grouped_fc2(const uint8_t* w2, const float* s2, int32_t weight
   status = dispatch_grouped<1>(g, intermediate, as_stream(stream));
   if (status != D3_OK) return status;
   D3_LAUNCHED("grouped_fc2");
+}
+
+extern "C" int d3_grouped_fc1_swiglu_by_pair(const uint8_t* w13, const float* s13,
+                                             int32_t weight_layout, int32_t num_experts,
+                                             int32_t intermediate, int32_t hidden,
+                                             const uint8_t* q, int64_t q_rows,
+                                             const float* x_scales, const int32_t* ids,
+                                             int32_t top_k, const int32_t* row_count,
+                                             int32_t capacity, uint8_t* act, float* act_scales,
+                                             void* stream) {
+  D3_REQUIRE(act && act_scales && ids && row_count, "grouped_fc1_swiglu_by_pair: null pointer");
+  D3_REQUIRE(intermediate > 0 && intermediate % kGroup == 0,
+             "grouped_fc1_swiglu_by_pair: intermediate %d must be a multiple of 128", intermediate);
+  D3_REQUIRE(capacity >= 1 && capacity <= q_rows, "grouped_fc1_swiglu_by_pair: capacity %d not in [1, %lld]",
+             capacity, static_cast<long long>(q_rows));
+  D3_SUPPORTED(static_cast<int64_t>(capacity) * top_k <= kGgMaxPairs,
+               "grouped_fc1_swiglu_by_pair: capacity %d x top_k %d above %d routes", capacity, top_k,
+               kGgMaxPairs);
+  D3_REQUIRE(aligned_to(act, 4), "grouped_fc1_swiglu_by_pair: act must be 4-byte aligned");
+  const int parts = (capacity + kGgRoutes - 1) / kGgRoutes;
+  GroupedLaunch g{0, weight_layout, w13, s13, 2 * intermediate, intermediate, q,
+                  static_cast<uint32_t>(q_rows * hidden), x_scales, ids, top_k, nullptr, row_count,
+                  num_experts * parts, kGgRoutes, SharedItems{nullptr, nullptr, 0, 0, 0}, act,
+                  act_scales, nullptr};
+  g.parts = parts;
+  g.capacity = capacity;
+  int status = check_grouped(g, num_experts, hidden, q_rows, "grouped_fc1_swiglu_by_pair",
+                             /*need_items=*/false);
+  if (status != D3_OK) return status;
+  status = dispatch_grouped<0>(g, hidden, as_stream(stream));
+  if (status != D3_OK) return status;
+  D3_LAUNCHED("grouped_fc1_swiglu_by_pair");
+}
+
+extern "C" int d3_grouped_fc2_by_pair(const uint8_t* w2, const float* s2, int32_t weight_layout,
+                                      int32_t num_experts, int32_t hidden, int32_t intermediate,
+                                      const uint8_t* act, const float* act_scales,
+                                      const int32_t* ids, int32_t top_k,
+                                      const int32_t* row_count, int32_t capacity, float* down,
+                                      void* stream) {
+  D3_REQUIRE(down && ids && row_count, "grouped_fc2_by_pair: null pointer");
+  D3_SUPPORTED(hidden > 0 && hidden % kGgRows == 0, "grouped_fc2_by_pair: hidden %d must be a multiple of %d",
+               hidden, kGgRows);
+  D3_REQUIRE(capacity >= 1 && top_k >= 1, "grouped_fc2_by_pair: capacity %d, top_k %d", capacity, top_k);
+  D3_SUPPORTED(static_cast<int64_t>(capacity) * top_k <= kGgMaxPairs,
+               "grouped_fc2_by_pair: capacity %d x top_k %d above %d routes", capacity, top_k,
+               kGgMaxPairs);
+  D3_REQUIRE(aligned_to(down, 16), "grouped_fc2_by_pair: down must be 16-byte aligned");
+  const int parts = (capacity + kGgRoutes - 1) / kGgRoutes;
+  const int64_t act_rows = static_cast<int64_t>(capacity) * top_k;
+  GroupedLaunch g{1, weight_layout, w2, s2, hidden, hidden, act,
+                  static_cast<uint32_t>(act_rows * intermediate), act_scales, ids, top_k, nullptr,
+                  row_count, num_experts * parts, kGgRoutes, SharedItems{nullptr, nullptr, 0, 0, 0},
+                  nullptr, nullptr, down};
+  g.parts = parts;
+  g.capacity = capacity;
+  int status = check_grouped(g, num_experts, intermediate, act_rows, "grouped_fc2_by_pair",
+                             /*need_items=*/false);
+  if (status != D3_OK) return status;
+  status = dispatch_grouped<1>(g, intermediate, as_stream(stream));
+  if (status != D3_OK) return status;
+  D3_LAUNCHED("grouped_fc2_by_pair");
 }

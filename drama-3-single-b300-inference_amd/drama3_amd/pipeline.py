@@ -44,6 +44,7 @@ EXACT_ROUTES = 64
 GROUPED_K = (256, 512, 768, 1024, 1536, 2048)
 GROUPED_ROUTES = 128  # most routes per work item of the tiled grouped GEMMs
 GROUPED_ITEM_ROUTES = 128  # their default item size
+BY_PAIR_MAX_PAIRS = 8192  # most (row, rank) pairs of the grouped GEMMs without a sort
 # Up to this many (row, rank) pairs the route sort can run inside the fused
 # front kernel (its last workgroup; opt-in, MoEWorkspace(fused_sort=True));
 # otherwise the 1024-thread sort kernel follows the front, and from
@@ -109,7 +110,8 @@ class MoEWorkspace:
                  item_rows: int | None = None, weights_dtype: torch.dtype = torch.bfloat16,
                  exact_routes: int = EXACT_ROUTES,
                  swiglu_in_fc2: bool | None = None, sortless: bool = False,
-                 grouped: bool | None = None, shared_rows: int = 0, fused_sort: bool = False):
+                 grouped: bool | None = None, shared_rows: int = 0, fused_sort: bool = False,
+                 by_pair: bool = False):
         lib = _lib.load()
         self.shape = shape
         # front(): sort in the front launch's last workgroup (256 threads)
@@ -179,6 +181,14 @@ class MoEWorkspace:
             raise ValueError(f"tiled grouped GEMMs need item_rows <= {GROUPED_ROUTES}, hidden and "
                              f"intermediate in {GROUPED_K}, hidden % 256 == 0")
         self.grouped = bool(grouped) and not sortless
+        # Grouped GEMMs without the route sort (small batches): the front
+        # launch skips the sort and the GEMM workgroups find their routes in
+        # `ids`; act / down rows by pair.
+        if by_pair and not (self.grouped and shared_rows == 0 and pairs <= BY_PAIR_MAX_PAIRS):
+            raise ValueError(f"by_pair needs the grouped GEMMs, no folded shared expert and "
+                             f"<= {BY_PAIR_MAX_PAIRS} (row, rank) pairs")
+        self.by_pair = bool(by_pair)
+        self.rows_dev = torch.full((1,), t, **i32)  # the live row count when none is given
         # Scratch of the wide route sort (prefill-sized batches).
         self.wide_sort = pairs > WIDE_SORT_PAIRS
         self.sort_scratch = torch.empty(
@@ -234,7 +244,7 @@ class MoEWorkspace:
              ptr(row_count), s.hidden, s.num_experts, s.top_k, ptr(self.ids), ptr(self.weights),
              dtype_code(self.weights.dtype), ptr(self.q), ptr(self.x_scales), self.tile,
              self.item_rows, *sort_args, stream)
-        if not fused and not self.sortless:
+        if not fused and not self.sortless and not self.by_pair:
             self.sort(None, count if occupancy is not None else row_count, stream)
 
     def fc1(self, experts, stream=None) -> None:
@@ -279,6 +289,25 @@ class MoEWorkspace:
              ptr(self.sorted_ids), s.top_k, ptr(self.items), ptr(self.num_items), self.max_items,
              self.item_rows, ptr(sw), ptr(sws), srows, self.max_rows, s.pairs, ptr(self.down),
              stream)
+
+    def grouped_fc1_by_pair(self, experts, row_count=None, stream=None) -> None:
+        """Grouped FC1 + SwiGLU requant without a sorted route list: act /
+        act_scales by pair."""
+        s, stream = self.shape, self._stream(stream)
+        w, ws, layout = fc1_operands(experts)
+        count = self.rows_dev if row_count is None else row_count
+        call("d3_grouped_fc1_swiglu_by_pair", ptr(w), ptr(ws), layout, s.num_experts,
+             s.intermediate, s.hidden, ptr(self.q), s.rows, ptr(self.x_scales), ptr(self.ids),
+             s.top_k, ptr(count), s.rows, ptr(self.act), ptr(self.act_scales), stream)
+
+    def grouped_fc2_by_pair(self, experts, row_count=None, stream=None) -> None:
+        """Grouped FC2 reading act by pair: fp32 down rows by pair."""
+        s, stream = self.shape, self._stream(stream)
+        w, ws, layout = fc2_operands(experts)
+        count = self.rows_dev if row_count is None else row_count
+        call("d3_grouped_fc2_by_pair", ptr(w), ptr(ws), layout, s.num_experts, s.hidden,
+             s.intermediate, ptr(self.act), ptr(self.act_scales), ptr(self.ids), s.top_k,
+             ptr(count), s.rows, ptr(self.down), stream)
 
     @property
     def shared_down(self) -> torch.Tensor:
@@ -424,6 +453,9 @@ class MoEWorkspace:
         if self.sortless:
             self.decode_fc1(experts, row_count, stream)
             self.decode_fc2(experts, row_count, stream)
+        elif self.by_pair:
+            self.grouped_fc1_by_pair(experts, row_count, stream)
+            self.grouped_fc2_by_pair(experts, row_count, stream)
         elif self.grouped:
             self.grouped_fc1(experts, stream=stream)
             self.grouped_fc2(experts, stream=stream)

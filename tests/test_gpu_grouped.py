@@ -212,3 +212,37 @@ def test_shared_expert_on_side_stream_and_folded_graph_replays(device):
     shared_expected = om.dense_ffn(np_bf16(x), so.w13[0], so.s13[0], so.w2[0], so.s2[0])
     stats = assert_bf16_close(np_bf16(out), om.add_shared(routed, shared_expected), **CONTRACTION)
     print(f"side-stream shared expert: {stats}")
+
+
+@pytest.mark.parametrize("shape", [(560, 16, 1024, 256), (300, 8, 512, 512), (1024, 128, 2048, 768),
+                                   (37, 8, 256, 1536)],
+                         ids=["c5_shapes", "h512_i512", "c4_model_1024_rows", "tiny"])
+def test_grouped_by_pair_matches_sorted(device, shape):
+    """The grouped GEMMs that find their own routes (no sort) give the sorted
+    launches' values: act codes and scales of every live pair (by pair
+    against by sorted position) and the fp32 down rows, byte for byte; a
+    live row count below the capacity leaves the rows past it untouched."""
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.pipeline import MoEWorkspace, Shape
+
+    rows, e, h, i = shape
+    w, x, logits = _workload(rows, e, h, i, seed=23)
+    experts = prepare_experts(w.to(device))
+    sorted_ws = MoEWorkspace(Shape(rows, e, h, i), device, item_rows=128, grouped=True)
+    pair_ws = MoEWorkspace(Shape(rows, e, h, i), device, item_rows=128, grouped=True, by_pair=True)
+    live_rows = torch.tensor([rows - rows // 5], dtype=torch.int32, device=device)
+    for ws in (sorted_ws, pair_ws):
+        ws.front(x.to(device), logits.to(device), row_count=live_rows)
+        ws.down.fill_(7.0)
+        ws.routes_down(experts, live_rows)
+    torch.cuda.synchronize()
+    live_pairs = int(live_rows.item()) * 8
+    inverse = sorted_ws.inverse[:live_pairs].long()
+    live = int(live_rows.item())
+    assert torch.equal(pair_ws.ids[:live], sorted_ws.ids[:live])
+    assert torch.equal(pair_ws.act[:live_pairs], sorted_ws.act[inverse])
+    assert torch.equal(pair_ws.act_scales[:live_pairs].view(torch.int32),
+                       sorted_ws.act_scales[inverse].view(torch.int32))
+    assert torch.equal(pair_ws.down[:live_pairs].view(torch.int32),
+                       sorted_ws.down[:live_pairs].view(torch.int32))
+    assert bool((pair_ws.down[live_pairs:] == 7.0).all())
