@@ -14,7 +14,8 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr
-from .pipeline import WIDE_SORT_PAIRS, MoEWorkspace, Shape, dtype_code, require_cuda
+from .pipeline import (WIDE_SORT_PAIRS, MoEWorkspace, Shape, by_pair_suited, dtype_code,
+                       grouped_supported, require_cuda)
 
 TOP_K = 8
 
@@ -298,6 +299,7 @@ def routed_moe(x, router, experts, decode=True, *, row_slots=None, padding_start
                                          padding_start=padding_start)
     if x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
+    by_pair = by_pair_suited(rows, e, TOP_K) and grouped_supported(h, i)
     ws = _workspace(Shape(rows, e, h, i, TOP_K), x.device,
-                    item_rows=128 if rows > 128 else None)
+                    item_rows=128 if rows > 128 else None, by_pair=by_pair)
     return ws.forward(x, logits, experts, out=out)

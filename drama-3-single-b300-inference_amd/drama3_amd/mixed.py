@@ -20,7 +20,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr
-from .pipeline import BY_PAIR_MAX_PAIRS, MoEWorkspace, Shape, grouped_supported, require_cuda
+from .pipeline import MoEWorkspace, Shape, by_pair_suited, grouped_supported, require_cuda
 
 MAX_REUSE_PROMPTS = 16
 MAX_REUSE_ROWS = 8192
@@ -147,7 +147,7 @@ class MixedStep:
         self.out = torch.empty((full, hidden), **bf16)
         # The grouped GEMMs find their own routes (no per-layer sort launch)
         # whenever the step's rows allow it.
-        by_pair = full > 128 and full * top_k <= BY_PAIR_MAX_PAIRS and grouped_supported(hidden, intermediate)
+        by_pair = by_pair_suited(full, num_experts, top_k) and grouped_supported(hidden, intermediate)
         self.workspace = MoEWorkspace(Shape(full, num_experts, hidden, intermediate, top_k), dev,
                                       item_rows=128 if full > 128 else None, by_pair=by_pair)
         self.graph: torch.cuda.CUDAGraph | None = None

@@ -75,6 +75,15 @@ def require_cuda(*tensors: torch.Tensor | None) -> None:
             raise ValueError("MI355X MoE operators need device tensors (no CPU fallback)")
 
 
+def by_pair_suited(rows: int, num_experts: int, top_k: int = 8) -> bool:
+    """Whether the grouped GEMMs without a route sort suit a batch: at most
+    BY_PAIR_MAX_PAIRS (row, rank) pairs, and a grid of at most 128 (expert,
+    128-route part) items, since every item's workgroups read all the ids
+    before they know whether their part holds routes."""
+    parts = -(-rows // 128)
+    return rows > 128 and rows * top_k <= BY_PAIR_MAX_PAIRS and num_experts * parts <= 128
+
+
 def default_item_rows(rows: int, tile: int = SORT_TILE, num_experts: int | None = None,
                       top_k: int = 8) -> int:
     """Routes per work item (a multiple of ``tile``).  Up to 128 rows an

@@ -55,3 +55,27 @@ def test_fragment_only_experts_match_two_layouts(device, config):
     want = routed_moe(xd, ld, both, True)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_routed_moe_small_batch_without_sort_matches_sorted(device):
+    """routed_moe at 560 rows over 16 experts takes the grouped GEMMs that
+    find their own routes (no sort); the output equals the sorted chain's."""
+    from drama3_amd import kernels, workloads
+    from drama3_amd.kernels import routed_moe
+    from drama3_amd.pipeline import MoEWorkspace, Shape
+
+    w = workloads.config5()
+    x, logits = w.steps[0].packed()
+    rows = 560
+    xd, ld = x[:rows].to(device), logits[:rows].to(device)
+    experts = w.experts.to(device)
+    kernels._workspaces.clear()
+    got = routed_moe(xd, ld, experts, True)
+    ws = next(iter(kernels._workspaces.values()))
+    assert ws.by_pair and ws.grouped
+    sorted_ws = MoEWorkspace(Shape(rows, w.num_experts, w.hidden, w.intermediate), device,
+                             item_rows=128)
+    assert sorted_ws.grouped and not sorted_ws.by_pair
+    want = sorted_ws.forward(xd, ld, experts, out=torch.empty_like(got))
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
