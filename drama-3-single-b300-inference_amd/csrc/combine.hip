@@ -323,8 +323,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
     float g[4], u[4], v[4];
     load4(in + column, g);
     load4(in + width + column, u);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = silu_mul_value(g[i], u[i]);
+    silu_mul_values<4>(g, u, v);
     store4(out + static_cast<int64_t>(row) * width + column, v);
   }
 }

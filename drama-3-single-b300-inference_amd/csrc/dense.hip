@@ -160,10 +160,10 @@ __global__ __launch_bounds__(kDenseThreads) void dense_bf16_kernel(DenseArgs a) 
       if (r_tile == 1) up_sum[t_tile][lane] = floatx4{rounded[0], rounded[1], rounded[2], rounded[3]};
       __syncthreads();
       if (r_tile == 0 && token < a.rows) {
-        const floatx4 up = up_sum[t_tile][lane];
+        const floatx4 up4 = up_sum[t_tile][lane];
+        const float up[4] = {up4[0], up4[1], up4[2], up4[3]};
         float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = silu_mul_value(rounded[i], up[i]);
+        silu_mul_values<4>(rounded, up, v);
         const uint32_t lo = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
         const uint32_t hi = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
         *reinterpret_cast<uint2*>(a.act + static_cast<int64_t>(token) * a.act_stride + t0 * 16 + 4 * quarter) =

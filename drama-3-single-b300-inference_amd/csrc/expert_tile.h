@@ -120,28 +120,55 @@ __device__ __forceinline__ float recip_rn(float d) {
   return fmaf(e, y, y);
 }
 
-// SwiGLU of one bf16-rounded gate / up pair in fp32: a = (g * sigmoid(g)) * u
+// SwiGLU of bf16-rounded gate / up pairs in fp32: a = (g * sigmoid(g)) * u
 // with sigmoid(g) = 1 / (1 + exp(-g)) in IEEE fp32 (the library expf, within
 // one ulp, and a correctly rounded reciprocal, recip_rn), the arithmetic of the
 // reference's in-repo SwiGLU (kernels.py:392-394) without its bf16 rounding
 // of silu(g).  Every kernel of this build that requantises FC1 outputs uses
-// this one function, so they agree bit for bit.
+// these functions, so they agree bit for bit.
+//
+// N values at once: d >= 2^126 (g < -87.3, the reciprocal subnormal or
+// zero) takes the IEEE division, behind one wave-uniform branch for all N
+// values that real data never takes, so the common path is straight-line
+// code whose N exponentials and reciprocals the compiler can interleave.
+template <int N>
+__device__ __forceinline__ void sigmoid_rn_n(const float* g, float* sig) {
+  float d[N];
+  bool tiny = false;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    d[i] = 1.0f + expf(-g[i]);
+    sig[i] = recip_rn(d[i]);
+    tiny |= !(d[i] < 0x1p126f);
+  }
+  if (__builtin_amdgcn_ballot_w64(tiny)) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) sig[i] = d[i] < 0x1p126f ? sig[i] : 1.0f / d[i];
+  }
+}
 __device__ __forceinline__ float sigmoid_rn(float g) {
-  const float d = 1.0f + expf(-g);
-  float sig = recip_rn(d);
-  // d >= 2^126 (g < -87.3, the reciprocal subnormal or zero): the IEEE
-  // division, behind a wave-uniform branch that real data never takes.
-  const bool tiny = !(d < 0x1p126f);
-  if (__builtin_amdgcn_ballot_w64(tiny)) sig = tiny ? 1.0f / d : sig;
+  float sig;
+  sigmoid_rn_n<1>(&g, &sig);
   return sig;
+}
+template <int N>
+__device__ __forceinline__ void swiglu_values(const float* g, const float* u, float* a) {
+  float sig[N];
+  sigmoid_rn_n<N>(g, sig);
+#pragma unroll
+  for (int i = 0; i < N; ++i) a[i] = (g[i] * sig[i]) * u[i];
 }
 __device__ __forceinline__ float swiglu_value(float g, float u) { return (g * sigmoid_rn(g)) * u; }
 
 // The reference's bf16 SwiGLU, silu_mul (kernels.py:392-394): silu(g)
 // rounded to bf16, times u; the caller rounds the product to bf16 as it
 // stores it.
-__device__ __forceinline__ float silu_mul_value(float g, float u) {
-  return bf16_to_f32(f32_to_bf16(g * sigmoid_rn(g))) * u;
+template <int N>
+__device__ __forceinline__ void silu_mul_values(const float* g, const float* u, float* a) {
+  float sig[N];
+  sigmoid_rn_n<N>(g, sig);
+#pragma unroll
+  for (int i = 0; i < N; ++i) a[i] = bf16_to_f32(f32_to_bf16(g[i] * sig[i])) * u[i];
 }
 
 // SwiGLU + e4m3 requantisation of one 128-column group held by 16 lanes
@@ -153,15 +180,16 @@ __device__ __forceinline__ float silu_mul_value(float g, float u) {
 __device__ __forceinline__ float swiglu_quant_group(uint4 graw, uint4 uraw, uint2* codes) {
   const uint32_t gw[4] = {graw.x, graw.y, graw.z, graw.w};
   const uint32_t uw[4] = {uraw.x, uraw.y, uraw.z, uraw.w};
-  float v[8];
-  float amax = 0.0f;
+  float g[8], u[8], v[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const uint32_t gbits = (i & 1) ? (gw[i / 2] & 0xffff0000u) : (gw[i / 2] << 16);
-    const uint32_t ubits = (i & 1) ? (uw[i / 2] & 0xffff0000u) : (uw[i / 2] << 16);
-    v[i] = swiglu_value(__uint_as_float(gbits), __uint_as_float(ubits));
-    amax = fmaxf(amax, fabsf(v[i]));
+    g[i] = __uint_as_float((i & 1) ? (gw[i / 2] & 0xffff0000u) : (gw[i / 2] << 16));
+    u[i] = __uint_as_float((i & 1) ? (uw[i / 2] & 0xffff0000u) : (uw[i / 2] << 16));
   }
+  swiglu_values<8>(g, u, v);
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
   amax = segment_max<16>(amax);
   const float scale = group_scale(amax);
   const uint32_t lo = quantize_four(v, scale);

@@ -31,7 +31,7 @@
 //   * FC1 (mode 0): a workgroup covers 128 gate rows and the 128 matching up
 //     rows, so each lane holds gate and up of the same columns: the epilogue
 //     rounds both to bf16 (the reference's FC1 output), computes SwiGLU
-//     (swiglu_value), reduces the per-(route, 128-column) amax across lanes
+//     (swiglu_values), reduces the per-(route, 128-column) amax across lanes
 //     and waves and writes the e4m3 codes and scale, the bytes
 //     d3_silu_mul_quant would write.  FC2 (mode 1) stores fp32 rows by pair (the unpermute).
 //   * Workgroups are grouped so that two consecutive items' tiles run on one
@@ -96,12 +96,15 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   __shared__ int chunk_base[kByPair ? kGgMaxPairChunks * kGgWaves + 1 : 1];
 
   // XCD-aware order: workgroup b runs on XCD b % 8; logical index L gives
-  // each XCD runs of `chunk` consecutive (item, tile) pairs.
+  // each XCD runs of `chunk` = 2 n_tiles consecutive workgroups: the tiles
+  // of two consecutive items, interleaved so that the two workgroups that
+  // read one weight tile are dispatched back to back.
   const int b = blockIdx.x;
   const int xcd = b % kGgXcds, j = b / kGgXcds;
   const int logical = ((j / chunk) * kGgXcds + xcd) * chunk + j % chunk;
-  const int item_index = logical / n_tiles;
-  const int tile = logical % n_tiles;
+  const int within = logical % chunk;
+  const int item_index = (logical / chunk) * 2 + (within & 1);
+  const int tile = within >> 1;
   const bool dense = item_index >= max_items;  // a shared-expert item (uniform)
   int expert = 0, first = 0, routes = 0;
   if constexpr (kByPair) {
@@ -113,6 +116,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     expert = item.x;
     first = item.y;
     routes = min(item.z, kGgRoutes);
+    if (routes <= 0) return;  // a padding item (uniform)
   } else {
     first = (item_index - max_items) * kGgRoutes;
     if (first >= shared.rows) return;
@@ -360,19 +364,22 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     float v[kGgRouteTiles][8];
 #pragma unroll
     for (int rt = 0; rt < kGgRouteTiles; ++rt) {
-      float amax = 0.0f;
+      float g[8], u[8];
 #pragma unroll
       for (int p = 0; p < 2; ++p)
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
           const uint32_t gw = pack_bf16x2(acc[p][rt][i], acc[p][rt][i + 1]);
           const uint32_t uw = pack_bf16x2(acc[2 + p][rt][i], acc[2 + p][rt][i + 1]);
-          const float a0 = swiglu_value(bf16_lo(gw), bf16_lo(uw));
-          const float a1 = swiglu_value(bf16_hi(gw), bf16_hi(uw));
-          v[rt][4 * p + i] = a0;
-          v[rt][4 * p + i + 1] = a1;
-          amax = fmaxf(amax, fmaxf(fabsf(a0), fabsf(a1)));
+          g[4 * p + i] = bf16_lo(gw);
+          g[4 * p + i + 1] = bf16_hi(gw);
+          u[4 * p + i] = bf16_lo(uw);
+          u[4 * p + i + 1] = bf16_hi(uw);
         }
+      swiglu_values<8>(g, u, v[rt]);
+      float amax = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[rt][k]));
       amax = fmaxf(amax, __shfl_xor(amax, 16));
       amax = fmaxf(amax, __shfl_xor(amax, 32));
       if (group == 0) amax_part[wave][16 * rt + row16] = amax;
