@@ -72,24 +72,29 @@ struct SharedItems {
   int pair;
 };
 
-// kByPair (small batches): no sorted route list.  Work item i is part i % parts (routes
-// [128 part, 128 part + 128) in pair order) of expert i / parts; the
-// workgroup finds those routes itself in `sorted_ids`, which then holds the
-// routed expert of every (row, rank) pair, the live row count being
-// *num_items.  FC1 writes act rows by pair and FC2 reads them by pair, so
-// both match the sorted launches value for value.
+// kByPair (FC1 of small batches): no sorted route list.  Work item i is
+// part i % parts (routes [128 part, 128 part + 128) in pair order) of
+// expert i / parts; the workgroup finds those routes itself in
+// `sorted_ids`, which then holds the routed expert of every (row, rank)
+// pair, the live row count being *num_items.  What it found is written out
+// as a sorted route list with one 128-route item per (expert, part) - item
+// i = (expert, 128 i, routes), its pairs at list_ids[128 i ..] in ascending
+// order - and FC1 writes act rows at those positions, so the sorted FC2
+// launch reads them as it reads a route sort's.
 template <int KB, int MODE, bool kPacked, bool kByPair>
 __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2))) void grouped_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows, int out_cols,
     const uint8_t* __restrict__ act, uint32_t act_bytes, const float* __restrict__ act_scales,
     const int32_t* __restrict__ sorted_ids, int top_k, const int4* __restrict__ items,
     const int32_t* __restrict__ num_items, int max_items, SharedItems shared, int n_tiles, int chunk,
-    int parts, int capacity, uint8_t* __restrict__ out_codes, float* __restrict__ out_scales,
+    int parts, int capacity, int32_t* __restrict__ list_ids, int4* __restrict__ list_items,
+    int32_t* __restrict__ list_count, uint8_t* __restrict__ out_codes, float* __restrict__ out_scales,
     float* __restrict__ out_f32) {
+  static_assert(!kByPair || MODE == 0, "the route lists come from FC1");
   constexpr int K = KB * kGroup;
   __shared__ __attribute__((aligned(16))) uint8_t stage[2][kGgStage];
   __shared__ float a_scale[KB][kGgRoutes];
-  __shared__ int target[kGgRoutes];  // FC1: sorted position (by pair: the pair), FC2: pair; -1 = no route
+  __shared__ int target[kGgRoutes];  // FC1: sorted position, FC2: pair; -1 = no route
   __shared__ float amax_part[MODE == 0 ? kGgWaves : 1][kGgRoutes];
   __shared__ int route_pair[kByPair ? kGgRoutes : 1];
   __shared__ uint64_t chunk_masks[kByPair ? kGgMaxPairChunks * kGgWaves : 1];
@@ -220,8 +225,16 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     }
     const int base = chunk_base[kGgMaxPairChunks * kGgWaves];
     routes = __builtin_amdgcn_readfirstlane(min(max(base - part_first, 0), kGgRoutes));
-    if (routes == 0) return;  // uniform: this part of the expert is empty
     __syncthreads();
+    if (tile == 0) {  // the item of the route list (empty parts included)
+      for (int r = static_cast<int>(threadIdx.x); r < routes; r += kGgThreads)
+        list_ids[item_index * kGgRoutes + r] = route_pair[r];
+      if (threadIdx.x == 0) {
+        list_items[item_index] = make_int4(expert, item_index * kGgRoutes, routes, 0);
+        if (item_index == 0) *list_count = max_items;
+      }
+    }
+    if (routes == 0) return;  // uniform: this part of the expert is empty
   }
 
   // Route rows of the item, loaded branch-free (a dead route reads the
@@ -229,7 +242,6 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   // items map row r of the item to token first + r.
   auto route_row = [&](int r, int id) {
     if (dense) return MODE == 0 ? first + r : shared.pos + first + r;
-    if constexpr (kByPair) return MODE == 0 ? id / top_k : id;
     return MODE == 0 ? id / top_k : first + r;
   };
   const int part = tid & 7;
@@ -280,7 +292,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     for (int q = 0; q * kSplit + k0 < KB; ++q) sc[q] = srow[q * kSplit + k0];
 #pragma unroll
     for (int q = 0; q * kSplit + k0 < KB; ++q) a_scale[q * kSplit + k0][rs] = live ? sc[q] : 0.0f;
-    int t = MODE == 0 && !kByPair ? first + rs : id_s;
+    int t = MODE == 1 ? id_s : (kByPair ? item_index * kGgRoutes : first) + rs;
     if (dense) t = (MODE == 0 ? shared.pos : shared.pair) + first + rs;
     if (k0 == 0) target[rs] = live ? t : -1;
   }
@@ -425,6 +437,9 @@ struct GroupedLaunch {
   float* out;
   int parts = 0;     // by-pair launches: work items per expert (0: sorted items)
   int capacity = 0;  // by-pair launches: slot rows of the ids
+  int32_t* list_ids = nullptr;  // by-pair launches: the route list they write
+  int4* list_items = nullptr;
+  int32_t* list_count = nullptr;
 };
 
 template <int KB, int MODE>
@@ -438,13 +453,18 @@ void launch_grouped(const GroupedLaunch& g, hipStream_t s) {
   const int blocks = static_cast<int>((logical + per_round - 1) / per_round * per_round);
 #define D3_GG_ARGS dim3(blocks), dim3(kGgThreads), 0, s, g.w, g.ws, g.n_rows, g.out_cols, g.a, \
                    g.a_bytes, g.as, g.sorted_ids, g.top_k, g.items, g.num_items, g.max_items, \
-                   g.shared, n_tiles, chunk, g.parts, g.capacity, g.codes, g.scales, g.out
-  if (g.parts > 0) {
-    if (g.layout == D3_LAYOUT_FRAGMENT)
-      hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true, true>), D3_GG_ARGS);
-    else
-      hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, false, true>), D3_GG_ARGS);
-  } else if (g.layout == D3_LAYOUT_FRAGMENT) {
+                   g.shared, n_tiles, chunk, g.parts, g.capacity, g.list_ids, g.list_items,   \
+                   g.list_count, g.codes, g.scales, g.out
+  if constexpr (MODE == 0) {
+    if (g.parts > 0) {
+      if (g.layout == D3_LAYOUT_FRAGMENT)
+        hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true, true>), D3_GG_ARGS);
+      else
+        hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, false, true>), D3_GG_ARGS);
+      return;
+    }
+  }
+  if (g.layout == D3_LAYOUT_FRAGMENT) {
     hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true, false>), D3_GG_ARGS);
   } else {
     hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, false, false>), D3_GG_ARGS);
@@ -562,8 +582,10 @@ extern "C" int d3_grouped_fc1_swiglu_by_pair(const uint8_t* w13, const float* s1
                                              const float* x_scales, const int32_t* ids,
                                              int32_t top_k, const int32_t* row_count,
                                              int32_t capacity, uint8_t* act, float* act_scales,
-                                             void* stream) {
-  D3_REQUIRE(act && act_scales && ids && row_count, "grouped_fc1_swiglu_by_pair: null pointer");
+                                             int32_t* list_ids, int32_t* list_items,
+                                             int32_t* list_count, void* stream) {
+  D3_REQUIRE(act && act_scales && ids && row_count && list_ids && list_items && list_count,
+             "grouped_fc1_swiglu_by_pair: null pointer");
   D3_REQUIRE(intermediate > 0 && intermediate % kGroup == 0,
              "grouped_fc1_swiglu_by_pair: intermediate %d must be a multiple of 128", intermediate);
   D3_REQUIRE(capacity >= 1 && capacity <= q_rows, "grouped_fc1_swiglu_by_pair: capacity %d not in [1, %lld]",
@@ -579,6 +601,9 @@ extern "C" int d3_grouped_fc1_swiglu_by_pair(const uint8_t* w13, const float* s1
                   act_scales, nullptr};
   g.parts = parts;
   g.capacity = capacity;
+  g.list_ids = list_ids;
+  g.list_items = reinterpret_cast<int4*>(list_items);
+  g.list_count = list_count;
   int status = check_grouped(g, num_experts, hidden, q_rows, "grouped_fc1_swiglu_by_pair",
                              /*need_items=*/false);
   if (status != D3_OK) return status;
@@ -587,32 +612,4 @@ extern "C" int d3_grouped_fc1_swiglu_by_pair(const uint8_t* w13, const float* s1
   D3_LAUNCHED("grouped_fc1_swiglu_by_pair");
 }
 
-extern "C" int d3_grouped_fc2_by_pair(const uint8_t* w2, const float* s2, int32_t weight_layout,
-                                      int32_t num_experts, int32_t hidden, int32_t intermediate,
-                                      const uint8_t* act, const float* act_scales,
-                                      const int32_t* ids, int32_t top_k,
-                                      const int32_t* row_count, int32_t capacity, float* down,
-                                      void* stream) {
-  D3_REQUIRE(down && ids && row_count, "grouped_fc2_by_pair: null pointer");
-  D3_SUPPORTED(hidden > 0 && hidden % kGgRows == 0, "grouped_fc2_by_pair: hidden %d must be a multiple of %d",
-               hidden, kGgRows);
-  D3_REQUIRE(capacity >= 1 && top_k >= 1, "grouped_fc2_by_pair: capacity %d, top_k %d", capacity, top_k);
-  D3_SUPPORTED(static_cast<int64_t>(capacity) * top_k <= kGgMaxPairs,
-               "grouped_fc2_by_pair: capacity %d x top_k %d above %d routes", capacity, top_k,
-               kGgMaxPairs);
-  D3_REQUIRE(aligned_to(down, 16), "grouped_fc2_by_pair: down must be 16-byte aligned");
-  const int parts = (capacity + kGgRoutes - 1) / kGgRoutes;
-  const int64_t act_rows = static_cast<int64_t>(capacity) * top_k;
-  GroupedLaunch g{1, weight_layout, w2, s2, hidden, hidden, act,
-                  static_cast<uint32_t>(act_rows * intermediate), act_scales, ids, top_k, nullptr,
-                  row_count, num_experts * parts, kGgRoutes, SharedItems{nullptr, nullptr, 0, 0, 0},
-                  nullptr, nullptr, down};
-  g.parts = parts;
-  g.capacity = capacity;
-  int status = check_grouped(g, num_experts, intermediate, act_rows, "grouped_fc2_by_pair",
-                             /*need_items=*/false);
-  if (status != D3_OK) return status;
-  status = dispatch_grouped<1>(g, intermediate, as_stream(stream));
-  if (status != D3_OK) return status;
-  D3_LAUNCHED("grouped_fc2_by_pair");
-}
+

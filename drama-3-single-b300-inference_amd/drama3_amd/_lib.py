@@ -69,9 +69,8 @@ SIGNATURES = {
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _p, _i32, _i32, _p, _p,
                _i32, _i32, _i32, _p, _p]),
     "d3_grouped_fc1_swiglu_by_pair": (
-        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _i32, _p, _p, _p]),
-    "d3_grouped_fc2_by_pair": (
-        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _i32, _p, _p]),
+        _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _i32, _p, _p, _p, _p,
+               _p, _p]),
     "d3_pack_expert_weights": (_i32, [_p, _i32, _i32, _i32, _p, _p]),
     "d3_expert_fc2_swiglu": (
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _p, _p]),

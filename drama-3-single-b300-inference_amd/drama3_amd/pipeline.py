@@ -191,12 +191,24 @@ class MoEWorkspace:
                              f"intermediate in {GROUPED_K}, hidden % 256 == 0")
         self.grouped = bool(grouped) and not sortless
         # Grouped GEMMs without the route sort (small batches): the front
-        # launch skips the sort and the GEMM workgroups find their routes in
-        # `ids`; act / down rows by pair.
+        # launch skips the sort, FC1's workgroups find their routes in `ids`
+        # and write them as a route list of one 128-route item per (expert,
+        # part), act rows at the list's positions; FC2 reads that list as it
+        # reads a sort's.
         if by_pair and not (self.grouped and shared_rows == 0 and pairs <= BY_PAIR_MAX_PAIRS):
             raise ValueError(f"by_pair needs the grouped GEMMs, no folded shared expert and "
                              f"<= {BY_PAIR_MAX_PAIRS} (row, rank) pairs")
         self.by_pair = bool(by_pair)
+        if self.by_pair:
+            self.list_items_max = e * -(-t // GROUPED_ROUTES)
+            list_rows = self.list_items_max * GROUPED_ROUTES
+            self.list_ids = torch.empty(list_rows, **i32)
+            self.list_items = torch.empty((self.list_items_max, 4), **i32)
+            self.list_count = torch.empty(1, **i32)
+            if list_rows > len(self.act):
+                self.act = torch.empty((list_rows, i), dtype=torch.uint8, device=dev)
+                self.act_scales = torch.empty((list_rows, i // 128), dtype=torch.float32,
+                                              device=dev)
         self.rows_dev = torch.full((1,), t, **i32)  # the live row count when none is given
         # Scratch of the wide route sort (prefill-sized batches).
         self.wide_sort = pairs > WIDE_SORT_PAIRS
@@ -300,23 +312,26 @@ class MoEWorkspace:
              stream)
 
     def grouped_fc1_by_pair(self, experts, row_count=None, stream=None) -> None:
-        """Grouped FC1 + SwiGLU requant without a sorted route list: act /
-        act_scales by pair."""
+        """Grouped FC1 + SwiGLU requant without a sorted route list: the
+        routes found as ``list_ids`` / ``list_items`` / ``list_count``, act /
+        act_scales at the list's positions."""
         s, stream = self.shape, self._stream(stream)
         w, ws, layout = fc1_operands(experts)
         count = self.rows_dev if row_count is None else row_count
         call("d3_grouped_fc1_swiglu_by_pair", ptr(w), ptr(ws), layout, s.num_experts,
              s.intermediate, s.hidden, ptr(self.q), s.rows, ptr(self.x_scales), ptr(self.ids),
-             s.top_k, ptr(count), s.rows, ptr(self.act), ptr(self.act_scales), stream)
+             s.top_k, ptr(count), s.rows, ptr(self.act), ptr(self.act_scales),
+             ptr(self.list_ids), ptr(self.list_items), ptr(self.list_count), stream)
 
-    def grouped_fc2_by_pair(self, experts, row_count=None, stream=None) -> None:
-        """Grouped FC2 reading act by pair: fp32 down rows by pair."""
+    def grouped_fc2_listed(self, experts, stream=None) -> None:
+        """Grouped FC2 over the route list grouped_fc1_by_pair wrote: fp32
+        down rows by pair."""
         s, stream = self.shape, self._stream(stream)
         w, ws, layout = fc2_operands(experts)
-        count = self.rows_dev if row_count is None else row_count
-        call("d3_grouped_fc2_by_pair", ptr(w), ptr(ws), layout, s.num_experts, s.hidden,
-             s.intermediate, ptr(self.act), ptr(self.act_scales), ptr(self.ids), s.top_k,
-             ptr(count), s.rows, ptr(self.down), stream)
+        call("d3_grouped_fc2", ptr(w), ptr(ws), layout, s.num_experts, s.hidden, s.intermediate,
+             ptr(self.act), len(self.act), ptr(self.act_scales), ptr(self.list_ids), s.top_k,
+             ptr(self.list_items), ptr(self.list_count), self.list_items_max, GROUPED_ROUTES,
+             None, None, 0, 0, 0, ptr(self.down), stream)
 
     @property
     def shared_down(self) -> torch.Tensor:
@@ -464,7 +479,7 @@ class MoEWorkspace:
             self.decode_fc2(experts, row_count, stream)
         elif self.by_pair:
             self.grouped_fc1_by_pair(experts, row_count, stream)
-            self.grouped_fc2_by_pair(experts, row_count, stream)
+            self.grouped_fc2_listed(experts, stream)
         elif self.grouped:
             self.grouped_fc1(experts, stream=stream)
             self.grouped_fc2(experts, stream=stream)

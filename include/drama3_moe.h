@@ -336,28 +336,29 @@ int d3_grouped_fc2(const uint8_t *w2, const float *s2, int32_t weight_layout,
                    int32_t shared_out_row, float *down, void *stream);
 
 /*
- * A8 + A9 + A10 and A11  The tiled grouped FP8 GEMMs without a route sort,
- * for small batches (routes of up to 8192 (row, rank) pairs): replaces the
- * sort kernels.py:658-731 + fused_moe_gemm (kernels.py:734-779) pair for
+ * A5-A8 + A9 + A10  The tiled grouped FP8 FC1 without a route sort, for
+ * small batches (routes of up to 8192 (row, rank) pairs): replaces the sort
+ * kernels.py:658-731 + the first fused_moe_gemm (kernels.py:734-779) for
  * batches where one sort launch is a large share of the step.  Work item
- * (expert e, part j) takes e's routes of ranks [128 j, 128 j + 128) in pair
- * order, found by the workgroup in `ids` ([capacity, top_k] int32 routed
- * expert ids of the rows, *row_count live).  FC1 writes act [capacity *
- * top_k, I] / act_scales [capacity * top_k, I/128] by pair, FC2 reads them
- * by pair and writes down fp32 [capacity * top_k, H] by pair: the values of
- * d3_grouped_fc1_swiglu / d3_grouped_fc2 after d3_sort_routes (whose act
- * rows sit at sorted positions instead).  Requires capacity * top_k <= 8192.
+ * (expert e, part j), item index i = e * parts + j with parts =
+ * ceil(capacity / 128), takes e's routes of ranks [128 j, 128 j + 128) in
+ * pair order, found by the workgroup in `ids` ([capacity, top_k] int32
+ * routed expert ids of the rows, *row_count live).  It writes what it found
+ * as a sorted route list: list_items[i] = (e, 128 i, routes, 0) int32x4,
+ * the item's pairs at list_ids[128 i ..] (ascending), *list_count =
+ * E * parts; and act [E * parts * 128, I] / act_scales at those positions.
+ * d3_grouped_fc2 with sorted_ids = list_ids, items = list_items, num_items
+ * = list_count, max_items = E * parts, item_rows = 128 then writes down by
+ * pair.  The values are those of d3_grouped_fc1_swiglu / d3_grouped_fc2
+ * after d3_sort_routes.  Requires capacity * top_k <= 8192.
  */
 int d3_grouped_fc1_swiglu_by_pair(const uint8_t *w13, const float *s13, int32_t weight_layout,
                                   int32_t num_experts, int32_t intermediate, int32_t hidden,
                                   const uint8_t *q, int64_t q_rows, const float *x_scales,
                                   const int32_t *ids, int32_t top_k, const int32_t *row_count,
-                                  int32_t capacity, uint8_t *act, float *act_scales, void *stream);
-int d3_grouped_fc2_by_pair(const uint8_t *w2, const float *s2, int32_t weight_layout,
-                           int32_t num_experts, int32_t hidden, int32_t intermediate,
-                           const uint8_t *act, const float *act_scales, const int32_t *ids,
-                           int32_t top_k, const int32_t *row_count, int32_t capacity, float *down,
-                           void *stream);
+                                  int32_t capacity, uint8_t *act, float *act_scales,
+                                  int32_t *list_ids, int32_t *list_items, int32_t *list_count,
+                                  void *stream);
 
 /*
  * A9/A11 weight preparation (once, at load time).

@@ -218,10 +218,12 @@ def test_shared_expert_on_side_stream_and_folded_graph_replays(device):
                                    (37, 8, 256, 1536)],
                          ids=["c5_shapes", "h512_i512", "c4_model_1024_rows", "tiny"])
 def test_grouped_by_pair_matches_sorted(device, shape):
-    """The grouped GEMMs that find their own routes (no sort) give the sorted
-    launches' values: act codes and scales of every live pair (by pair
-    against by sorted position) and the fp32 down rows, byte for byte; a
-    live row count below the capacity leaves the rows past it untouched."""
+    """FC1 finding its own routes (no sort) writes them as a route list of
+    one 128-route item per (expert, part) - each expert's list equal to the
+    sort's - with act codes and scales at the list's positions equal to the
+    sorted launch's; FC2 over that list gives the sorted chain's fp32 down
+    rows byte for byte; a live row count below the capacity leaves the rows
+    past it untouched."""
     from drama3_amd.expert_weights import prepare_experts
     from drama3_amd.pipeline import MoEWorkspace, Shape
 
@@ -236,13 +238,32 @@ def test_grouped_by_pair_matches_sorted(device, shape):
         ws.down.fill_(7.0)
         ws.routes_down(experts, live_rows)
     torch.cuda.synchronize()
-    live_pairs = int(live_rows.item()) * 8
-    inverse = sorted_ws.inverse[:live_pairs].long()
     live = int(live_rows.item())
+    live_pairs = live * 8
     assert torch.equal(pair_ws.ids[:live], sorted_ws.ids[:live])
-    assert torch.equal(pair_ws.act[:live_pairs], sorted_ws.act[inverse])
-    assert torch.equal(pair_ws.act_scales[:live_pairs].view(torch.int32),
-                       sorted_ws.act_scales[inverse].view(torch.int32))
+    # the route list: item e * parts + j holds expert e's sorted routes [128 j, 128 j + 128)
+    parts = -(-rows // 128)
+    assert int(pair_ws.list_count.item()) == e * parts
+    items = pair_ws.list_items.cpu()
+    list_ids = pair_ws.list_ids.cpu()
+    counts, starts = sorted_ws.counts.cpu(), sorted_ws.starts.cpu()
+    sorted_ids = sorted_ws.sorted_ids.cpu()
+    position = torch.full((live_pairs,), -1, dtype=torch.long)
+    for ex in range(e):
+        want = sorted_ids[starts[ex]:starts[ex] + counts[ex]]
+        got = []
+        for j in range(parts):
+            item = ex * parts + j
+            n = min(max(int(counts[ex]) - 128 * j, 0), 128)
+            assert items[item].tolist() == [ex, 128 * item, n, 0]
+            got.append(list_ids[128 * item:128 * item + n])
+            position[list_ids[128 * item:128 * item + n].long()] = torch.arange(128 * item, 128 * item + n)
+        assert torch.equal(torch.cat(got), want)
+    assert bool((position >= 0).all())
+    inverse = sorted_ws.inverse[:live_pairs].long()
+    at = position.to(device)
+    assert torch.equal(pair_ws.act[at], sorted_ws.act[inverse])
+    assert torch.equal(pair_ws.act_scales[at].view(torch.int32), sorted_ws.act_scales[inverse].view(torch.int32))
     assert torch.equal(pair_ws.down[:live_pairs].view(torch.int32),
                        sorted_ws.down[:live_pairs].view(torch.int32))
     assert bool((pair_ws.down[live_pairs:] == 7.0).all())
