@@ -47,12 +47,10 @@ namespace {
 constexpr int kGgWaves = 4;
 constexpr int kGgThreads = kGgWaves * kWave;
 constexpr int kGgRoutes = 128;                     // routes per work item (MFMA N side)
-constexpr int kGgRouteTiles = kGgRoutes / 16;      // 16-route tiles per wave
+constexpr int kGgPairRoutes = 64;                  // routes per work item of by-pair launches
 constexpr int kGgWaveTiles = 4;                    // 16-row weight tiles per wave
 constexpr int kGgRows = kGgWaves * kGgWaveTiles * 16;  // 256 weight rows per workgroup
 constexpr int kGgStride = kGroup + 16;             // LDS bytes per staged route row
-constexpr int kGgStage = kGgRoutes * kGgStride;
-constexpr int kGgStaged = kGgRoutes * kGroup / (16 * kGgThreads);  // 16-byte copies per thread and K block
 constexpr int kGgXcds = 8;
 // Routes found by the workgroups themselves (by-pair launches): at most this
 // many (row, rank) pairs, read in chunks of one id per thread.
@@ -72,15 +70,15 @@ struct SharedItems {
   int pair;
 };
 
-// kByPair (FC1 of small batches): no sorted route list.  Work item i is
-// part i % parts (routes [128 part, 128 part + 128) in pair order) of
-// expert i / parts; the workgroup finds those routes itself in
-// `sorted_ids`, which then holds the routed expert of every (row, rank)
-// pair, the live row count being *num_items.  What it found is written out
-// as a sorted route list with one 128-route item per (expert, part) - item
-// i = (expert, 128 i, routes), its pairs at list_ids[128 i ..] in ascending
-// order - and FC1 writes act rows at those positions, so the sorted FC2
-// launch reads them as it reads a route sort's.
+// kByPair (FC1 of small batches): no sorted route list.  A work item is
+// part j (routes [64 j, 64 j + 64) in pair order) of an expert; the
+// workgroup finds those routes itself in `sorted_ids`, which
+// then holds the routed expert of every (row, rank) pair, the live row
+// count being *num_items.  What they found is written out as a sorted
+// route list of 128-route items, two parts each - item i = (expert, 128 i,
+// routes), its pairs at list_ids[128 i ..] in ascending order - and FC1
+// writes act rows at those positions, so the sorted FC2 launch reads them
+// as it reads a route sort's.
 template <int KB, int MODE, bool kPacked, bool kByPair>
 __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2))) void grouped_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows, int out_cols,
@@ -92,11 +90,17 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     float* __restrict__ out_f32) {
   static_assert(!kByPair || MODE == 0, "the route lists come from FC1");
   constexpr int K = KB * kGroup;
-  __shared__ __attribute__((aligned(16))) uint8_t stage[2][kGgStage];
-  __shared__ float a_scale[KB][kGgRoutes];
-  __shared__ int target[kGgRoutes];  // FC1: sorted position, FC2: pair; -1 = no route
-  __shared__ float amax_part[MODE == 0 ? kGgWaves : 1][kGgRoutes];
-  __shared__ int route_pair[kByPair ? kGgRoutes : 1];
+  // Routes per work item: by-pair launches take 64 (twice the workgroups,
+  // each with half the epilogue, for batches that leave most CUs idle).
+  constexpr int kR = kByPair ? kGgPairRoutes : kGgRoutes;
+  constexpr int kRT = kR / 16;                              // 16-route tiles per wave
+  constexpr int kStage = kR * kGgStride;
+  constexpr int kStaged = kR * kGroup / (16 * kGgThreads);  // 16-byte copies per thread and K block
+  __shared__ __attribute__((aligned(16))) uint8_t stage[2][kStage];
+  __shared__ float a_scale[KB][kR];
+  __shared__ int target[kR];  // FC1: sorted position, FC2: pair; -1 = no route
+  __shared__ float amax_part[MODE == 0 ? kGgWaves : 1][kR];
+  __shared__ int route_pair[kByPair ? kR : 1];
   __shared__ uint64_t chunk_masks[kByPair ? kGgMaxPairChunks * kGgWaves : 1];
   __shared__ int chunk_base[kByPair ? kGgMaxPairChunks * kGgWaves + 1 : 1];
 
@@ -112,20 +116,28 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   const int tile = within >> 1;
   const bool dense = item_index >= max_items;  // a shared-expert item (uniform)
   int expert = 0, first = 0, routes = 0;
+  int pj = 0, slot = 0;  // by-pair: the expert's part, and its expert-major index
   if constexpr (kByPair) {
     if (item_index >= max_items) return;
-    expert = item_index / parts;
+    // Part-pair-major order (parts 2 p and 2 p + 1 of every expert, then
+    // the next p): the launch's first workgroups take the parts that hold
+    // routes, so they start on CUs of their own.
+    const int experts_n = max_items / parts;
+    const int pp = item_index / (2 * experts_n), rem = item_index - pp * 2 * experts_n;
+    expert = rem >> 1;
+    pj = 2 * pp + (rem & 1);
+    slot = expert * parts + pj;
   } else if (!dense) {
     if (item_index >= *num_items) return;
     const int4 item = items[item_index];
     expert = item.x;
     first = item.y;
-    routes = min(item.z, kGgRoutes);
+    routes = min(item.z, kR);
     if (routes <= 0) return;  // a padding item (uniform)
   } else {
-    first = (item_index - max_items) * kGgRoutes;
+    first = (item_index - max_items) * kR;
     if (first >= shared.rows) return;
-    routes = min(kGgRoutes, shared.rows - first);
+    routes = min(kR, shared.rows - first);
   }
 
   const int tid = threadIdx.x;
@@ -179,7 +191,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     // wave's ballot of chunk j goes to LDS; one wave turns their counts into
     // exclusive bases (in pair order: chunk, then wave); each thread then
     // ranks only its own matches (a few of its 32 chunks).
-    const int part_first = (item_index % parts) * kGgRoutes;
+    const int part_first = pj * kR;
     const int live_rows = min(*num_items, capacity);
     const int pairs = live_rows * top_k;
     const BufferView id_view(sorted_ids, static_cast<uint32_t>(capacity * top_k) * 4);
@@ -221,17 +233,21 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
       const int j = __builtin_ctz(m);
       const int cell = j * kGgWaves + my_wave;
       const int r = chunk_base[cell] + __popcll(chunk_masks[cell] & lanemask_lt()) - part_first;
-      if (r >= 0 && r < kGgRoutes) route_pair[r] = j * kGgThreads + static_cast<int>(threadIdx.x);
+      if (r >= 0 && r < kR) route_pair[r] = j * kGgThreads + static_cast<int>(threadIdx.x);
     }
     const int base = chunk_base[kGgMaxPairChunks * kGgWaves];
-    routes = __builtin_amdgcn_readfirstlane(min(max(base - part_first, 0), kGgRoutes));
+    routes = __builtin_amdgcn_readfirstlane(min(max(base - part_first, 0), kR));
     __syncthreads();
-    if (tile == 0) {  // the item of the route list (empty parts included)
+    if (tile == 0) {  // the route list (empty parts included)
       for (int r = static_cast<int>(threadIdx.x); r < routes; r += kGgThreads)
-        list_ids[item_index * kGgRoutes + r] = route_pair[r];
-      if (threadIdx.x == 0) {
-        list_items[item_index] = make_int4(expert, item_index * kGgRoutes, routes, 0);
-        if (item_index == 0) *list_count = max_items;
+        list_ids[slot * kR + r] = route_pair[r];
+      // list item = kGgRoutes / kR consecutive parts, written by the first
+      constexpr int kPer = kGgRoutes / kR;
+      if (threadIdx.x == 0 && pj % kPer == 0) {
+        const int list_item = slot / kPer;
+        const int listed = min(max(base - part_first, 0), kGgRoutes);
+        list_items[list_item] = make_int4(expert, list_item * kGgRoutes, listed, 0);
+        if (item_index == 0) *list_count = max_items / kPer;
       }
     }
     if (routes == 0) return;  // uniform: this part of the expert is empty
@@ -246,37 +262,37 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   };
   const int part = tid & 7;
   const int r0 = tid >> 3;
-  int ids[kGgStaged];
+  int ids[kStaged];
 #pragma unroll
-  for (int i = 0; i < kGgStaged; ++i) {
+  for (int i = 0; i < kStaged; ++i) {
     const int r = r0 + (kGgThreads / 8) * i;
     if constexpr (kByPair)
       ids[i] = route_pair[r < routes ? r : 0];
     else
       ids[i] = dense ? 0 : sorted_ids[first + (r < routes ? r : 0)];
   }
-  const int rs = tid % kGgRoutes;       // route of this thread's scales / target
-  const int k0 = tid / kGgRoutes;       // first K block of its scales
+  const int rs = tid % kR;       // route of this thread's scales / target
+  const int k0 = tid / kR;       // first K block of its scales
   const int id_s = kByPair ? route_pair[rs < routes ? rs : 0]
                            : (dense ? 0 : sorted_ids[first + (rs < routes ? rs : 0)]);
 
   // Staging: thread t copies 16 bytes (chunk t % 8 of the K block) of routes
   // t / 8 + 32 i.  Dead routes read past the buffer (zeros).
   const BufferView view(act, act_bytes);
-  uint32_t src[kGgStaged];
+  uint32_t src[kStaged];
 #pragma unroll
-  for (int i = 0; i < kGgStaged; ++i) {
+  for (int i = 0; i < kStaged; ++i) {
     const int r = r0 + (kGgThreads / 8) * i;
     src[i] = r < routes ? static_cast<uint32_t>(route_row(r, ids[i])) * K + part * 16 : kNoRow;
   }
-  int4 staged[kGgStaged];
+  int4 staged[kStaged];
   auto stage_load = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < kGgStaged; ++i) staged[i] = view.load16(src[i] + kb * kGroup);
+    for (int i = 0; i < kStaged; ++i) staged[i] = view.load16(src[i] + kb * kGroup);
   };
   auto stage_store = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < kGgStaged; ++i)
+    for (int i = 0; i < kStaged; ++i)
       *reinterpret_cast<int4*>(&stage[kb & 1][(r0 + (kGgThreads / 8) * i) * kGgStride + part * 16]) =
           staged[i];
   };
@@ -284,7 +300,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 
   // Route targets and activation scales of the item.
   {
-    constexpr int kSplit = kGgThreads / kGgRoutes;  // threads per route row of scales
+    constexpr int kSplit = kGgThreads / kR;  // threads per route row of scales
     const bool live = rs < routes;
     const float* srow = act_scales + static_cast<size_t>(route_row(rs, id_s)) * KB;
     float sc[(KB + kSplit - 1) / kSplit];
@@ -292,7 +308,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     for (int q = 0; q * kSplit + k0 < KB; ++q) sc[q] = srow[q * kSplit + k0];
 #pragma unroll
     for (int q = 0; q * kSplit + k0 < KB; ++q) a_scale[q * kSplit + k0][rs] = live ? sc[q] : 0.0f;
-    int t = MODE == 1 ? id_s : (kByPair ? item_index * kGgRoutes : first) + rs;
+    int t = MODE == 1 ? id_s : (kByPair ? slot * kR : first) + rs;
     if (dense) t = (MODE == 0 ? shared.pos : shared.pair) + first + rs;
     if (k0 == 0) target[rs] = live ? t : -1;
   }
@@ -308,11 +324,11 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   stage_store(0);
   __syncthreads();
 
-  floatx4 acc[kGgWaveTiles][kGgRouteTiles];
+  floatx4 acc[kGgWaveTiles][kRT];
 #pragma unroll
   for (int t = 0; t < kGgWaveTiles; ++t)
 #pragma unroll
-    for (int rt = 0; rt < kGgRouteTiles; ++rt) acc[t][rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int rt = 0; rt < kRT; ++rt) acc[t][rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
@@ -333,9 +349,9 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     floatx4 partial[2][kGgWaveTiles];
     float as_prev = 0.0f;
 #pragma unroll
-    for (int rt = 0; rt <= kGgRouteTiles; ++rt) {
+    for (int rt = 0; rt <= kRT; ++rt) {
       float as = 0.0f;
-      if (rt < kGgRouteTiles) {
+      if (rt < kRT) {
         const int route = 16 * rt + row16;
         const int32x8 bfrag = load_fragment(buf + route * kGgStride, 0, group);
         as = a_scale[kb][route];
@@ -361,7 +377,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 
   if constexpr (MODE == 1) {
 #pragma unroll
-    for (int rt = 0; rt < kGgRouteTiles; ++rt) {
+    for (int rt = 0; rt < kRT; ++rt) {
       const int pair = target[16 * rt + row16];
       if (pair < 0) continue;
 #pragma unroll
@@ -373,9 +389,9 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   } else {
     // SwiGLU on the bf16-rounded FC1 outputs; lane holds gate / up columns
     // 32 wave + 16 p + 4 group + i (p < 2, i < 4) of route 16 rt + row16.
-    float v[kGgRouteTiles][8];
+    float v[kRT][8];
 #pragma unroll
-    for (int rt = 0; rt < kGgRouteTiles; ++rt) {
+    for (int rt = 0; rt < kRT; ++rt) {
       float g[8], u[8];
 #pragma unroll
       for (int p = 0; p < 2; ++p)
@@ -399,7 +415,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     __syncthreads();
     const int groups = out_cols / kGroup;
 #pragma unroll
-    for (int rt = 0; rt < kGgRouteTiles; ++rt) {
+    for (int rt = 0; rt < kRT; ++rt) {
       const int route = 16 * rt + row16;
       const int position = target[route];
       if (position < 0) continue;
@@ -594,10 +610,11 @@ extern "C" int d3_grouped_fc1_swiglu_by_pair(const uint8_t* w13, const float* s1
                "grouped_fc1_swiglu_by_pair: capacity %d x top_k %d above %d routes", capacity, top_k,
                kGgMaxPairs);
   D3_REQUIRE(aligned_to(act, 4), "grouped_fc1_swiglu_by_pair: act must be 4-byte aligned");
-  const int parts = (capacity + kGgRoutes - 1) / kGgRoutes;
+  // work items of 64 routes, two per 128-route item of the list
+  const int parts = (capacity + kGgRoutes - 1) / kGgRoutes * (kGgRoutes / kGgPairRoutes);
   GroupedLaunch g{0, weight_layout, w13, s13, 2 * intermediate, intermediate, q,
                   static_cast<uint32_t>(q_rows * hidden), x_scales, ids, top_k, nullptr, row_count,
-                  num_experts * parts, kGgRoutes, SharedItems{nullptr, nullptr, 0, 0, 0}, act,
+                  num_experts * parts, kGgPairRoutes, SharedItems{nullptr, nullptr, 0, 0, 0}, act,
                   act_scales, nullptr};
   g.parts = parts;
   g.capacity = capacity;
