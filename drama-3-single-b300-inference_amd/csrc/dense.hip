@@ -6,17 +6,22 @@
 // (kernels.py:386-395), and for the shared expert's down projection.
 //
 // Design (gfx950, wave64, mfma_f32_16x16x32_bf16):
-//   * A workgroup owns two 16-row tiles of W and up to 64 rows of x per
-//     pass.  K is walked in chunks of 256 columns: the workgroup copies the
-//     chunk of both operands (64 x rows, 32 W rows; 48 KB) into LDS with
-//     coalesced 16-byte loads (each wave instruction reads 1 KB of
-//     contiguous row), the next two chunks' loads in flight (registers)
-//     while the current chunk is multiplied.
+//   * A workgroup owns two 16-row tiles of W and one 16-row tile of x, so a
+//     decode-sized batch spreads over (tile pairs) x (x tiles) workgroups
+//     instead of leaving most CUs idle (64 rows of x per workgroup measured
+//     3.5 us slower on the reference model's layer).  K is walked in chunks
+//     of 256 columns: the workgroup copies the chunk of both operands (16 x
+//     rows, 32 W rows; 24 KB) into LDS with coalesced 16-byte loads (each
+//     wave instruction reads 1 KB of contiguous row), the next two chunks'
+//     loads in flight (registers) while the current chunk is multiplied.
 //   * LDS rows are 512 bytes; the 16-byte part p of row r is stored at
 //     position p ^ (r & 31), so the 16 rows an MFMA fragment read touches
 //     land on distinct banks.
-//   * Wave w computes weight tile w / 4 against token tile w % 4 over the
-//     whole K, so no cross-wave reduction is needed.
+//   * Wave w computes weight tile w / 4 over the K quarter w % 4 of every
+//     chunk; the four quarters' fp32 sums meet in LDS and are added in
+//     quarter order.  (Operands loaded straight into MFMA fragments, with
+//     no LDS, measured 1.7 us slower: each wave instruction then reads 16
+//     row pieces of 64 bytes.)
 //   * Paired tiles (the projection's first 2I rows are the shared expert's
 //     gate rows then its up rows): a workgroup takes gate tile j and up tile
 //     j, so it holds both halves of 16 activation columns and writes
@@ -31,10 +36,10 @@ namespace {
 
 constexpr int kDenseWaves = 8;
 constexpr int kDenseThreads = kDenseWaves * kWave;
-constexpr int kDenseTokens = 64;   // x rows per pass (4 token tiles)
+constexpr int kDenseTokens = 16;   // x rows per workgroup (one token tile)
 constexpr int kDenseChunk = 256;   // K columns per LDS chunk (512 bytes of a row)
 constexpr int kDenseParts = kDenseChunk * 2 / 16;  // 16-byte parts per chunk row (32)
-constexpr int kXLoads = kDenseTokens * kDenseParts / kDenseThreads;  // 4 per thread
+constexpr int kXLoads = kDenseTokens * kDenseParts / kDenseThreads;  // 1 per thread
 constexpr int kWLoads = 32 * kDenseParts / kDenseThreads;            // 2 per thread
 
 struct DenseArgs {
@@ -63,7 +68,8 @@ template <int CHUNKS>
 __global__ __launch_bounds__(kDenseThreads) void dense_bf16_kernel(DenseArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kDenseTokens * 512];
   __shared__ __attribute__((aligned(16))) uint8_t wsm[2][32 * 512];
-  __shared__ floatx4 up_sum[4][kWave];
+  __shared__ floatx4 quarter_sum[2][4][kWave];
+  __shared__ floatx4 up_sum[kWave];
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -84,13 +90,14 @@ __global__ __launch_bounds__(kDenseThreads) void dense_bf16_kernel(DenseArgs a) 
   const BufferView w_view(a.w, static_cast<uint32_t>(static_cast<int64_t>(a.n) * a.k * 2));
   const BufferView x_view(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.rows) * a.x_stride * 2));
   const int r_tile = wave >> 2;  // this wave's weight tile (0: t0, 1: t1)
-  const int t_tile = wave & 3;   // and token tile
+  const int kq = wave & 3;       // and quarter of each chunk's K columns
 
-  for (int m0 = 0; m0 < a.rows; m0 += kDenseTokens) {
+  {
+    const int m0 = blockIdx.y * kDenseTokens;
     // staging of chunk c: thread loads x parts q = tid + 512 i (row q / 32,
     // part q % 32) and W parts likewise (rows 0-15: tile t0, 16-31: t1);
     // the next two chunks are in flight in registers (set c % 2) while chunk
-    // c is multiplied from LDS (a third measured no faster).
+    // c is multiplied from LDS.
     constexpr int kSets = chunks < 2 ? chunks : 2;
     int4 xr[kSets][kXLoads], wr[kSets][kWLoads];
     auto load_chunk = [&](int c, int set) {
@@ -133,9 +140,9 @@ __global__ __launch_bounds__(kDenseThreads) void dense_bf16_kernel(DenseArgs a) 
       __builtin_amdgcn_sched_barrier(0);
       const uint8_t* xb = xs[c & 1];
       const uint8_t* wb = wsm[c & 1];
-      const int xrow = 16 * t_tile + row16, wrow = 16 * r_tile + row16;
+      const int xrow = row16, wrow = 16 * r_tile + row16;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s = 2 * kq; s < 2 * kq + 2; ++s) {
         const int p = 4 * s + quarter;  // k = 32 s + 8 quarter .. + 8
         const int32x4 av = *reinterpret_cast<const int32x4*>(&wb[lds_part(wrow, p)]);
         const int32x4 bv = *reinterpret_cast<const int32x4*>(&xb[lds_part(xrow, p)]);
@@ -144,23 +151,32 @@ __global__ __launch_bounds__(kDenseThreads) void dense_bf16_kernel(DenseArgs a) 
       if (c + 1 < chunks) store_chunk((c + 1) % kSets, (c + 1) & 1);
       __syncthreads();
     }
-    // lane holds rows 16 tile + 4 quarter .. + 3 of token m0 + 16 t_tile + row16
-    const int token = m0 + 16 * t_tile + row16;
+    // The quarters' sums meet in LDS and the first wave of each W tile adds
+    // them in quarter order; lane holds rows 16 tile + 4 quarter .. + 3 of
+    // token m0 + row16.
+    quarter_sum[r_tile][kq][lane] = acc;
+    __syncthreads();
+    const int token = m0 + row16;
     const int tile = r_tile ? t1 : t0;
-    float rounded[4];
+    float rounded[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (kq == 0) {
+      floatx4 sum = quarter_sum[r_tile][0][lane];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rounded[i] = bf16_to_f32(f32_to_bf16(acc[i]));
-    if (token < a.rows && (r_tile == 0 || second)) {
-      const uint32_t lo = f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
-      const uint32_t hi = f32_to_bf16(acc[2]) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16);
-      *reinterpret_cast<uint2*>(a.out + static_cast<int64_t>(token) * a.out_stride + tile * 16 + 4 * quarter) =
-          make_uint2(lo, hi);
+      for (int q = 1; q < 4; ++q) sum += quarter_sum[r_tile][q][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rounded[i] = bf16_to_f32(f32_to_bf16(sum[i]));
+      if (token < a.rows && (r_tile == 0 || second)) {
+        const uint32_t lo = f32_to_bf16(sum[0]) | (static_cast<uint32_t>(f32_to_bf16(sum[1])) << 16);
+        const uint32_t hi = f32_to_bf16(sum[2]) | (static_cast<uint32_t>(f32_to_bf16(sum[3])) << 16);
+        *reinterpret_cast<uint2*>(a.out + static_cast<int64_t>(token) * a.out_stride + tile * 16 + 4 * quarter) =
+            make_uint2(lo, hi);
+      }
+      if (r_tile == 1) up_sum[lane] = floatx4{rounded[0], rounded[1], rounded[2], rounded[3]};
     }
     if (b < a.pairs && a.act != nullptr) {  // uniform over the workgroup
-      if (r_tile == 1) up_sum[t_tile][lane] = floatx4{rounded[0], rounded[1], rounded[2], rounded[3]};
       __syncthreads();
-      if (r_tile == 0 && token < a.rows) {
-        const floatx4 up4 = up_sum[t_tile][lane];
+      if (kq == 0 && r_tile == 0 && token < a.rows) {
+        const floatx4 up4 = up_sum[lane];
         const float up[4] = {up4[0], up4[1], up4[2], up4[3]};
         float v[4];
         silu_mul_values<4>(rounded, up, v);
@@ -169,7 +185,6 @@ __global__ __launch_bounds__(kDenseThreads) void dense_bf16_kernel(DenseArgs a) 
         *reinterpret_cast<uint2*>(a.act + static_cast<int64_t>(token) * a.act_stride + t0 * 16 + 4 * quarter) =
             make_uint2(lo, hi);
       }
-      __syncthreads();
     }
   }
 }
@@ -209,7 +224,7 @@ extern "C" int d3_dense_bf16(const uint16_t* x, int64_t x_stride, int32_t rows, 
   const int pairs = pair_rows / 16;
   const int rest = n / 16 - 2 * pairs;
   const DenseArgs args{x, x_stride, rows, w, n, k, out, out_stride, pairs, pair_rows, act, act_stride};
-  const dim3 grid(pairs + (rest + 1) / 2), block(kDenseThreads);
+  const dim3 grid(pairs + (rest + 1) / 2, (rows + kDenseTokens - 1) / kDenseTokens), block(kDenseThreads);
   hipStream_t s = as_stream(stream);
   switch (k / kDenseChunk) {
     case 1: hipLaunchKernelGGL(dense_bf16_kernel<1>, grid, block, 0, s, args); break;
