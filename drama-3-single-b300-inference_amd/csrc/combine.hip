@@ -207,6 +207,11 @@ __global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLog
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int width = a.width;
   const int64_t base = static_cast<int64_t>(row) * width;
+  // without the norm, workgroup (row, slice) takes the row's columns
+  // [slice * 4 * blockDim, (slice + 1) * 4 * blockDim) and recomputes the
+  // row's routing
+  const int span = static_cast<int>(blockDim.x) * 4;
+  const int column0 = static_cast<int>(blockIdx.y) * span * kChunks;
   RouteLogits<NPL> logits;
   if (wave == 0)
     load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
@@ -216,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLog
   float s[kChunks][4], res[kChunks][4];
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
-    const int column = threadIdx.x * 4 + c * kThreads * 4;
+    const int column = column0 + threadIdx.x * 4 + c * span;
     const bool inside = column < width;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -235,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLog
     const RouteChoice choice = route_top_k<NPL>(logits, a.num_experts, a.top_k);
     if (lane < a.top_k) {
       route_w[lane] = stored_weight(choice.weight, a.weights_f32);
-      if (a.weights != nullptr) {
+      if (a.weights != nullptr && blockIdx.y == 0) {
         const int64_t index = static_cast<int64_t>(row) * a.top_k + lane;
         if (a.weights_f32)
           static_cast<float*>(a.weights)[index] = choice.weight;
@@ -249,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLog
   float squares = 0.0f;
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
-    const int column = threadIdx.x * 4 + c * kThreads * 4;
+    const int column = column0 + threadIdx.x * 4 + c * span;
     if (column >= width) continue;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
@@ -283,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLog
     const float inv = 1.0f / sqrtf(total / static_cast<float>(width) + a.eps);
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
-      const int column = threadIdx.x * 4 + c * kThreads * 4;
+      const int column = column0 + threadIdx.x * 4 + c * span;
       if (column >= width) continue;
       float w[4], v[4];
       load4(a.norm + column, w);
@@ -296,10 +301,16 @@ __global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLog
 
 template <int NPL, bool kF32, bool kNorm>
 void launch_route_logits(const RouteLogitArgs& a, int rows, hipStream_t s) {
-  if (a.width <= kThreads * 4)
+  if constexpr (!kNorm) {  // 512-column slices: a decode batch's rows alone leave most CUs idle
+    constexpr int kSliceThreads = 128;
+    const int slices = (a.width + kSliceThreads * 4 - 1) / (kSliceThreads * 4);
+    hipLaunchKernelGGL((combine_route_logits_kernel<NPL, kF32, kNorm, 1>), dim3(rows, slices),
+                       dim3(kSliceThreads), 0, s, a);
+  } else if (a.width <= kThreads * 4) {
     hipLaunchKernelGGL((combine_route_logits_kernel<NPL, kF32, kNorm, 1>), dim3(rows), dim3(kThreads), 0, s, a);
-  else
+  } else {
     hipLaunchKernelGGL((combine_route_logits_kernel<NPL, kF32, kNorm, 2>), dim3(rows), dim3(kThreads), 0, s, a);
+  }
 }
 
 template <int NPL>
