@@ -138,11 +138,12 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
         if (kb >= kb0 && kb < kb1)
           a_frag[rt][kb] = load_packed_fragment(wexp + static_cast<size_t>(n0_of(tile) + rt * 16) * K, kb, lane);
   };
-  auto load_scales = [&](int tile) {
+  auto load_scales = [&](int tile, int kb0 = 0, int kb1 = KB) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) w_scale[rt][kb] = wsexp[((n0_of(tile) + rt * 16) / kGroup) * KB + kb];
+      for (int kb = 0; kb < KB; ++kb)
+        if (kb >= kb0 && kb < kb1) w_scale[rt][kb] = wsexp[((n0_of(tile) + rt * 16) / kGroup) * KB + kb];
   };
 
   int routes;
@@ -489,7 +490,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           const floatx4 partial = mfma_block_bf16(a_frag[rt][kb], b_wide);
-          acc[rt] += partial * (w_scale[rt][kb] * b_scale);
+          scale_accumulate(acc[rt], partial, w_scale[rt][kb] * b_scale);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           const floatx4 partial = mfma_fp8(a_frag[rt][kb], b_frag);
-          acc[rt] += partial * (w_scale[rt][kb] * b_scale);
+          scale_accumulate(acc[rt], partial, w_scale[rt][kb] * b_scale);
         }
       }
     }
@@ -542,7 +543,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     // tt + 1 is loaded into its registers while the second half of tile tt
     // is multiplied, and so on, so every wave keeps at least half a tile of
     // loads in flight until its last tile (memory returns are counted in
-    // issue order, so each wait covers only the half it needs).
+    // issue order, so each wait covers only the half it needs).  A half's
+    // block scales load with its weights: loaded after the second half,
+    // they would make the first half's wait cover the whole tile.
 #pragma unroll
     for (int tt = 0; tt < TILES; ++tt) {
       floatx4 acc[RT];
@@ -552,12 +555,13 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       if (tt + 1 < TILES) {
         __builtin_amdgcn_sched_barrier(0);  // the next half reuses these registers
         load_weights(first_tile + tt + 1, 0, kFirstHalf);
+        load_scales(first_tile + tt + 1, 0, kFirstHalf);
       }
       mma_range(acc, kFirstHalf, KB);
       if (tt + 1 < TILES) {
         __builtin_amdgcn_sched_barrier(0);
         load_weights(first_tile + tt + 1, kFirstHalf, KB);
-        load_scales(first_tile + tt + 1);
+        load_scales(first_tile + tt + 1, kFirstHalf, KB);
       }
       epilogue(acc, first_tile + tt);
     }
@@ -775,6 +779,7 @@ int check_expert_gemm(int32_t mode, const uint8_t* w, const float* ws, int32_t n
   args.capacity = capacity;
   args.top_k = top_k;
   args.exact_routes = exact_routes;
+  args.num_experts = num_experts;
   args.ids = ids;
   args.row_count = row_count;
   args.act = a;

@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           const floatx4 partial = mfma_block_bf16(a_frag[rt][kb], b_wide);
-          acc[rt] += partial * (w_scale[rt][kb] * b_scale);
+          scale_accumulate(acc[rt], partial, w_scale[rt][kb] * b_scale);
         }
         // Keep one K block's widened operands live at a time (the weights
         // already occupy most of the register file).
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           const floatx4 partial = mfma_fp8(a_frag[rt][kb], b_frag);
-          acc[rt] += partial * (w_scale[rt][kb] * b_scale);
+          scale_accumulate(acc[rt], partial, w_scale[rt][kb] * b_scale);
         }
       }
     }

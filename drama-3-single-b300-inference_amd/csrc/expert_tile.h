@@ -83,6 +83,18 @@ __device__ __forceinline__ floatx4 mfma_fp8(const int32x8& a, const int32x8& b) 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
 }
 
+// acc += partial * scale with one fused multiply-add per element: the
+// per-K-block rescale of every expert GEMM.  Spelled out rather than left to
+// the compiler's contraction, which it may skip where the add ends up in
+// another basic block than the product (two roundings instead of one): the
+// expert kernels agree bit for bit only with the same rounding everywhere.
+__device__ __forceinline__ void scale_accumulate(floatx4& acc, const floatx4& partial, float scale) {
+  acc[0] = fmaf(partial[0], scale, acc[0]);
+  acc[1] = fmaf(partial[1], scale, acc[1]);
+  acc[2] = fmaf(partial[2], scale, acc[2]);
+  acc[3] = fmaf(partial[3], scale, acc[3]);
+}
+
 // 32 e4m3 bytes -> 4 x 8 bf16, exactly (scale 1.0).  Element i of part j is
 // byte 8j + i, for both operands alike.
 __device__ __forceinline__ void widen_fp8(const int32x8& v, bf16x8 out[4]) {

@@ -361,7 +361,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
       if (rt > 0) {
 #pragma unroll
         for (int t = 0; t < kGgWaveTiles; ++t) {
-          acc[t][rt - 1] += partial[(rt - 1) & 1][t] * (wsc[t] * as_prev);
+          scale_accumulate(acc[t][rt - 1], partial[(rt - 1) & 1][t], wsc[t] * as_prev);
           // Materialise the sum here: the accumulators are only used under
           // the epilogue's per-route conditions, and without this the
           // compiler sinks every K block's FMAs (keeping every product live).
