@@ -179,6 +179,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     __builtin_amdgcn_sched_barrier(0);
     // 2. The first half of the first weight tile streams meanwhile.
     load_weights(first_tile, 0, kFirstHalf);
+    load_scales(first_tile, 0, kFirstHalf);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. Occupied slots (every wave holds the masks) and this expert's rank
@@ -306,6 +307,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     const int rows = live_rows(a.row_count, capacity);
     // 2. The first half of the first weight tile streams meanwhile.
     load_weights(first_tile, 0, kFirstHalf);
+    load_scales(first_tile, 0, kFirstHalf);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. This expert's route list, in ascending pair order: pair p = j * 256 +
@@ -534,7 +536,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   fetch_tile(0);
   __builtin_amdgcn_sched_barrier(0);
   load_weights(first_tile, kFirstHalf, KB);
-  load_scales(first_tile);
+  load_scales(first_tile, kFirstHalf, KB);
   store_tile();
   __syncthreads();
   if constexpr (TILES > 1) {
