@@ -103,6 +103,7 @@ constexpr int kMixedMaxRows = 8192;   // row space with prefix reuse (LDS owner 
 constexpr int kMixedMaxPrompts = 16;  // prompts compared for prefix reuse
 constexpr int kMixedMaxBounds = 1025; // boundaries staged in LDS (1024 sequences)
 constexpr int kMixedMaxCodes = 16;    // frame codes compared from registers
+constexpr int kMixedMaxPairs = kMixedMaxPrompts * (kMixedMaxPrompts - 1) / 2;  // 120
 
 // Exclusive rank of `flag` among the workgroup's threads (thread order) and
 // the workgroup's total.  Two barriers; `wave_counts` is free again on return.
@@ -150,6 +151,7 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
   __shared__ int starts[kMixedMaxPrompts + 1];
   __shared__ int common[kMixedMaxPrompts * kMixedMaxPrompts];
   __shared__ int bounds[kMixedMaxBounds];
+  __shared__ int first[kMixedMaxPairs + 1];
   const int tid = static_cast<int>(threadIdx.x);
   const int full = decode_rows + capacity;
   const bool reuse = frames != nullptr && prompts >= 2;
@@ -208,36 +210,51 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
       const int li = starts[i + 1] - starts[i], lj = starts[j + 1] - starts[j];
       common[i * kMixedMaxPrompts + j] = li < lj ? li : lj;
     }
+    // Every (pair, row) comparison of all pairs at once, one per thread
+    // (flat index f = first[q] + p, first[] the pairs' running row counts),
+    // so the frames cost one memory round trip per 1024 rows rather than
+    // one per 64 rows of each pair.
     __syncthreads();
-    const int wave = tid / kWave;
-    for (int q = wave; q < pairs; q += kMixedWaves) {
+    if (tid == 0) {
+      int sum = 0;
+      for (int q = 0; q < pairs; ++q) {
+        int i = 1, base = 0;
+        while (base + i <= q) base += i++;
+        first[q] = sum;
+        sum += common[i * kMixedMaxPrompts + (q - base)];
+      }
+      first[pairs] = sum;
+    }
+    __syncthreads();
+    const int compares = first[pairs];
+    for (int f = tid; f < compares; f += kMixedThreads) {
+      int q = 0;  // the pair holding f: last q with first[q] <= f
+      for (int step = 64; step >= 1; step >>= 1)  // pairs <= 120 < 128
+        if (q + step < pairs && first[q + step] <= f) q += step;
       int i = 1, base = 0;
       while (base + i <= q) base += i++;
       const int j = q - base;
-      const int li = starts[i + 1] - starts[i], lj = starts[j + 1] - starts[j];
-      const int limit = li < lj ? li : lj;
-      for (int p = lane_id(); p < limit; p += kWave) {
-        const int64_t* a = frames + static_cast<int64_t>(starts[i] + p) * codes;
-        const int64_t* b = frames + static_cast<int64_t>(starts[j] + p) * codes;
-        bool differ = false;
-        if (codes <= kMixedMaxCodes) {
-          // Issue every load of both rows before the first compare (a loop
-          // that compares as it loads waits a round trip per code).
-          int64_t va[kMixedMaxCodes], vb[kMixedMaxCodes];
+      const int p = f - first[q];
+      const int64_t* a = frames + static_cast<int64_t>(starts[i] + p) * codes;
+      const int64_t* b = frames + static_cast<int64_t>(starts[j] + p) * codes;
+      bool differ = false;
+      if (codes <= kMixedMaxCodes) {
+        // Issue every load of both rows before the first compare (a loop
+        // that compares as it loads waits a round trip per code).
+        int64_t va[kMixedMaxCodes], vb[kMixedMaxCodes];
 #pragma unroll
-          for (int c = 0; c < kMixedMaxCodes; ++c)
-            if (c < codes) {
-              va[c] = a[c];
-              vb[c] = b[c];
-            }
+        for (int c = 0; c < kMixedMaxCodes; ++c)
+          if (c < codes) {
+            va[c] = a[c];
+            vb[c] = b[c];
+          }
 #pragma unroll
-          for (int c = 0; c < kMixedMaxCodes; ++c)
-            if (c < codes) differ |= va[c] != vb[c];
-        } else {
-          for (int c = 0; c < codes; ++c) differ |= a[c] != b[c];
-        }
-        if (differ) atomicMin(&common[i * kMixedMaxPrompts + j], p);
+        for (int c = 0; c < kMixedMaxCodes; ++c)
+          if (c < codes) differ |= va[c] != vb[c];
+      } else {
+        for (int c = 0; c < codes; ++c) differ |= a[c] != b[c];
       }
+      if (differ) atomicMin(&common[i * kMixedMaxPrompts + j], p);
     }
     __syncthreads();
     for (int i = 1; i < prompts; ++i) {
