@@ -35,10 +35,13 @@ __device__ __forceinline__ void store4(uint16_t* p, const float v[4]) {
 
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
-// bf16(sigmoid(fp32 gate)) (kernels.py:434-438).
-__device__ __forceinline__ float gate_bf16(const uint16_t* gate, int64_t stride, int row) {
-  const float g = bf16_to_f32(gate[static_cast<int64_t>(row) * stride]);
+// bf16(sigmoid(fp32 gate)) (kernels.py:434-438), of the gate's bf16 bits.
+__device__ __forceinline__ float gate_sigmoid_bf16(uint16_t bits) {
+  const float g = bf16_to_f32(bits);
   return round_bf16(1.0f / (1.0f + expf(-g)));
+}
+__device__ __forceinline__ float gate_bf16(const uint16_t* gate, int64_t stride, int row) {
+  return gate_sigmoid_bf16(gate[static_cast<int64_t>(row) * stride]);
 }
 
 // Single rounding of a*b + c to bf16 for bf16 operands: the fp64 fma is exact
@@ -118,13 +121,25 @@ __global__ __launch_bounds__(kThreads) void add_norm_kernel(
   const int source = inverse != nullptr ? static_cast<int>(inverse[row]) : row;
   const int64_t src = static_cast<int64_t>(source) * width;
   const int64_t dst = static_cast<int64_t>(row) * width;
-  float g = 0.0f;
-  if constexpr (kMode != 0) g = gate_bf16(gate, gate_stride, source);
-  float values[kMaxPerThread];
+  // Every load of a column group (norm weights, residual, shared row, gate,
+  // then the routed rows) is issued before the first value is used, so a
+  // row costs one memory round trip: the gate's sigmoid hoisted above the
+  // row loads, or the residual loaded after the routed sum, each cost one
+  // more.
+  float values[kMaxPerThread], norm[kMaxPerThread];
   float squares = 0.0f;
   int count = 0;
   for (int column = threadIdx.x * 4; column < width; column += kThreads * 4, count += 4) {
-    float r[4], res[4], v[4];
+    float r[4], res[4], v[4], s[4];
+    uint16_t gate_bits = 0;
+    load4(weight + column, &norm[count]);
+    load4(residual + dst + column, res);
+    if constexpr (kMode != 0) {
+      load4(shared + src + column, s);
+      const uint16_t* gate_row = gate;
+      asm volatile("" : "+s"(gate_row));  // loaded here, not hoisted out of the loop and waited for
+      gate_bits = gate_row[static_cast<int64_t>(source) * gate_stride];
+    }
     if constexpr (kMode == 2) {
       const float4 sum = routes.top_k == 8
                              ? combine4_fixed<8>(routes.down, routes.weights, routes.weights_f32,
@@ -138,10 +153,8 @@ __global__ __launch_bounds__(kThreads) void add_norm_kernel(
     } else {
       load4(routed + src + column, r);
     }
-    load4(residual + dst + column, res);
     if constexpr (kMode != 0) {
-      float s[4];
-      load4(shared + src + column, s);
+      const float g = gate_sigmoid_bf16(gate_bits);
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = round_bf16(fma_bf16(s[i], g, r[i]) + res[i]);
     } else {
@@ -159,10 +172,9 @@ __global__ __launch_bounds__(kThreads) void add_norm_kernel(
   const float inv = 1.0f / sqrtf(total / static_cast<float>(width) + eps);
   count = 0;
   for (int column = threadIdx.x * 4; column < width; column += kThreads * 4, count += 4) {
-    float w[4], v[4];
-    load4(weight + column, w);
+    float v[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = values[count + i] * inv * (1.0f + w[i]);
+    for (int i = 0; i < 4; ++i) v[i] = values[count + i] * inv * (1.0f + norm[count + i]);
     store4(out + dst + column, v);
   }
 }

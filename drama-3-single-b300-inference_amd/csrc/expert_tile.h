@@ -242,18 +242,30 @@ __device__ __forceinline__ float4 combine4(const float* down, const void* weight
 }
 
 // combine4 for a compile-time top_k: every route row and weight is loaded
-// before the first FMA; the same rank-order chain, so the same bits.
+// before the first FMA; the same rank-order chain, so the same bits.  The
+// route rows are issued first and the weights' dtype is chosen once for all
+// ranks: a dtype branch per rank made each weight load wait before the next
+// rank's loads were issued (one memory round trip per rank).
 template <int kTopK>
 __device__ __forceinline__ float4 combine4_fixed(const float* down, const void* weights,
                                                  int weights_f32, int token, int hidden,
                                                  int column) {
-  float w[kTopK];
   float4 y[kTopK];
 #pragma unroll
-  for (int r = 0; r < kTopK; ++r) {
-    w[r] = route_weight(weights, weights_f32, static_cast<size_t>(token) * kTopK + r);
+  for (int r = 0; r < kTopK; ++r)
     y[r] = *reinterpret_cast<const float4*>(down + (static_cast<size_t>(token) * kTopK + r) * hidden +
                                             column);
+  float w[kTopK];
+  const size_t first = static_cast<size_t>(token) * kTopK;
+  if (weights_f32) {
+#pragma unroll
+    for (int r = 0; r < kTopK; ++r) w[r] = static_cast<const float*>(weights)[first + r];
+  } else {
+    uint16_t raw[kTopK];
+#pragma unroll
+    for (int r = 0; r < kTopK; ++r) raw[r] = static_cast<const uint16_t*>(weights)[first + r];
+#pragma unroll
+    for (int r = 0; r < kTopK; ++r) w[r] = bf16_to_f32(raw[r]);
   }
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
