@@ -224,13 +224,18 @@ __global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLog
   // row's routing
   const int span = static_cast<int>(blockDim.x) * 4;
   const int column0 = static_cast<int>(blockIdx.y) * span * kChunks;
+  // Every load (logits in every wave, the gate, the route rows, shared,
+  // residual and norm weights) is issued before the first value is used:
+  // logits loaded under a wave-0 branch, or the gate and norm weights
+  // loaded after the first use of another load, each cost a memory round
+  // trip of their own.
   RouteLogits<NPL> logits;
-  if (wave == 0)
-    load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
-                                     static_cast<int64_t>(row) * a.logits_stride * (kF32 ? 4 : 2),
-                                 a.num_experts, logits);
+  load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
+                                   static_cast<int64_t>(row) * a.logits_stride * (kF32 ? 4 : 2),
+                               a.num_experts, logits);
+  const uint16_t gate_bits = a.gate[static_cast<int64_t>(row) * a.gate_stride];
   float4 y[kChunks][8];
-  float s[kChunks][4], res[kChunks][4];
+  float s[kChunks][4], res[kChunks][4], norm[kChunks][4];
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
     const int column = column0 + threadIdx.x * 4 + c * span;
@@ -244,10 +249,13 @@ __global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLog
     }
     if (inside) {
       load4(a.shared + base + column, s[c]);
-      if constexpr (kNorm) load4(a.residual + base + column, res[c]);
+      if constexpr (kNorm) {
+        load4(a.residual + base + column, res[c]);
+        load4(a.norm + column, norm[c]);
+      }
     }
   }
-  const float g = gate_bf16(a.gate, a.gate_stride, row);
+  const float g = gate_sigmoid_bf16(gate_bits);
   if (wave == 0) {
     const RouteChoice choice = route_top_k<NPL>(logits, a.num_experts, a.top_k);
     if (lane < a.top_k) {
@@ -302,10 +310,9 @@ __global__ __launch_bounds__(kThreads) void combine_route_logits_kernel(RouteLog
     for (int c = 0; c < kChunks; ++c) {
       const int column = column0 + threadIdx.x * 4 + c * span;
       if (column >= width) continue;
-      float w[4], v[4];
-      load4(a.norm + column, w);
+      float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = values[c][i] * inv * (1.0f + w[i]);
+      for (int i = 0; i < 4; ++i) v[i] = values[c][i] * inv * (1.0f + norm[c][i]);
       store4(a.out + base + column, v);
     }
   }

@@ -685,6 +685,12 @@ __global__ __launch_bounds__(kRoutedCombineThreads) void routed_combine_kernel(R
   const int slice = blockIdx.x % slices;
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) / kWave;
+  // The slot's logits (indexed by slot, so issued before its row is known;
+  // every wave loads them, so no branch makes the first wait come early).
+  RouteLogits<NPL> logits;
+  load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
+                                     static_cast<int64_t>(slot) * a.logits_stride * (kF32 ? 4 : 2),
+                                 a.num_experts, logits);
   // The slot's row: occupied slots below it (every wave counts them).
   int row = 0;
   bool on = false;
@@ -700,11 +706,6 @@ __global__ __launch_bounds__(kRoutedCombineThreads) void routed_combine_kernel(R
     }
   }
   if (!on) return;  // uniform over the workgroup
-  RouteLogits<NPL> logits;
-  if (wave == 0)
-    load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
-                                     static_cast<int64_t>(slot) * a.logits_stride * (kF32 ? 4 : 2),
-                                 a.num_experts, logits);
   const int column = slice * kRoutedCombineColumns + static_cast<int>(threadIdx.x) * 4;
   const bool inside = column < a.hidden;
   float4 y[8];

@@ -164,10 +164,12 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
     // workgroup 0 also writes the ascending slot list.
     const int slot = blockIdx.x;
     load_row_part(a.x + static_cast<int64_t>(slot) * a.x_stride, a.hidden, wave, xrow);
-    if (wave == 0)
-      load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
-                                       static_cast<int64_t>(slot) * a.logits_stride * (kF32 ? 4 : 2),
-                                   a.num_experts, logits);
+    // Every wave loads the logits (only wave 0 routes): under a wave-0
+    // branch their first use waits inside the branch, before the occupancy
+    // loads below are issued.
+    load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
+                                     static_cast<int64_t>(slot) * a.logits_stride * (kF32 ? 4 : 2),
+                                 a.num_experts, logits);
     int running = 0;
     row = 0;
     on = false;
@@ -196,10 +198,9 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
     if (on) {
       const int source = a.row_index != nullptr ? a.row_index[row] : row;
       load_row_part(a.x + static_cast<int64_t>(source) * a.x_stride, a.hidden, wave, xrow);
-      if (wave == 0)
-        load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
-                                         static_cast<int64_t>(source) * a.logits_stride * (kF32 ? 4 : 2),
-                                     a.num_experts, logits);
+      load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
+                                       static_cast<int64_t>(source) * a.logits_stride * (kF32 ? 4 : 2),
+                                   a.num_experts, logits);
     }
   }
 

@@ -49,8 +49,11 @@ __device__ __forceinline__ void load_route_logits(const char* base, int num_expe
   const int lane = lane_id();
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
+    // Lanes past E load the last column and discard it: no branch around
+    // the load, so all NPL loads are in flight before the first wait.
     const int column = lane + j * kWave;
-    logits.values[j] = column < num_experts ? load_logit<kF32>(base, column) : -INFINITY;
+    const float v = load_logit<kF32>(base, column < num_experts ? column : num_experts - 1);
+    logits.values[j] = column < num_experts ? v : -INFINITY;
   }
 }
 
