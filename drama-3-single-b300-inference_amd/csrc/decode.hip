@@ -615,10 +615,12 @@ void launch_tiles(int num_experts, hipStream_t s, const DecodeArgs& a) {
       return;
     }
   }
-  // At least four routes per expert at full capacity: few experts go
-  // without routes, so the whole first tile is issued up front (c2: -0.8 us
-  // per step; at two routes per expert, as for 256 experts, +2.8 us).
-  if (a.capacity * a.top_k >= 4 * num_experts)
+  // Several tiles per workgroup and at least four routes per expert at full
+  // capacity (few experts go without routes): the whole first tile is
+  // issued up front (c2: -0.7 to -1.1 us per step; at two routes per expert,
+  // as for 256 experts, +2.8 us; with one tile per workgroup, as for 16
+  // experts, +1.0 to +1.6 us).
+  if (TILES > 1 && a.capacity * a.top_k >= 4 * num_experts)
     hipLaunchKernelGGL((decode_gemm_kernel<KB, rt_for(KB), MODE, TILES, 1, true>), grid, block, 0, s, a);
   else
     hipLaunchKernelGGL((decode_gemm_kernel<KB, rt_for(KB), MODE, TILES, 1>), grid, block, 0, s, a);
