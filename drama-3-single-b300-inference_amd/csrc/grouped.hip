@@ -184,7 +184,7 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
       wf[kb & 1][t] = v;
     }
   };
-  load_weights(0);  // depends on the item only
+  if constexpr (!kByPair) load_weights(0);  // depends on the item only
 
   if constexpr (kByPair) {
     // The expert's routes in pair order: pair p = 256 j + thread.  Each
@@ -204,6 +204,9 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
         const int p = j * kGgThreads + static_cast<int>(threadIdx.x);
         idv[j] = p < pairs ? static_cast<int>(id_view.load4(static_cast<uint32_t>(p) * 4)) : -1;
       }
+      // The first weight block after the ids: memory returns are counted in
+      // issue order, so the wait for the ids does not cover the weights.
+      load_weights(0);
 #pragma unroll
       for (int j = 0; j < kGgMaxPairChunks; ++j) {
         mine |= (idv[j] == expert ? 1u : 0u) << j;
