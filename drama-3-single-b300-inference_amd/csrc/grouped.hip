@@ -128,11 +128,14 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     pj = 2 * pp + (rem & 1);
     slot = expert * parts + pj;
   } else if (!dense) {
-    if (item_index >= *num_items) return;
+    // The item is read together with the item count (item_index <
+    // max_items: in bounds) and both decide the one early exit, so both
+    // loads are in flight at once: one memory round trip, not two.
     const int4 item = items[item_index];
+    const int count = *num_items;
     expert = item.x;
     first = item.y;
-    routes = min(item.z, kR);
+    routes = item_index < count ? min(item.z, kR) : 0;
     if (routes <= 0) return;  // a padding item (uniform)
   } else {
     first = (item_index - max_items) * kR;
