@@ -293,6 +293,8 @@ int32_t d3_expert_tile_rows(int32_t k);
  * fp8 [2I, hidden] in weight_layout, block scales s13[e]); FC1 is rounded
  * to bf16, a = silu(gate) * up is requantised per 128 columns and written
  * at sorted position p: act fp8 [rows, I], act_scales [rows, I/128].
+ * items holds max_items entries ({e, start, n, -}, the sort's layout); every
+ * one of them may be read, those at or beyond *num_items are ignored.
  * Contraction on FP8 MFMAs with the per-K128 rescale of d3_expert_gemm's
  * FP8 path; act / act_scales equal d3_expert_gemm (mode 0, exact_routes 0)
  * followed by d3_silu_mul_quant, byte for byte.  hidden in {256, 512, 768,
@@ -319,6 +321,7 @@ int d3_grouped_fc1_swiglu(const uint8_t *w13, const float *s13, int32_t weight_l
  * [start, start+n) of act fp8 [act_rows, intermediate] (act_scales
  * [act_rows, intermediate/128]) contract with w2[e] (fp8 [hidden, I]) and
  * are stored fp32 by pair sorted_ids[p]: down [pairs, hidden] (unpermute).
+ * items holds max_items entries, as for d3_grouped_fc1_swiglu.
  * Equal to d3_expert_gemm mode 1 with exact_routes 0, bit for bit.
  * item_rows: upper bound on the routes of one item, <= 128.
  * intermediate in {256, 512, 768, 1024, 1536, 2048}; hidden a multiple of 256.
