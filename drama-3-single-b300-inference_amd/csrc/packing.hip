@@ -152,20 +152,31 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
   __shared__ int common[kMixedMaxPrompts * kMixedMaxPrompts];
   __shared__ int bounds[kMixedMaxBounds];
   __shared__ int first[kMixedMaxPairs + 1];
+  __shared__ int64_t sequence_slot[kMixedMaxBounds - 1];
   const int tid = static_cast<int>(threadIdx.x);
   const int full = decode_rows + capacity;
   const bool reuse = frames != nullptr && prompts >= 2;
   // Every boundary read below goes to this LDS copy (one parallel load; a
   // loop over global boundaries pays a memory round trip per entry).  The
   // compaction's barriers order it before its first use.
+  // The first 1024 slots' occupancy is loaded with the boundaries (at most
+  // 1025 of them: two per thread), every load before the first use: one
+  // memory round trip instead of one for each.
   const int nbounds = (prompts > sequences ? prompts : sequences) + 1;
-  for (int i = tid; i < nbounds; i += kMixedThreads) bounds[i] = boundaries[i];
+  const int bound0 = tid < nbounds ? boundaries[tid] : 0;
+  const int bound1 = tid + kMixedThreads < nbounds ? boundaries[tid + kMixedThreads] : 0;
+  const uint8_t occupancy0 = tid < num_slots ? occupancy[tid] : 0;
+  // the suffix sequences' slots (positions only; sequences <= 1024)
+  const int64_t slot_of = positions != nullptr && tid < sequences ? sequence_slots[tid] : 0;
+  if (tid < nbounds) bounds[tid] = bound0;
+  if (tid + kMixedThreads < nbounds) bounds[tid + kMixedThreads] = bound1;
+  if (positions != nullptr && tid < sequences) sequence_slot[tid] = slot_of;
 
   // 1. slot compaction and decode row slots
   int occupied = 0;
   for (int start = 0; start < num_slots; start += kMixedThreads) {
     const int slot = start + tid;
-    const bool live = slot < num_slots && occupancy[slot] != 0;
+    const bool live = slot < num_slots && (start == 0 ? occupancy0 : occupancy[slot]) != 0;
     int chunk;
     const int at = occupied + block_rank(live, wave_counts, &chunk);
     if (live) {
@@ -279,7 +290,7 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
       int sequence = 0;
       for (int i = 1; i < sequences; ++i) sequence += r >= bounds[i];
       positions[r] = r - bounds[sequence];
-      row_slots[r] = sequence_slots[sequence];
+      row_slots[r] = sequence_slot[sequence];
     }
   }
 
