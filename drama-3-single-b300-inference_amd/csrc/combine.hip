@@ -85,12 +85,16 @@ __global__ __launch_bounds__(kThreads) void combine_experts_kernel(
     const uint16_t* __restrict__ gate, int64_t gate_stride, int width,
     uint16_t* __restrict__ out) {
   const int row = blockIdx.x;
-  const float g = gate_bf16(gate, gate_stride, row);
   const int64_t base = static_cast<int64_t>(row) * width;
   for (int column = threadIdx.x * 4; column < width; column += kThreads * 4) {
     float r[4], s[4], v[4];
     load4(routed + base + column, r);
     load4(shared + base + column, s);
+    // the gate loads with the rows (kept in the loop by the empty asm):
+    // hoisted above them, its sigmoid's wait cost a round trip of its own
+    const uint16_t* gate_row = gate;
+    asm volatile("" : "+s"(gate_row));
+    const float g = gate_bf16(gate_row, gate_stride, row);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = fma_bf16(s[i], g, r[i]);
     store4(out + base + column, v);
