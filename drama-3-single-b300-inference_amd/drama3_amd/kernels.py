@@ -23,11 +23,19 @@ TOP_K = 8
 # shape, options, device and current stream (calls on one stream run in
 # order, so they never share buffers concurrently); the oldest is dropped
 # past _MAX_WORKSPACES.  Outputs are always fresh tensors.
+#
+# Under graph capture a workspace is built fresh and never cached: the
+# constants a workspace fills when it is built (the live row count, the
+# fused-sort ticket) would otherwise be written only inside the graph that
+# built it, and every graph shares torch's capture stream, so a second graph
+# of the same shape replayed before the first would read them unwritten.
 _MAX_WORKSPACES = 16
 _workspaces: dict = {}
 
 
 def _workspace(shape: Shape, device: torch.device, **options) -> MoEWorkspace:
+    if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+        return MoEWorkspace(shape, device, **options)
     stream = torch.cuda.current_stream(device).cuda_stream if device.type == "cuda" else 0
     key = (str(device), stream, shape.rows, shape.num_experts, shape.hidden, shape.intermediate,
            shape.top_k, tuple(sorted(options.items())))

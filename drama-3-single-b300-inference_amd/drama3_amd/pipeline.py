@@ -598,12 +598,10 @@ def moe_with_shared(ws: MoEWorkspace, dense: DenseExpert | None, x, logits, expe
     else:
         side.wait_stream(main)  # q / x_scales are ready
         shared_y = dense.forward(ws.q, ws.x_scales, shared_experts, stream=side.cuda_stream)
-    if ws.grouped:
-        ws.grouped_fc1(experts, stream=stream)
-        ws.grouped_fc2(experts, stream=stream)
-    else:
-        ws.fc1(experts, stream)
-        ws._fc2_stage(experts, stream)
+    # The routed experts as the workspace's front left them: sorted items, or
+    # (by-pair workspaces, whose front skips the sort) the by-pair FC1 and
+    # the FC2 over the route list it writes.
+    ws.routes_down(experts, row_count, stream)
     if side is not None:
         main.wait_stream(side)
     return ws.combine(None, row_count, shared_y, out, stream)

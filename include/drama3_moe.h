@@ -489,7 +489,7 @@ int d3_decode_step(const uint8_t *w13, const float *s13, const uint8_t *w2, cons
                    int32_t *active, int32_t *count, uint16_t *out, void *stream);
 
 /*
- * A1-A12  d3_decode_step without a caller workspace, for callers that
+ * d3_decode_step on the library's static device scratch, for callers that
  * cannot allocate device memory (code under graph capture, serving loops
  * that forbid allocation); it has no counterpart in the reference.  The
  * intermediate buffers (ids, route weights in the logits' dtype, gate_up,

@@ -165,6 +165,54 @@ def test_decode_step_entry_points_check_before_launching(lib):
                   8, 64, None, 16, 0, 16, 16, 16, 16, 16, None)
 
 
+def test_decode_gemm_contract(lib):
+    """Every call is rejected by the host checks before a launch (the
+    pointers are aligned dummies, never dereferenced)."""
+    from drama3_amd import _lib
+
+    with pytest.raises(ValueError, match="mode"):
+        _lib.call("d3_decode_expert_gemm", 1, 16, 16, 4, 512, 1024, 16, None, 64, 8, 16, 16, 64,
+                  16, None, None)
+    with pytest.raises(ValueError, match="capacity"):
+        _lib.call("d3_decode_expert_gemm", 0, 16, 16, 4, 512, 1024, 16, None, 300, 8, 16, 16, 64,
+                  16, None, None)
+    with pytest.raises(ValueError, match="K=768"):
+        _lib.call("d3_decode_expert_gemm", 0, 16, 16, 4, 512, 768, 16, None, 64, 8, 16, 16, 64,
+                  16, None, None)
+
+
+def test_route_fc1_and_combine_contract(lib):
+    from drama3_amd import _lib
+
+    p = 256  # any aligned non-null address: every call below is rejected before a launch
+    fc1 = [p, p, 128, 1536, 2048, p, 64, p, 2048, p, _lib.DTYPE_BF16, 128, 8, 16, p, p, p, p, None]
+    bad = list(fc1)
+    bad[3 - 1] = 300  # E above what a workgroup ranks
+    with pytest.raises(ValueError, match="E=300"):
+        _lib.call("d3_decode_route_fc1", *bad)
+    bad = list(fc1)
+    bad[11] = 130  # logits rows not 16-byte aligned
+    with pytest.raises(ValueError, match="aligned"):
+        _lib.call("d3_decode_route_fc1", *bad)
+    bad = list(fc1)
+    bad[6] = 300  # capacity
+    with pytest.raises(ValueError, match="capacity"):
+        _lib.call("d3_decode_route_fc1", *bad)
+    bad = list(fc1)
+    bad[10] = _lib.DTYPE_I32
+    with pytest.raises(ValueError, match="logits"):
+        _lib.call("d3_decode_route_fc1", *bad)
+    combine = [p, 64, p, _lib.DTYPE_BF16, 128, 128, 8, 2048, p, p, _lib.DTYPE_BF16, p, None]
+    bad = list(combine)
+    bad[6] = 9  # top_k above 8
+    with pytest.raises(ValueError, match="top_k"):
+        _lib.call("d3_decode_route_combine", *bad)
+    bad = list(combine)
+    bad[0] = None
+    with pytest.raises(ValueError, match="null"):
+        _lib.call("d3_decode_route_combine", *bad)
+
+
 def test_product_code_does_not_import_the_oracle():
     package = ROOT / "drama-3-single-b300-inference_amd"
     for path in package.rglob("*.py"):

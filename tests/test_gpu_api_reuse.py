@@ -79,3 +79,37 @@ def test_routed_moe_small_batch_without_sort_matches_sorted(device):
     want = sorted_ws.forward(xd, ld, experts, out=torch.empty_like(got))
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_routed_moe_graphs_of_one_shape_replay_in_any_order(device):
+    """Two graphs that capture routed_moe at the same shape (a by-pair
+    workspace, whose live row count is a device constant written when the
+    workspace is built): under capture each gets a workspace of its own, none
+    is cached, and the second graph replayed before the first gives the eager
+    result."""
+    from drama3_amd import kernels, workloads
+    from drama3_amd.kernels import routed_moe
+
+    w = workloads.config5()
+    x, logits = w.steps[0].packed()
+    rows = 560
+    xd, ld = x[:rows].to(device), logits[:rows].to(device)
+    experts = w.experts.to(device)
+    kernels._workspaces.clear()
+    want = routed_moe(xd, ld, experts, True).clone()
+    kernels._workspaces.clear()
+    torch.cuda.synchronize()
+    graphs, outs = [], []
+    for _ in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(routed_moe(xd, ld, experts, True))
+        graphs.append(g)
+    assert len(kernels._workspaces) == 0  # nothing built under capture is cached
+    for order in ((1, 0), (0, 1), (1, 1)):
+        for k in order:
+            outs[k].zero_()
+            torch.cuda.synchronize()
+            graphs[k].replay()
+            torch.cuda.synchronize()
+            assert torch.equal(outs[k].view(torch.int16), want.view(torch.int16)), f"graph {k}"

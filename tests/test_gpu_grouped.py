@@ -267,3 +267,44 @@ def test_grouped_by_pair_matches_sorted(device, shape):
     assert torch.equal(pair_ws.down[:live_pairs].view(torch.int32),
                        sorted_ws.down[:live_pairs].view(torch.int32))
     assert bool((pair_ws.down[live_pairs:] == 7.0).all())
+
+
+def test_moe_with_shared_on_by_pair_workspace(device):
+    """moe_with_shared on a by-pair workspace (its front skips the route
+    sort): the routed experts run the by-pair FC1 and the FC2 over the route
+    list it writes, so the result equals the sorted workspace's byte for
+    byte, eagerly and after several replays of a captured graph."""
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.pipeline import DenseExpert, MoEWorkspace, Shape, moe_with_shared
+
+    rows, e, h, i = 560, 16, 1024, 256
+    gen = torch.Generator("cpu").manual_seed(41)
+    w = workloads.make_experts(gen, e, h, i)
+    sw = workloads.make_experts(gen, 1, h, i)
+    x = workloads._bf16(gen, (rows, h)).to(device)
+    logits = workloads._bf16(gen, (rows, e)).to(device)
+    experts, shared = prepare_experts(w.to(device)), prepare_experts(sw.to(device))
+    sorted_ws = MoEWorkspace(Shape(rows, e, h, i), device, item_rows=128, grouped=True)
+    pair_ws = MoEWorkspace(Shape(rows, e, h, i), device, item_rows=128, grouped=True, by_pair=True)
+    dense = DenseExpert(rows, h, i, device)
+    expected = moe_with_shared(sorted_ws, dense, x, logits, experts, shared).clone()
+    # stale sorted-route buffers must not matter on the by-pair workspace
+    pair_ws.sorted_ids.fill_(-1)
+    pair_ws.items.fill_(-1)
+    pair_ws.num_items.fill_(1 << 20)
+    got = moe_with_shared(pair_ws, dense, x, logits, experts, shared).clone()
+    torch.cuda.synchronize()
+    print(f"by-pair moe_with_shared rows {rows} E {e}: "
+          f"{int(pair_ws.list_count.item())} listed items", flush=True)
+    assert torch.equal(got, expected)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = moe_with_shared(pair_ws, dense, x, logits, experts, shared)
+    for replay in range(3):
+        pair_ws.out.zero_()
+        pair_ws.down.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, expected), f"replay {replay}"

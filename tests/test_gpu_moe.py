@@ -59,6 +59,38 @@ def test_decode_configs(device, config):
     print(f"config {config}: rows {n} {stats}")
 
 
+@pytest.mark.parametrize("config", [1, 2, 3])
+def test_decode_configs_benched_path(device, config):
+    """The step bench.py times: fragment-major weights (prepare_experts), so
+    DecodeStep runs its three launches (FC1 routing and quantising the slots,
+    FC2 finding its routes, routed combine) with no front and no route sort;
+    against the oracle directly."""
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.pipeline import DecodeStep
+
+    w = workloads.CONFIGS[config]()
+    step = w.steps[0]
+    experts = prepare_experts(w.experts.to(device))
+    ds = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device)
+    occ, xs, ls = (step.occupancy.to(device), step.x_slots.to(device),
+                   step.logits_slots.to(device))
+    assert ds.uses_sortless(experts) and ds.uses_frontless(occ, xs, ls)
+    out = ds(occ, xs, ls, experts)
+    torch.cuda.synchronize()
+    active, n = om.compact_slots(step.occupancy.numpy())
+    assert int(ds.count.item()) == n
+    assert np.array_equal(ds.active.cpu().numpy()[:n], active)
+    weights, ids = om.route(np_f32(step.logits_slots)[active])
+    assert np.array_equal(ds.workspace.ids.cpu().numpy()[:n], ids)
+    # routing weights: fp32 exp / sums in another order, within one bf16 ulp
+    got_w, want_w = np_f32(ds.workspace.weights)[:n], bf16_to_f32(weights)
+    assert np.all(np.abs(got_w - want_w) <= np.abs(want_w) * 2.0**-8 + 1e-7)
+    expected = om.expert_ffn(np_bf16(step.x_slots)[active], ids, weights, oracle_weights(w.experts))
+    stats = assert_bf16_close(np_bf16(out)[:n], expected, **EXACT)
+    print(f"config {config} (benched step): rows {n} {stats}")
+
+
 def test_prefill_with_shared_expert(device):
     """Config 4: 16 packed prompts (cu_seqlens), routed + dense FP8 shared expert."""
     from drama3_amd import workloads

@@ -91,3 +91,54 @@ def test_static_step_rejects_sizes_beyond_its_scratch(device):
                   _lib.stream(device))
     torch.cuda.synchronize()
     assert int(count.item()) == -7  # nothing was launched
+
+
+def test_static_step_captured_in_a_graph_replays_with_new_occupancy(device):
+    """d3_decode_step_static captured in a graph (the callers it is for):
+    the first call on the device, which looks up the scratch address, runs
+    before the capture; the graph is then replayed twice with a different
+    occupancy copied into the captured input each time, and every replay's
+    outputs equal d3_decode_step's on a caller workspace byte for byte."""
+    from drama3_amd import _lib
+    from drama3_amd.pipeline import DTYPE_BF16, EXACT_ROUTES
+
+    ex, occ, x, logits = _case(device, 43, 64, 128, 2048, 768, 0.75)
+    slots, hidden = x.shape
+    experts, inter, top_k = logits.shape[1], ex.w2_weight.shape[2], 8
+    common = (*_operands(ex), experts, hidden, inter, occ.data_ptr(), slots, x.data_ptr(),
+              x.stride(0), logits.data_ptr(), DTYPE_BF16, logits.stride(0), top_k, EXACT_ROUTES)
+    active, count, out = _outputs(device, slots, hidden)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):  # eager first call: the scratch lookup happens here
+        _lib.call("d3_decode_step_static", *common, active.data_ptr(), count.data_ptr(),
+                  out.data_ptr(), _lib.stream(device))
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _lib.call("d3_decode_step_static", *common, active.data_ptr(), count.data_ptr(),
+                  out.data_ptr(), _lib.stream(device))
+    gen = torch.Generator("cpu").manual_seed(44)
+    for replay, p in enumerate((0.4, 0.9)):
+        occ.copy_((torch.rand(slots, generator=gen) < p).to(torch.uint8))
+        active.fill_(12345)
+        count.fill_(-7)
+        out.fill_(3.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        snapshot = (active.clone(), int(count.item()), out.clone())
+        n = _run_both(device, ex, occ, x, logits)  # the workspace step, fresh buffers
+        assert snapshot[1] == n, f"replay {replay}"
+        ids = torch.empty((slots, top_k), dtype=torch.int32, device=device)
+        weights = torch.empty((slots, top_k), dtype=torch.bfloat16, device=device)
+        gate_up = torch.empty((slots * top_k, 2 * inter), dtype=torch.bfloat16, device=device)
+        down = torch.empty((slots * top_k, hidden), dtype=torch.float32, device=device)
+        active_a, count_a, out_a = _outputs(device, slots, hidden)
+        _lib.call("d3_decode_step", *common, ids.data_ptr(), weights.data_ptr(), DTYPE_BF16,
+                  gate_up.data_ptr(), down.data_ptr(), active_a.data_ptr(), count_a.data_ptr(),
+                  out_a.data_ptr(), _lib.stream(device))
+        torch.cuda.synchronize()
+        assert torch.equal(snapshot[0], active_a), f"replay {replay}"
+        assert np.array_equal(np_bf16(snapshot[2][:n]), np_bf16(out_a[:n])), f"replay {replay}"
