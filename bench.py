@@ -182,6 +182,44 @@ def decode_parity(workload, step, out) -> dict:
             "ok": err < 1e-3}
 
 
+def parity_stats(got_bits, expected_bits, tolerance_rrms: float) -> dict:
+    """RRMS, max-abs and exact fraction of bf16 outputs (uint16 bits) against
+    the oracle's."""
+    import numpy as np
+
+    from oracle.numerics import bf16_to_f32
+
+    a = bf16_to_f32(got_bits).astype(np.float64)
+    b = bf16_to_f32(expected_bits).astype(np.float64)
+    err = float(np.sqrt(np.mean((a - b) ** 2) / np.mean(b ** 2)))
+    return {"rrms_vs_oracle": err, "max_abs": float(np.abs(a - b).max()),
+            "exact_fraction": float(np.mean(got_bits == expected_bits)),
+            "tolerance_rrms": tolerance_rrms, "ok": err < tolerance_rrms}
+
+
+def prefill_parity(workload, x, logits, out) -> dict:
+    """Config 4's output (routed top-8 + the dense shared expert) against the
+    numpy oracle: the FP8-MFMA contraction path, held to the reference's
+    same-quantisation threshold (RRMS < 3e-3)."""
+    import torch
+
+    from oracle import moe as om
+
+    def np_u8(t):
+        return t.view(torch.uint8).numpy()
+
+    ex, sh = workload.experts, workload.shared
+    weights, ids = om.route(logits.float().numpy())
+    xb = x.view(torch.int16).numpy().view("uint16")
+    routed = om.expert_ffn(xb, ids, weights, om.ExpertWeights(
+        np_u8(ex.w13_weight), ex.w13_scale_inv.numpy(), np_u8(ex.w2_weight), ex.w2_scale_inv.numpy()))
+    shared = om.dense_ffn(xb, np_u8(sh.w13_weight[0]), sh.w13_scale_inv[0].numpy(),
+                          np_u8(sh.w2_weight[0]), sh.w2_scale_inv[0].numpy())
+    expected = om.add_shared(routed, shared)
+    got = out.view(torch.int16).cpu().numpy().view("uint16")
+    return parity_stats(got, expected, 3e-3)
+
+
 def bench_decode_config(torch, config: int, replays: int, working_set: float = 6e8) -> dict:
     """A decode configuration's step (config 1: 4 of 64 slots; config 3: all
     64 slots under Zipf-skewed routing; E16 H1024 I256) through DecodeStep:
@@ -234,7 +272,8 @@ def bench_decode_config(torch, config: int, replays: int, working_set: float = 6
                       "MALL: cold); hot: the same graph on one copy"}
 
 
-def bench_prefill(torch, steps: int, copies: int = 2, replays: int = 100) -> dict:
+def bench_prefill(torch, steps: int, copies: int = 2, replays: int = 100,
+                  check_parity: bool = True) -> dict:
     """Config 4: 16 packed prompts (~3.7k rows), routed top-8 FP8 MoE (H2048,
     E128, I768) plus a dense FP8 shared expert: route + quantise, wide route
     sort, tiled grouped FC1 (SwiGLU requant in its epilogue) and FC2 with the
@@ -273,8 +312,9 @@ def bench_prefill(torch, steps: int, copies: int = 2, replays: int = 100) -> dic
         return time_graphs(torch, [g], max(1, steps // reps)) / (reps * len(fns))
 
     for routed, shared in sets:
-        full(routed, shared)
+        out = full(routed, shared)
     torch.cuda.synchronize()
+    parity = prefill_parity(w, x, logits, out) if check_parity else None
     step_us = graph_us([lambda r=r, s=s: full(r, s) for r, s in sets], 2)
 
     def graph_of(pairs):
@@ -313,6 +353,7 @@ def bench_prefill(torch, steps: int, copies: int = 2, replays: int = 100) -> dic
         "fc1_TFLOP_s": round(fc1_flop / stage_us["fc1_swiglu"] / 1e6, 1),
         "fc2_TFLOP_s": round(fc2_flop / stage_us["fc2"] / 1e6, 1),
         "peak_TFLOP_s": FP8_PEAK_TFLOPS, "dtype": "fp8_e4m3 MFMA (fp32 accumulate)",
+        "parity": parity,
         "timing": f"hipGraph, {copies} rotated weight copies (routed + shared, fragment-major)",
     }
 
@@ -402,7 +443,100 @@ def bench_moe_layer(torch, steps: int = 30, copies: int = 3) -> dict:
             "timing": f"hipGraph, {copies} rotated weight copies"}
 
 
-def bench_mixed(torch, steps: int = 50) -> dict:
+def mixed_parity(step, workload, kept: int) -> dict:
+    """The MoE rows of a replayed config-5 mixed step (the kept rows, after
+    prefix reuse) against the numpy oracle: the routed combine of the
+    step's own per-route rows, FP8-MFMA contraction path (RRMS < 3e-3)."""
+    import torch
+
+    from oracle import moe as om
+
+    routed = step.workspace.combine(None, step.rows.keep_count, None, step.routed)
+    torch.cuda.synchronize()
+    rows = step.rows.keep.cpu().numpy()[:kept]
+    x = step.x.view(torch.int16).cpu().numpy().view("uint16")[rows]
+    weights, ids = om.route(step.logits.float().cpu().numpy()[rows])
+    ex = workload.experts
+    expected = om.expert_ffn(x, ids, weights, om.ExpertWeights(
+        ex.w13_weight.view(torch.uint8).numpy(), ex.w13_scale_inv.numpy(),
+        ex.w2_weight.view(torch.uint8).numpy(), ex.w2_scale_inv.numpy()))
+    got = routed[:kept].view(torch.int16).cpu().numpy().view("uint16")
+    return {**parity_stats(got, expected, 3e-3), "rows": kept}
+
+
+def bench_moe_layer_prefill(torch, rows: int = 4096, steps: int = 20, copies: int = 2) -> dict:
+    """``MoELayer`` at a prefill-sized batch (4096 packed rows) of the
+    reference model's shape (H2048, E256, I512, shared I512): the tiled bf16
+    projection (SwiGLU in its epilogue) and shared down projection on
+    d3_dense_bf16, the routed experts on the prefill path (wide route sort,
+    tiled grouped FP8 GEMMs), the combine; two rotated weight copies.  The
+    two bf16 GEMMs are also timed alone, and next to them the same products
+    through torch.mm (hipBLASLt) for context."""
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.moe_layer import MoELayer, dense_bf16, pack_input_projection
+
+    device = torch.device("cuda:0")
+    e, h, i, si = 256, 2048, 512, 512
+    gen = torch.Generator("cpu").manual_seed(13)
+
+    def bf16(*shape, scale):
+        return (torch.randn(shape, generator=gen) * scale).to(torch.bfloat16).to(device)
+
+    sets = []
+    for _ in range(copies):
+        experts = prepare_experts(workloads.make_experts(gen, e, h, i).to(device))
+        projection = pack_input_projection(bf16(si, h, scale=h ** -0.5), bf16(si, h, scale=h ** -0.5),
+                                           bf16(e, h, scale=1.0), bf16(1, h, scale=h ** -0.5))
+        sets.append((experts, projection, bf16(h, si, scale=si ** -0.5)))
+    x = workloads._bf16(gen, (rows, h)).to(device)
+    layer = MoELayer(rows, e, h, i, si, device=device)
+    for experts, projection, down in sets:
+        layer(x, projection, down, experts)
+    torch.cuda.synchronize()
+
+    def graph_us(fn, reps):
+        for experts, projection, down in sets:  # eager first (library set-up outside capture)
+            fn(experts, projection, down)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                for experts, projection, down in sets:
+                    fn(experts, projection, down)
+        g.replay()
+        torch.cuda.synchronize()
+        return time_graphs(torch, [g], max(1, steps // reps)) / (reps * len(sets))
+
+    layer_us = graph_us(lambda ex, pr, dn: layer(x, pr, dn, ex), 1)
+    out = torch.empty_like(layer.projected)
+    act = torch.empty_like(layer.act)
+    shared = torch.empty_like(layer.shared)
+    proj_us = graph_us(lambda ex, pr, dn: dense_bf16(x, pr, out, si, act), 4)
+    down_us = graph_us(lambda ex, pr, dn: dense_bf16(act, dn, shared), 4)
+    lib_proj_us = graph_us(lambda ex, pr, dn: torch.mm(x, pr.t(), out=out), 4)
+    lib_down_us = graph_us(lambda ex, pr, dn: torch.mm(act, dn.t(), out=shared), 4)
+    n_proj = layer.projected.shape[1]
+    proj_flop, down_flop = 2 * rows * n_proj * h, 2 * rows * h * si
+    return {"workload": f"one MoE layer, {rows} packed rows, H2048 E256 I512 top-8 + bf16 shared "
+                        "expert (I512), packed input projection (the reference model's layer)",
+            "rows": rows, "us_per_layer": round(layer_us, 2),
+            "tokens_per_s": round(rows / (layer_us * 1e-6), 1),
+            "projection_us": round(proj_us, 2),
+            "projection_TFLOP_s": round(proj_flop / proj_us / 1e6, 1),
+            "shared_down_us": round(down_us, 2),
+            "shared_down_TFLOP_s": round(down_flop / down_us / 1e6, 1),
+            "hipblaslt_projection_us": round(lib_proj_us, 2),
+            "hipblaslt_shared_down_us": round(lib_down_us, 2),
+            "peak_bf16_TFLOP_s": 2500.0,
+            "step": "d3_dense_bf16 tiled projection (SwiGLU in its epilogue) -> front + wide route "
+                    "sort + tiled grouped FP8 FC1 / FC2 -> d3_dense_bf16 shared down projection "
+                    "-> routed combine + combine_experts",
+            "timing": f"hipGraph, {copies} rotated weight copies; the GEMMs alone: graphs of 4 "
+                      "launches per copy; hipblaslt_*: torch.mm of the same operands, context only"}
+
+
+def bench_mixed(torch, steps: int = 50, check_parity: bool = True) -> dict:
     """Config 5's mixed step as one captured graph (``MixedStep``): 48 live
     decode slots of 64 (decode bucket 64), two 256-row prompts in a 640-row
     prefill suffix (128 padding rows), E16 H1024 I256 top-8.  Timed twice:
@@ -433,6 +567,7 @@ def bench_mixed(torch, steps: int = 50) -> dict:
     step.residual.copy_(residual)
     step.capture(experts)
     out = {}
+    parity = None
     for name, shared_rows in (("distinct_prompts", 0), ("shared_prefix_128", 128)):
         f = frames.clone()
         f[256:256 + shared_rows] = f[:shared_rows]
@@ -440,13 +575,15 @@ def bench_mixed(torch, steps: int = 50) -> dict:
         step.replay()
         torch.cuda.synchronize()
         kept = int(step.rows.keep_count.item())
+        if name == "distinct_prompts" and check_parity:
+            parity = mixed_parity(step, w, kept)
         us = time_graphs(torch, [step.graph], steps)
         stats = replay_stats(torch, step.graph, max(steps, 100))
         out[name] = {"us_per_step": round(us, 2), "median_us_per_step": round(stats["median_us"], 2),
                      "moe_rows": kept, "tokens_per_s": round((48 + 512) / (us * 1e-6), 1)}
     return {"workload": "config 5 mixed step: 48 of 64 decode slots + 2 x 256 prompt rows "
                         "(640-row suffix), E16 H1024 I256 top-8",
-            "rows": full, "live_rows": 48 + 512, **out,
+            "rows": full, "live_rows": 48 + 512, **out, "parity": parity,
             "step": "d3_mixed_rows (with the suffix's row metadata) + MoE on the kept rows, "
                     "then the routed combine + residual + RMSNorm onto all rows in one launch; "
                     "one hipGraph",
@@ -467,11 +604,13 @@ def main():
     from drama3_amd.pipeline import DecodeStep
 
     if args.prefill_only:
-        print(json.dumps({"prefill": bench_prefill(torch, args.prefill_steps, replays=args.replays)}),
+        print(json.dumps({"prefill": bench_prefill(torch, args.prefill_steps, replays=args.replays,
+                                                   check_parity=not args.no_parity)}),
               flush=True)
         return
     if args.mixed_only:
-        print(json.dumps({"mixed": bench_mixed(torch, args.mixed_steps)}), flush=True)
+        print(json.dumps({"mixed": bench_mixed(torch, args.mixed_steps,
+                                               check_parity=not args.no_parity)}), flush=True)
         return
 
     device = torch.device("cuda:0")
@@ -610,10 +749,14 @@ def main():
                **base}
 
     prefill = None if args.no_prefill else bench_prefill(torch, args.prefill_steps,
-                                                         replays=args.replays)
+                                                         replays=args.replays,
+                                                         check_parity=not args.no_parity)
     reference_shape = None if args.no_reference_shape else bench_reference_shape(torch)
-    mixed = None if args.no_mixed else bench_mixed(torch, args.mixed_steps)
+    mixed = None if args.no_mixed else bench_mixed(torch, args.mixed_steps,
+                                                   check_parity=not args.no_parity)
     moe_layer = None if args.no_reference_shape else bench_moe_layer(torch)
+    if moe_layer is not None and not args.no_prefill:
+        moe_layer["prefill_4096_rows"] = bench_moe_layer_prefill(torch)
 
     result = {
         "metric": baseline_metric(),

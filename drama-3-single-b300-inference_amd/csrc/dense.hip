@@ -1,11 +1,10 @@
-// Dense bf16 GEMM of the MoE layer's small-batch projections (decode-sized
-// row counts): out[M, N] = x[M, K] . W[N, K]^T, fp32 accumulation, one bf16
-// rounding.  Used for the packed input projection (model.py:230-245,
+// Dense bf16 GEMM of the MoE layer's projections: out[M, N] = x[M, K] .
+// W[N, K]^T, fp32 accumulation, one bf16 rounding.  Used for the packed input projection (model.py:230-245,
 // 495-501: shared gate / up rows, router, shared-expert gate), whose
 // epilogue also forms the shared expert's activation silu_mul(gate, up)
 // (kernels.py:386-395), and for the shared expert's down projection.
 //
-// Design (gfx950, wave64, mfma_f32_16x16x32_bf16):
+// Decode-sized row counts (up to 768; gfx950, wave64, mfma_f32_16x16x32_bf16):
 //   * A workgroup owns two 16-row tiles of W and one 16-row tile of x, so a
 //     decode-sized batch spreads over (tile pairs) x (x tiles) workgroups
 //     instead of leaving most CUs idle (64 rows of x per workgroup measured
@@ -27,6 +26,33 @@
 //     j, so it holds both halves of 16 activation columns and writes
 //     act = bf16(bf16(silu(gate)) * up) from the rounded outputs, the bytes
 //     of d3_silu_mul.
+//
+// Prefill-sized row counts (the layer's projections over thousands of packed
+// rows) take a second kernel, tiled for contraction rather than for streaming
+// the weights:
+//   * A workgroup (4 waves, two workgroups per CU) owns a tile of 128 weight
+//     rows by 128 (or 64) x rows; each wave a 64 x 64 (or 64 x 32) part of
+//     it as 4 x 4 (4 x 2) blocks of mfma_f32_16x16x32_bf16, so every
+//     fragment read from LDS feeds four MFMAs.
+//   * K is walked in steps of 64 columns (128 bytes of a row): both operand
+//     tiles are staged global -> registers -> LDS (coalesced 16-byte loads,
+//     8 threads per 128-byte row; 144-byte LDS rows, the 16-byte pad putting
+//     the 16 rows of each ds_read_b128 on distinct banks), the next step's
+//     loads in flight while the current step is multiplied; two LDS slots,
+//     one barrier per step.
+//   * Paired tiles hold 64 gate rows and the matching 64 up rows, so each
+//     lane holds gate and up of the same (row, column) and the epilogue
+//     writes act as the small-batch kernel does.
+//   * Tiles are numbered weight-tile fastest and handed to the XCDs in
+//     contiguous ranges, so the tiles an XCD runs at once share their x rows
+//     (and, a few rows of tiles apart, their weight rows) in that XCD's L2.
+//   * Measured (per-phase timestamps of one wave): a step's 32 KB of global
+//     loads per workgroup take as long to issue as the step's MFMAs, so the
+//     two workgroups of a CU alternate between the two rather than overlap
+//     them; at 4096 x 1408 x 2048 the kernel reaches about 0.2 of the bf16
+//     MFMA peak.  Larger tiles (fewer bytes per MFMA) are the direction.
+#include <type_traits>
+
 #include "common.h"
 #include "expert_tile.h"
 #include "status.h"
@@ -189,6 +215,196 @@ __global__ __launch_bounds__(kDenseThreads) void dense_bf16_kernel(DenseArgs a) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tiled kernel for prefill-sized row counts.
+// ---------------------------------------------------------------------------
+constexpr int kTiledWaves = 4;
+constexpr int kTiledThreads = kTiledWaves * kWave;
+constexpr int kTiledN = 128;                    // weight rows per workgroup tile
+constexpr int kTiledK = 64;                     // K columns per step
+constexpr int kTiledRowBytes = kTiledK * 2;     // 128 bytes of a row per step
+constexpr int kTiledStride = kTiledRowBytes + 16;  // LDS bytes per staged row
+constexpr int kTiledPairRows = kTiledN / 2;     // gate (and up) rows of a paired tile
+constexpr int kTiledXcds = 8;
+constexpr int kTiledMinRows = 769;  // fewer rows (and K in its set): the small-batch kernel
+
+struct TiledGrid {
+  int m_tiles;
+  int n_tiles;
+  int pair_tiles;  // tiles 0 .. pair_tiles-1 are paired (gate rows + up rows)
+  int per_xcd;     // logical tiles per XCD range
+};
+
+// BM: x rows per workgroup (128 or 64).
+template <int BM>
+__global__ __launch_bounds__(kTiledThreads) __attribute__((amdgpu_waves_per_eu(2))) void dense_bf16_tiled_kernel(
+    DenseArgs a, TiledGrid grid) {
+  constexpr int kWM = BM / 2;       // x rows per wave
+  constexpr int kTB = kWM / 16;     // 16-row x blocks per wave
+  constexpr int kFB = 4;            // 16-row weight blocks per wave
+  constexpr int kWLoads = kTiledN * (kTiledRowBytes / 16) / kTiledThreads;  // 4
+  constexpr int kXLoads = BM * (kTiledRowBytes / 16) / kTiledThreads;       // 4 or 2
+  __shared__ __attribute__((aligned(16))) uint8_t wsm[2][kTiledN * kTiledStride];
+  __shared__ __attribute__((aligned(16))) uint8_t xsm[2][BM * kTiledStride];
+
+  // Contiguous logical ranges per XCD (workgroup b runs on XCD b % 8).
+  const int b = blockIdx.x;
+  const int logical = (b % kTiledXcds) * grid.per_xcd + b / kTiledXcds;
+  if (logical >= grid.m_tiles * grid.n_tiles) return;  // uniform
+  const int mt = logical / grid.n_tiles;
+  const int nt = logical - mt * grid.n_tiles;
+  const bool paired = nt < grid.pair_tiles;
+  const int m0 = mt * BM;
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wave & 1;   // x-row half of the tile
+  const int wn = wave >> 1;  // weight-row half
+  const int row16 = lane & 15;
+  const int quarter = lane >> 4;
+
+  // Weight row of LDS row r of this tile (paired: 64 gate rows, then the
+  // matching 64 up rows).
+  auto weight_row = [&](int r) {
+    if (paired) return r < kTiledPairRows ? kTiledPairRows * nt + r : a.pair_offset + kTiledPairRows * nt + r - kTiledPairRows;
+    return 2 * a.pair_offset + kTiledN * (nt - grid.pair_tiles) + r;
+  };
+  // LDS row of this wave's weight block fb: paired waves take gate blocks
+  // 0-1 and the up blocks of the same columns as 2-3.
+  auto block_lds_row = [&](int fb) {
+    if (paired) return (fb < 2 ? 0 : kTiledPairRows) + 32 * wn + 16 * (fb & 1);
+    return 64 * wn + 16 * fb;
+  };
+
+  const BufferView w_view(a.w, static_cast<uint32_t>(static_cast<int64_t>(a.n) * a.k * 2));
+  const BufferView x_view(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.rows) * a.x_stride * 2));
+  // Staging: thread t copies 16-byte part t % 8 of rows t / 8 + 32 i.
+  const int part = tid & 7;
+  const int r0 = tid >> 3;
+  uint32_t w_src[kWLoads], x_src[kXLoads];
+#pragma unroll
+  for (int i = 0; i < kWLoads; ++i) {
+    const int row = weight_row(r0 + 32 * i);
+    w_src[i] = row < a.n ? static_cast<uint32_t>(row) * a.k * 2 + part * 16 : kNoRow;
+  }
+#pragma unroll
+  for (int i = 0; i < kXLoads; ++i) {
+    const int token = m0 + r0 + 32 * i;
+    x_src[i] = token < a.rows ? static_cast<uint32_t>(static_cast<int64_t>(token) * a.x_stride * 2) + part * 16 : kNoRow;
+  }
+  // Two register sets: the loads of step k + 2 are issued while step k is
+  // multiplied, and step k + 1's data (loaded one step earlier) is stored to
+  // LDS after it, so every load has two steps of MFMAs to arrive.
+  int4 wr[2][kWLoads], xr[2][kXLoads];
+  // Steps past K (the loop runs an even number of steps) load zeros
+  // through the buffer bounds, so every load and store of the loop is
+  // unconditional: a branch around them would leave the compiler unable to
+  // count outstanding loads, and it would then wait for all of them (the
+  // ones just issued for step k + 2 included) before each LDS store.
+  const int steps = a.k / kTiledK;
+  auto load_step = [&](int step, auto set) {
+    const uint32_t k_off = static_cast<uint32_t>(step) * kTiledRowBytes;
+    const bool live = step < steps;
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i)
+      xr[set][i] = x_view.load16(live && x_src[i] != kNoRow ? x_src[i] + k_off : kNoRow);
+#pragma unroll
+    for (int i = 0; i < kWLoads; ++i)
+      wr[set][i] = w_view.load16(live && w_src[i] != kNoRow ? w_src[i] + k_off : kNoRow);
+  };
+  auto store_step = [&](auto set, int slot) {
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i)
+      *reinterpret_cast<int4*>(&xsm[slot][(r0 + 32 * i) * kTiledStride + part * 16]) = xr[set][i];
+#pragma unroll
+    for (int i = 0; i < kWLoads; ++i)
+      *reinterpret_cast<int4*>(&wsm[slot][(r0 + 32 * i) * kTiledStride + part * 16]) = wr[set][i];
+  };
+
+  floatx4 acc[kFB][kTB];
+#pragma unroll
+  for (int fb = 0; fb < kFB; ++fb)
+#pragma unroll
+    for (int tb = 0; tb < kTB; ++tb) acc[fb][tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto multiply = [&](int slot) {
+    const uint8_t* wb = wsm[slot];
+    const uint8_t* xb = xsm[slot];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {  // the two 32-column slices of the step
+      const int col = s * 64 + quarter * 16;
+      int32x4 wf[kFB], xf[kTB];
+#pragma unroll
+      for (int fb = 0; fb < kFB; ++fb)
+        wf[fb] = *reinterpret_cast<const int32x4*>(&wb[(block_lds_row(fb) + row16) * kTiledStride + col]);
+#pragma unroll
+      for (int tb = 0; tb < kTB; ++tb)
+        xf[tb] = *reinterpret_cast<const int32x4*>(&xb[(kWM * wm + 16 * tb + row16) * kTiledStride + col]);
+#pragma unroll
+      for (int fb = 0; fb < kFB; ++fb)
+#pragma unroll
+        for (int tb = 0; tb < kTB; ++tb)
+          acc[fb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wf[fb]), as_bf16x8(xf[tb]), acc[fb][tb], 0, 0, 0);
+    }
+  };
+  // Step k: issue step k + 2's loads into set k % 2 (its step-k data is in
+  // LDS already), multiply slot k % 2, store set (k + 1) % 2 to slot
+  // (k + 1) % 2 (last read in step k - 1, before the previous barrier),
+  // barrier.  With an odd step count the last step multiplies zeros.
+  auto iteration = [&](int step, auto set) {
+    constexpr int kSet = decltype(set)::value;
+    constexpr int kOther = 1 - kSet;
+    load_step(step + 2, set);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(kSet);
+    store_step(std::integral_constant<int, kOther>{}, kOther);
+    __syncthreads();
+  };
+
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, 1>;
+  load_step(0, Set0{});
+  load_step(1, Set1{});
+  store_step(Set0{}, 0);
+  __syncthreads();
+  for (int step = 0; step < steps; step += 2) {
+    iteration(step, Set0{});
+    iteration(step + 1, Set1{});
+  }
+
+  // Lane holds output columns (weight rows) 4 quarter + i of each block for
+  // x row row16 of each x block.
+#pragma unroll
+  for (int tb = 0; tb < kTB; ++tb) {
+    const int token = m0 + kWM * wm + 16 * tb + row16;
+    if (token >= a.rows) continue;
+    uint16_t* out_row = a.out + static_cast<int64_t>(token) * a.out_stride;
+#pragma unroll
+    for (int fb = 0; fb < kFB; ++fb) {
+      const int col = weight_row(block_lds_row(fb)) + 4 * quarter;
+      if (col < a.n)
+        *reinterpret_cast<uint2*>(out_row + col) =
+            make_uint2(pack_bf16x2(acc[fb][tb][0], acc[fb][tb][1]), pack_bf16x2(acc[fb][tb][2], acc[fb][tb][3]));
+    }
+    if (paired && a.act != nullptr) {
+#pragma unroll
+      for (int fb = 0; fb < 2; ++fb) {
+        float g[4], u[4], v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          g[i] = bf16_to_f32(f32_to_bf16(acc[fb][tb][i]));
+          u[i] = bf16_to_f32(f32_to_bf16(acc[fb + 2][tb][i]));
+        }
+        silu_mul_values<4>(g, u, v);
+        const int col = weight_row(block_lds_row(fb)) + 4 * quarter;  // a gate row: the act column
+        *reinterpret_cast<uint2*>(a.act + static_cast<int64_t>(token) * a.act_stride + col) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      }
+    }
+  }
+}
+
 bool aligned_to(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
 }  // namespace
@@ -202,13 +418,8 @@ extern "C" int d3_dense_bf16(const uint16_t* x, int64_t x_stride, int32_t rows, 
   D3_REQUIRE(x && w && out, "dense_bf16: null pointer");
   D3_REQUIRE(rows >= 0 && n > 0 && k > 0 && pair_rows >= 0 && 2 * pair_rows <= n,
              "dense_bf16: rows %d, N %d, K %d, pair_rows %d", rows, n, k, pair_rows);
-  const int chunks = k / kDenseChunk;
-  D3_SUPPORTED(k % kDenseChunk == 0 && (chunks == 1 || chunks == 2 || chunks == 3 || chunks == 4 ||
-                                        chunks == 6 || chunks == 8),
-               "dense_bf16: K=%d not in {256, 512, 768, 1024, 1536, 2048}", k);
   D3_SUPPORTED(n % 16 == 0 && pair_rows % 16 == 0, "dense_bf16: N=%d and pair_rows %d must be multiples of 16",
                n, pair_rows);
-  D3_SUPPORTED(rows <= 1024, "dense_bf16: %d rows above the 1024 of the small-batch kernel", rows);
   D3_REQUIRE(x_stride >= k && out_stride >= n && (act == nullptr || act_stride >= pair_rows),
              "dense_bf16: row strides");
   D3_REQUIRE(aligned_to(x, 16) && x_stride % 8 == 0 && aligned_to(w, 16) && aligned_to(out, 8) &&
@@ -217,15 +428,43 @@ extern "C" int d3_dense_bf16(const uint16_t* x, int64_t x_stride, int32_t rows, 
   D3_SUPPORTED(static_cast<int64_t>(rows) * x_stride * 2 < (int64_t{1} << 31) &&
                    static_cast<int64_t>(n) * k * 2 < (int64_t{1} << 31),
                "dense_bf16: operands above 2 GiB");
+  const int chunks = k / kDenseChunk;
+  const bool small_k = k % kDenseChunk == 0 && (chunks == 1 || chunks == 2 || chunks == 3 || chunks == 4 ||
+                                                 chunks == 6 || chunks == 8);
+  const bool small = rows < kTiledMinRows && small_k;
+  if (!small) {
+    D3_SUPPORTED(k % kTiledK == 0, "dense_bf16: K=%d must be a multiple of %d above %d rows (or in {256, 512, "
+                 "768, 1024, 1536, 2048})", k, kTiledK, kTiledMinRows - 1);
+    D3_SUPPORTED(pair_rows % kTiledPairRows == 0,
+                 "dense_bf16: pair_rows %d must be a multiple of %d above %d rows", pair_rows, kTiledPairRows,
+                 kTiledMinRows - 1);
+  }
   if (rows == 0) {
     clear_error();
     return D3_OK;
   }
   const int pairs = pair_rows / 16;
-  const int rest = n / 16 - 2 * pairs;
   const DenseArgs args{x, x_stride, rows, w, n, k, out, out_stride, pairs, pair_rows, act, act_stride};
-  const dim3 grid(pairs + (rest + 1) / 2, (rows + kDenseTokens - 1) / kDenseTokens), block(kDenseThreads);
   hipStream_t s = as_stream(stream);
+  if (!small) {
+    TiledGrid g{};
+    g.pair_tiles = pair_rows / kTiledPairRows;
+    g.n_tiles = g.pair_tiles + (n - 2 * pair_rows + kTiledN - 1) / kTiledN;
+    // 128-row x tiles when they already give every CU a workgroup, else 64
+    const int tiles128 = (rows + 127) / 128 * g.n_tiles;
+    const bool wide = tiles128 >= 256;
+    g.m_tiles = wide ? (rows + 127) / 128 : (rows + 63) / 64;
+    const int total = g.m_tiles * g.n_tiles;
+    g.per_xcd = (total + kTiledXcds - 1) / kTiledXcds;
+    const dim3 grid(g.per_xcd * kTiledXcds), block(kTiledThreads);
+    if (wide)
+      hipLaunchKernelGGL(dense_bf16_tiled_kernel<128>, grid, block, 0, s, args, g);
+    else
+      hipLaunchKernelGGL(dense_bf16_tiled_kernel<64>, grid, block, 0, s, args, g);
+    D3_LAUNCHED("dense_bf16");
+  }
+  const int rest = n / 16 - 2 * pairs;
+  const dim3 grid(pairs + (rest + 1) / 2, (rows + kDenseTokens - 1) / kDenseTokens), block(kDenseThreads);
   switch (k / kDenseChunk) {
     case 1: hipLaunchKernelGGL(dense_bf16_kernel<1>, grid, block, 0, s, args); break;
     case 2: hipLaunchKernelGGL(dense_bf16_kernel<2>, grid, block, 0, s, args); break;

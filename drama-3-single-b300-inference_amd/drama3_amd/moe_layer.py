@@ -9,15 +9,14 @@ rows), runs the bf16 shared expert (``silu_mul`` then ``down_proj``) on a
 side stream while the routed top-8 FP8 experts run on the main stream, and
 joins before the combine (``model.py:506-518``).
 
-Here, for decode-sized batches (up to 1024 rows), both bf16 GEMMs are this
-package's MFMA kernel (``d3_dense_bf16``: the projection, whose epilogue
-also writes the shared expert's ``silu_mul`` activation, and the shared
-down projection), and with
-at most 256 rows the routed experts are the decode step, whose combine is
-folded into the layer's (``d3_combine_route_logits``: routing weights,
-rank-order routed sum, gated shared add and optionally the residual +
-RMSNorm of ``combine_experts_add_norm``, one launch).  Larger batches run
-the projections as library GEMMs (``torch.mm``, hipBLASLt) and the prefill
+Here both bf16 GEMMs are this package's MFMA kernels at every batch size
+(``d3_dense_bf16``: the projection, whose epilogue also writes the shared
+expert's ``silu_mul`` activation, and the shared down projection; a
+streaming kernel up to 768 rows, a tiled one above).  With at most 256
+rows the routed experts are the decode step, whose combine is folded into
+the layer's (``d3_combine_route_logits``: routing weights, rank-order
+routed sum, gated shared add and optionally the residual + RMSNorm of
+``combine_experts_add_norm``, one launch); larger batches run the prefill
 path.  ``overlap`` puts the shared expert on a default-priority side stream
 forked after the projection and joined before the combine.
 """
@@ -32,8 +31,20 @@ from ._lib import call, ptr
 from .pipeline import DTYPE_BF16, DecodeStep, MoEWorkspace, Shape, dtype_code, require_cuda
 
 PROJECTION_PADDING = 127  # zero rows the reference appends (model.py:236-245)
-DENSE_ROWS = 1024  # most rows of d3_dense_bf16
-DENSE_K = (256, 512, 768, 1024, 1536, 2048)
+DENSE_ROWS = 768  # most rows of d3_dense_bf16's streaming (small-batch) kernel
+DENSE_K = (256, 512, 768, 1024, 1536, 2048)  # its contraction lengths
+TILED_K = 64  # the tiled kernel (more rows): K a multiple of this
+TILED_PAIRS = 64  # and gate / up pair rows a multiple of this
+
+
+def dense_supported(rows: int, n: int, k: int, pair_rows: int = 0) -> bool:
+    """Whether ``d3_dense_bf16`` covers an [rows, k] x [n, k]^T product with
+    ``pair_rows`` gate / up pairs (the checks of its C entry point)."""
+    if n % 16 or pair_rows % 16 or 2 * pair_rows > n or k <= 0:
+        return False
+    if rows <= DENSE_ROWS and k in DENSE_K:
+        return True
+    return k % TILED_K == 0 and pair_rows % TILED_PAIRS == 0
 
 
 def pack_input_projection(gate_proj: torch.Tensor, up_proj: torch.Tensor, router: torch.Tensor,
@@ -101,9 +112,13 @@ class MoELayer:
         self.shared = torch.empty((rows, hidden), **bf16)
         self.out = torch.empty((rows, hidden), **bf16)
         self.norm_out = torch.empty((rows, hidden), **bf16)
-        # own MFMA GEMMs for decode-sized batches whose shapes the kernel covers
-        self.dense = (rows <= DENSE_ROWS and hidden in DENSE_K and shared_intermediate in DENSE_K
-                      and width % 16 == 0 and width % 8 == 0 and hidden % 16 == 0)
+        # both bf16 GEMMs on d3_dense_bf16 (no library GEMM on the path)
+        if not (dense_supported(rows, width, hidden, shared_intermediate)
+                and dense_supported(rows, hidden, shared_intermediate)):
+            raise ValueError(
+                f"d3_dense_bf16 does not cover this layer: hidden {hidden} and shared "
+                f"intermediate {shared_intermediate} must be in {DENSE_K} (up to {DENSE_ROWS} "
+                f"rows) or multiples of {TILED_K}, the projection width {width} a multiple of 16")
         self.decode = rows <= 256
         if self.decode:
             self.step = DecodeStep(rows, num_experts, hidden, intermediate, top_k, device=dev)
@@ -131,21 +146,14 @@ class MoELayer:
             raise ValueError("down_proj must be [H, shared_intermediate]")
 
     def _project(self, x, projection) -> None:
-        """The packed projection; the own kernel also writes the shared
-        expert's activation ``silu_mul(gate | up)`` from its epilogue."""
-        if self.dense:
-            dense_bf16(x, projection.contiguous(), self.projected, self.shared_intermediate,
-                       self.act)
-        else:
-            torch.mm(x, projection.t(), out=self.projected)
+        """The packed projection; its epilogue also writes the shared
+        expert's activation ``silu_mul(gate | up)``."""
+        dense_bf16(x, projection.contiguous(), self.projected, self.shared_intermediate, self.act)
 
-    def _shared_expert(self, gate_up, down_proj) -> None:
-        if self.dense:
-            dense_bf16(self.act, down_proj.contiguous(), self.shared)
-            return
-        call("d3_silu_mul", ptr(gate_up), gate_up.stride(0), self.rows, self.shared_intermediate,
-             ptr(self.act), _lib.stream(self.device))
-        torch.mm(self.act, down_proj.t(), out=self.shared)
+    def _shared_expert(self, down_proj) -> None:
+        """The shared expert's down projection of the activation the
+        projection wrote."""
+        dense_bf16(self.act, down_proj.contiguous(), self.shared)
 
     def _fused(self, experts, x, router) -> bool:
         """Whether the routed combine folds into the layer's combine: the
@@ -161,13 +169,13 @@ class MoELayer:
         self._check(x, projection, down_proj)
         main = torch.cuda.current_stream(self.device)
         self._project(x, projection)
-        gate_up, router, _ = self._views()
+        _, router, _ = self._views()
         if self.side is not None:
             # Fork after the projection; join before the outputs are read
             # (the reference's moe_shared_stream, model.py:506-517).
             self.side.wait_stream(main)
             with torch.cuda.stream(self.side):
-                self._shared_expert(gate_up, down_proj)
+                self._shared_expert(down_proj)
         if fuse:
             ws, stream = self.step.workspace, _lib.stream(self.device)
             ws.decode_route_fc1(experts, self.all_rows, x, router, self.step.active,
@@ -178,7 +186,7 @@ class MoELayer:
         else:
             self.workspace.forward(x, router, experts, out=self.routed)
         if self.side is None:
-            self._shared_expert(gate_up, down_proj)
+            self._shared_expert(down_proj)
         else:
             main.wait_stream(self.side)
         return router

@@ -621,7 +621,7 @@ int d3_combine_route_logits(const float *down, const void *logits, int32_t logit
                             uint16_t *out, void *stream);
 
 /*
- * f4  Dense bf16 GEMM of the MoE layer's small-batch projections.
+ * f4  Dense bf16 GEMM of the MoE layer's projections.
  * Replaces the two bf16 linear layers around the routed experts in
  * DramaModel.moe_parts (src/drama3/model.py:495-518): the packed input
  * projection (shared gate / up rows, router, shared-expert gate;
@@ -633,9 +633,11 @@ int d3_combine_route_logits(const float *down, const void *logits, int32_t logit
  * act[r, c] = bf16(bf16(silu(out[r, c])) * out[r, P + c]) for c < P (the
  * bytes of d3_silu_mul on out).  x bf16 [rows, x_stride], w bf16 [n, k]
  * row-major (a torch Linear weight), out bf16 [rows, out_stride], act bf16
- * [rows, act_stride].  k in {256, 512, 768, 1024, 1536, 2048}, n and P
- * multiples of 16, rows <= 1024; x / w rows 16-byte aligned, out / act rows
- * 8-byte.
+ * [rows, act_stride].  Up to 768 rows with k in {256, 512, 768, 1024, 1536,
+ * 2048} a streaming kernel runs (n and P multiples of 16); otherwise a
+ * tiled kernel (k a multiple of 64, n a multiple of 16, P a multiple of
+ * 64).  x / w rows 16-byte aligned, out / act rows 8-byte; operands below
+ * 2 GiB.
  */
 int d3_dense_bf16(const uint16_t *x, int64_t x_stride, int32_t rows, const uint16_t *w, int32_t n,
                   int32_t k, int32_t pair_rows, uint16_t *out, int64_t out_stride, uint16_t *act,

@@ -46,7 +46,11 @@ def _close_to_fp32_product(got: torch.Tensor, want: torch.Tensor) -> None:
 
 
 @pytest.mark.parametrize("rows,n,k", [(64, 1408, 2048), (1, 16, 256), (37, 272, 768),
-                                      (300, 1024, 512), (1024, 48, 1536), (129, 64, 1024)])
+                                      (300, 1024, 512), (1024, 48, 1536), (129, 64, 1024),
+                                      # the tiled kernel: above 768 rows, or K outside
+                                      # the streaming kernel's set
+                                      (1025, 1408, 2048), (2048, 1408, 2048), (4096, 2048, 512),
+                                      (3001, 272, 64), (1500, 48, 1536), (100, 144, 320)])
 def test_dense_bf16_against_fp32(device, rows, n, k):
     from drama3_amd.moe_layer import dense_bf16
 
@@ -60,7 +64,9 @@ def test_dense_bf16_against_fp32(device, rows, n, k):
 
 
 @pytest.mark.parametrize("rows,pairs,n,k", [(64, 512, 1408, 2048), (5, 256, 656, 1024),
-                                            (200, 128, 272, 768), (70, 64, 128, 512)])
+                                            (200, 128, 272, 768), (70, 64, 128, 512),
+                                            (2048, 512, 1408, 2048), (1100, 64, 128, 512),
+                                            (4096, 512, 1408, 2048), (1030, 192, 400, 1024)])
 def test_dense_bf16_pairs_write_silu_mul(device, rows, pairs, n, k):
     """With gate / up pairs the projection's epilogue writes the shared
     expert's activation: the bytes of silu_mul on the projected rows."""
@@ -81,7 +87,13 @@ def test_dense_bf16_pairs_write_silu_mul(device, rows, pairs, n, k):
 
 
 @pytest.mark.parametrize("rows,e,h,i,si", [(48, 16, 1024, 256, 256), (300, 16, 1024, 256, 512),
-                                           (64, 128, 2048, 768, 512)])
+                                           (64, 128, 2048, 768, 512),
+                                           # the reference model's layer (E256, I512, shared I512)
+                                           (64, 256, 2048, 512, 512),
+                                           # prefill-sized layers: tiled projections
+                                           (2048, 256, 2048, 512, 512), (4096, 64, 1024, 256, 512)],
+                         ids=["r48_e16", "r300_e16", "r64_e128", "r64_reference_shape",
+                              "r2048_reference_shape", "r4096_e64"])
 def test_moe_layer_parts_and_combine(device, rows, e, h, i, si):
     from drama3_amd.kernels import combine_experts, combine_experts_add_norm
     from drama3_amd.moe_layer import MoELayer
@@ -106,8 +118,7 @@ def test_moe_layer_parts_and_combine(device, rows, e, h, i, si):
     # shared expert: SwiGLU bytes of silu_mul, the down projection within one
     # bf16 rounding of the fp32 product
     act = torch.from_numpy(bf16_to_f32(om.silu_mul(gate_up)))
-    if layer.dense:
-        assert np.array_equal(np_bf16(layer.act), om.silu_mul(gate_up))
+    assert np.array_equal(np_bf16(layer.act), om.silu_mul(gate_up))
     _close_to_fp32_product(shared, act @ down.float().cpu().t())
     # routed experts on the projected router columns
     weights, ids = om.route(router)
@@ -130,7 +141,8 @@ def test_moe_layer_parts_and_combine(device, rows, e, h, i, si):
     torch.cuda.synchronize()
     assert torch.equal(res_a.view(torch.int16), res_b.view(torch.int16))
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
-    print(f"rows {rows} E {e}: routed {stats}, fused epilogue {layer._fused(experts, x, layer._views()[1])}")
+    print(f"rows {rows} E {e} H {h} I {i} shared {si}: routed {stats}, "
+          f"fused epilogue {layer._fused(experts, x, layer._views()[1])}", flush=True)
 
 
 @pytest.mark.parametrize("logits_dtype,weights_dtype", [(torch.float32, torch.float32),
