@@ -66,6 +66,10 @@ def parse():
     p.add_argument("--mixed-only", action="store_true",
                    help="measure only the config-5 mixed step (one JSON line)")
     p.add_argument("--mixed-steps", type=int, default=50)
+    p.add_argument("--decode-config-only", type=int, choices=(1, 2, 3), default=None,
+                   help="measure only this decode configuration's step (one JSON line)")
+    p.add_argument("--layer-only", action="store_true",
+                   help="measure only the whole MoE layer lines (64 and 4096 rows; one JSON line)")
     return p.parse_args()
 
 
@@ -607,6 +611,15 @@ def main():
         print(json.dumps({"prefill": bench_prefill(torch, args.prefill_steps, replays=args.replays,
                                                    check_parity=not args.no_parity)}),
               flush=True)
+        return
+    if args.decode_config_only is not None:
+        print(json.dumps({"decode_config": bench_decode_config(torch, args.decode_config_only,
+                                                               args.replays)}), flush=True)
+        return
+    if args.layer_only:
+        layer = bench_moe_layer(torch)
+        layer["prefill_4096_rows"] = bench_moe_layer_prefill(torch)
+        print(json.dumps({"moe_layer": layer}), flush=True)
         return
     if args.mixed_only:
         print(json.dumps({"mixed": bench_mixed(torch, args.mixed_steps,

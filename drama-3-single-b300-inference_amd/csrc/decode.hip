@@ -28,6 +28,7 @@
 // front's per-128 rule.  The routing weights are then computed by the
 // combine (routed_combine_kernel) from the same logits with the front's
 // function, so every byte matches the chain that runs the front.
+#include <algorithm>
 #include <mutex>
 
 #include "common.h"
@@ -69,6 +70,9 @@ struct DecodeArgs {
   int32_t* active_out;
   uint16_t* out_bf16;  // MODE 0 / 1: gate|up [pairs, n_rows]
   float* out_f32;      // MODE 2: down [pairs, n_rows]
+  // Route slices per (expert, weight-tile group), set at launch: slice j of
+  // an expert takes its route tiles j, j + slices, ... (1: every tile).
+  int slices;
 };
 
 constexpr int kPassSlots = kGemmThreads / 4;         // MODE 1: 4 lanes per slot
@@ -93,9 +97,32 @@ struct LogitPass {
 // kWholeFirst: the whole first weight tile is issued before the routes are
 // known (batches that reach nearly every expert), instead of its first half
 // (otherwise the wasted loads of experts without routes cost more).
-template <int KB, int RT, int MODE, int TILES, int PASSES = 1, bool kWholeFirst = false>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_gemm_kernel(
-    DecodeArgs a) {
+// Launches that may split an expert's route tiles over several workgroups
+// (route slices): one weight tile per workgroup, except FC1 from the slots
+// at K = 2048, whose two bodies together would not fit the registers.
+constexpr bool sliced_kernel(int kb, int mode, int tiles) { return tiles == 1 && !(mode == 1 && kb >= 16); }
+
+// LDS of one decode GEMM workgroup (declared once in the kernel, shared by
+// both instantiations of its body).
+template <int KB, int MODE>
+struct DecodeLds {
+  static constexpr int kStride = KB * kGroup + 16;  // 16-byte pad: the 16 rows of a ds_read_b128 hit distinct banks
+  __attribute__((aligned(16))) uint8_t b_tile[16 * kStride];
+  float b_scales[16 * KB];
+  int b_target[16];  // pair of each route column, -1 = none
+  int route_pairs[kMaxSlots];
+  int route_slots[MODE == 1 ? kMaxSlots : 1];
+  int chunk_counts[kIdsPerThread * kGemmWaves];
+};
+
+// One workgroup's work: expert `expert`, weight tiles [first_tile,
+// first_tile + TILES), route tiles first_route, first_route + 16 slices, ...
+// kEarly: the first weights are issued before the route scan (every
+// workgroup of an unsliced launch, slice 0 of a sliced one); otherwise only
+// after it, once the workgroup knows it has a route tile.
+template <int KB, int RT, int MODE, int TILES, int PASSES, bool kWholeFirst, bool kEarly>
+__device__ __forceinline__ void decode_gemm_body(const DecodeArgs& a, DecodeLds<KB, MODE>& lds, int expert,
+                                                 int first_tile, int slice, int slices) {
   const uint8_t* __restrict__ w = a.w;
   const float* __restrict__ ws = a.ws;
   const int n_rows = a.n_rows;
@@ -109,20 +136,16 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   constexpr int K = KB * kGroup;
   constexpr int kRowsPerWave = RT * 16;
   constexpr int kRowsPerGroup = kGemmWaves * kRowsPerWave;
-  constexpr int kStride = K + 16;  // 16-byte pad: the 16 rows of a ds_read_b128 hit distinct banks
+  constexpr int kStride = DecodeLds<KB, MODE>::kStride;
   constexpr int kChunks = K / 256;
   constexpr int kFirstHalf = KB > 1 ? KB / 2 : KB;
-  __shared__ __attribute__((aligned(16))) uint8_t b_tile[16 * kStride];
-  __shared__ float b_scales[16 * KB];
-  __shared__ int b_target[16];  // pair of each route column, -1 = none
-  __shared__ int route_pairs[kMaxSlots];
-  __shared__ int route_slots[MODE == 1 ? kMaxSlots : 1];
-  __shared__ int chunk_counts[kIdsPerThread * kGemmWaves];
-
-  const int tiles = n_rows / kRowsPerGroup;
-  const int groups = tiles / TILES;
-  const int expert = blockIdx.x / groups;
-  const int first_tile = (blockIdx.x % groups) * TILES;
+  auto& b_tile = lds.b_tile;
+  auto& b_scales = lds.b_scales;
+  auto& b_target = lds.b_target;
+  auto& route_pairs = lds.route_pairs;
+  auto& route_slots = lds.route_slots;
+  auto& chunk_counts = lds.chunk_counts;
+  const int first_route = 16 * slice;  // this slice's first route tile
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int row16 = lane & 15;
@@ -181,8 +204,10 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     load_pass(0, lp);
     __builtin_amdgcn_sched_barrier(0);
     // 2. The first half of the first weight tile streams meanwhile.
-    load_weights(first_tile, 0, kWholeFirst ? KB : kFirstHalf);
-    load_scales(first_tile, 0, kWholeFirst ? KB : kFirstHalf);
+    if constexpr (kEarly) {
+      load_weights(first_tile, 0, kWholeFirst ? KB : kFirstHalf);
+      load_scales(first_tile, 0, kWholeFirst ? KB : kFirstHalf);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. Occupied slots (every wave holds the masks) and this expert's rank
@@ -196,6 +221,10 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       occ_base[p] = live;
       live += __popcll(occ_mask[p]);
     }
+    // An expert has at most one route per live row: a slice whose first
+    // route tile lies beyond the live rows has nothing to do (uniform).
+    // (Slice 0 always goes on: one of its workgroups writes the slot list.)
+    if (slice > 0 && first_route >= live) return;
     const uint32_t own_key_column = static_cast<uint32_t>(expert);
     uint64_t hits[PASSES];
     int my_pair[PASSES];
@@ -250,7 +279,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       const bool routed = occupied && static_cast<int>(above) < top_k;
       hits[p] = __ballot(q == 0 && routed);
       my_pair[p] = row * top_k + static_cast<int>(above);
-      if (q == 0 && routed && first_tile == 0) a.ids_out[my_pair[p]] = expert;
+      if (q == 0 && routed && first_tile == 0 && slice == 0) a.ids_out[my_pair[p]] = expert;
     };
     rank_pass(0, lp);
 #pragma unroll
@@ -263,7 +292,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       }
     }
     // The slot list and the live count (one workgroup writes them).
-    if (blockIdx.x == 0) {
+    if (expert == 0 && first_tile == 0 && slice == 0) {
       if (wave == 0) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p)
@@ -308,9 +337,12 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       id[j] = id_view.load4(p * 4 < id_bytes ? p * 4 : kNoRow);
     }
     const int rows = live_rows(a.row_count, capacity);
+    if (slice > 0 && first_route >= rows) return;  // at most one route per live row (uniform)
     // 2. The first half of the first weight tile streams meanwhile.
-    load_weights(first_tile, 0, kWholeFirst ? KB : kFirstHalf);
-    load_scales(first_tile, 0, kWholeFirst ? KB : kFirstHalf);
+    if constexpr (kEarly) {
+      load_weights(first_tile, 0, kWholeFirst ? KB : kFirstHalf);
+      load_scales(first_tile, 0, kWholeFirst ? KB : kFirstHalf);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. This expert's route list, in ascending pair order: pair p = j * 256 +
@@ -341,7 +373,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   }
   __syncthreads();
   routes = __builtin_amdgcn_readfirstlane(routes);
-  if (routes == 0) return;  // no route for this expert: the loads issued so far are dropped
+  // No route for this expert (or for this slice): the loads issued so far
+  // are dropped.
+  if (routes <= first_route) return;
   const bool exact = routes <= exact_routes;
 
   // 4. Staging of one route tile (16 threads per route column), branch-free.
@@ -536,9 +570,12 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   };
 
   // 5. First route tile between the weight halves, then the tiles.
-  fetch_tile(0);
+  fetch_tile(first_route);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (!kWholeFirst) {
+  if constexpr (!kEarly) {  // the whole tile, after the route tile's loads
+    load_weights(first_tile, 0, KB);
+    load_scales(first_tile, 0, KB);
+  } else if constexpr (!kWholeFirst) {
     load_weights(first_tile, kFirstHalf, KB);
     load_scales(first_tile, kFirstHalf, KB);
   }
@@ -591,7 +628,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     floatx4 acc[RT];
     mma(acc);
     epilogue(acc, first_tile);
-    for (int m0 = 16; m0 < routes; m0 += 16) {
+    for (int m0 = first_route + 16 * slices; m0 < routes; m0 += 16 * slices) {
       __syncthreads();  // previous route tile fully consumed
       fetch_tile(m0);
       store_tile();
@@ -603,12 +640,65 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   }
 }
 
+template <int KB, int RT, int MODE, int TILES, int PASSES = 1, bool kWholeFirst = false>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_gemm_kernel(
+    DecodeArgs a) {
+  __shared__ DecodeLds<KB, MODE> lds;
+  constexpr int kRowsPerGroup = kGemmWaves * RT * 16;
+  const int groups = a.n_rows / kRowsPerGroup / TILES;
+  // Workgroup -> (expert, tile group, route slice).  Slice-major: every
+  // (expert, group)'s slice 0 is dispatched first, the extra slices after;
+  // the slice stride is a multiple of 8 workgroups, so the slices of one
+  // (expert, group) run on one XCD (workgroup b on XCD b % 8) and share the
+  // weight tile in its L2.
+  const int slices = sliced_kernel(KB, MODE, TILES) && a.slices > 1 ? a.slices : 1;
+  int unit = static_cast<int>(blockIdx.x), slice = 0;
+  if (slices > 1) {
+    const int units = a.num_experts * groups;
+    const int stride = (units + 7) / 8 * 8;
+    slice = unit / stride;
+    unit -= slice * stride;
+    if (unit >= units) return;  // padding up to the stride (uniform)
+  }
+  const int expert = unit / groups;
+  const int first_tile = (unit % groups) * TILES;
+  // Two straight-line bodies, never merged: a branch around the early loads
+  // inside one body would leave the compiler unable to count outstanding
+  // loads at the join.
+  if constexpr (sliced_kernel(KB, MODE, TILES)) {
+    if (slice > 0) {
+      decode_gemm_body<KB, RT, MODE, TILES, PASSES, kWholeFirst, false>(a, lds, expert, first_tile, slice, slices);
+      return;
+    }
+  }
+  decode_gemm_body<KB, RT, MODE, TILES, PASSES, kWholeFirst, true>(a, lds, expert, first_tile, slice, slices);
+}
+
 bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
+constexpr int kResidentGroups = 512;
+
+// Route slices of a one-tile-per-workgroup launch: while (expert, tile)
+// workgroups fill less than one round of resident workgroups (few experts),
+// each gets up to `capacity / 16` slices that take its route tiles in turn,
+// so a busy expert's route tiles run side by side instead of one after
+// another in one workgroup (skewed routing: a few experts with up to one
+// route per slot).  Slices beyond an expert's route tiles exit after the
+// route scan.
+int route_slices(int units, int capacity) {
+  const int most = (capacity + 15) / 16;
+  const int fit = kResidentGroups / (units > 0 ? units : 1);
+  return std::max(1, std::min(most, fit));
+}
+
 template <int KB, int MODE, int TILES>
-void launch_tiles(int num_experts, hipStream_t s, const DecodeArgs& a) {
-  const int tiles = a.n_rows / tile_rows_for(KB);
-  const dim3 grid(num_experts * (tiles / TILES)), block(kGemmThreads);
+void launch_tiles(int num_experts, hipStream_t s, const DecodeArgs& args) {
+  const int tiles = args.n_rows / tile_rows_for(KB);
+  const int units = num_experts * (tiles / TILES);
+  DecodeArgs a = args;
+  a.slices = sliced_kernel(KB, MODE, TILES) ? route_slices(units, a.capacity) : 1;
+  const int blocks = a.slices > 1 ? (units + 7) / 8 * 8 * a.slices : units;
+  const dim3 grid(blocks), block(kGemmThreads);
   if constexpr (MODE == 1) {
     if (a.capacity > kPassSlots) {
       hipLaunchKernelGGL((decode_gemm_kernel<KB, rt_for(KB), MODE, TILES, kMaxPasses>), grid, block, 0, s, a);
@@ -632,7 +722,6 @@ void launch_tiles(int num_experts, hipStream_t s, const DecodeArgs& a) {
 // expert's tile count (8 for 256 experts of 16 tiles).  Experts averaging
 // more than 8 routes at full capacity take one tile per workgroup (each
 // further route tile would walk all of a workgroup's tiles again).
-constexpr int kResidentGroups = 512;
 int tiles_per_group(int num_experts, int tiles, int capacity, int top_k, int mode) {
   if (capacity * top_k > 8 * num_experts) return 1;
   const int options[] = {1, 2, 4, 6, 8};

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import EXACT, assert_bf16_close, np_bf16, np_f32, oracle_weights
+from helpers import CONTRACTION, EXACT, assert_bf16_close, np_bf16, np_f32, oracle_weights
 from oracle import moe as om
 
 pytestmark = pytest.mark.gpu
@@ -222,3 +222,52 @@ def test_real_drama3_shape_eight_tiles_per_workgroup(device):
     expected = om.expert_ffn(np_bf16(xs.cpu())[active], ids, weights, oracle_weights(experts_cpu))
     stats = assert_bf16_close(np_bf16(steps[0].workspace.out)[:n], expected, **EXACT)
     print(f"E 256 I 512: rows {n} {stats}", flush=True)
+
+
+@pytest.mark.parametrize("slots,live", [(256, 256), (256, 200), (64, 17), (128, 33)])
+def test_route_slices_of_hot_experts(device, slots, live):
+    """Few experts (E16) and routing skewed so that the hottest experts take
+    a route from nearly every live slot: the one-tile-per-workgroup GEMMs
+    split each expert's route tiles over several workgroups (route slices;
+    at 256 slots an expert's 16 route tiles are taken four per slice), and
+    slices beyond the live rows exit early.  The frontless and front-started
+    sortless steps agree bit for bit; with at most 64 routes per expert
+    (the exact path everywhere) both equal the sorted chain bit for bit;
+    all are within tolerance of the oracle (the FP8 contraction tolerance
+    once an expert takes more than 64 routes)."""
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.workloads import Workload, make_experts
+
+    gen = torch.Generator("cpu").manual_seed(slots + live)
+    e, h, i = 16, 1024, 256
+    experts_cpu = make_experts(gen, e, h, i)
+    w = Workload("hot", 0, h, e, i, experts_cpu, [])
+    experts = prepare_experts(experts_cpu.to(device))
+    steps = steps_for(w, device, experts, slots=slots)
+    occupancy = torch.zeros(slots, dtype=torch.uint8)
+    occupancy[torch.randperm(slots, generator=gen)[:live]] = 1
+    xs = torch.randn((slots, h), generator=gen).to(torch.bfloat16)
+    bias = torch.zeros(e)
+    bias[[3, 7, 11, 12]] = 4.0  # four experts in (nearly) every row's top 8
+    ls = (torch.randn((slots, e), generator=gen) + bias).to(torch.bfloat16)
+    active, n = om.compact_slots(occupancy.numpy())
+    weights, ids = om.route(np_f32(ls)[active])
+    counts = np.bincount(ids.ravel(), minlength=e)
+    assert counts.max() > 16  # a hot expert spans several route tiles
+    occ_d, xs_d, ls_d = occupancy.to(device), xs.to(device), ls.to(device)
+    for ds in steps:
+        ds(occ_d, xs_d, ls_d, experts)
+    torch.cuda.synchronize()
+    frontless, front, chain = steps
+    assert frontless.uses_frontless(occ_d, xs_d, ls_d)
+    a, b = frontless.workspace, front.workspace
+    assert int(frontless.count.item()) == n and torch.equal(frontless.active, chain.active)
+    assert torch.equal(a.ids[:n], b.ids[:n]) and torch.equal(a.ids[:n], chain.workspace.ids[:n])
+    assert torch.equal(a.down[:8 * n].view(torch.int32), b.down[:8 * n].view(torch.int32))
+    assert torch.equal(a.out[:n].view(torch.int16), b.out[:n].view(torch.int16))
+    if counts.max() <= 64:
+        assert compare(frontless, chain) == n
+    expected = om.expert_ffn(np_bf16(xs)[active], ids, weights, oracle_weights(experts_cpu))
+    tolerance = EXACT if counts.max() <= 64 else CONTRACTION
+    stats = assert_bf16_close(np_bf16(a.out)[:n], expected, **tolerance)
+    print(f"slots {slots} live {n}: routes per expert {counts.tolist()} {stats}", flush=True)
