@@ -85,11 +85,38 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t code) {
   return __uint_as_float(__float_as_uint(mag) | sign);
 }
 
+// 1 / d rounded to nearest even for d in [2^-43, 2^126): the hardware
+// reciprocal (v_rcp_f32, within one ulp) and one Newton-Raphson correction
+// with the exact residual 1 - d * y (Markstein's reciprocal step).
+// d3_check_epilogue_arithmetic (selftest.hip) compares it with the IEEE
+// division 1.0f / d for every fp32 d in that range on the device.
+__device__ __forceinline__ float recip_rn(float d) {
+  const float y = __builtin_amdgcn_rcpf(d);
+  const float e = fmaf(-d, y, 1.0f);
+  return fmaf(e, y, y);
+}
+
 // Per-128 group quantisation rule of the reference (moe_input.py:24-27):
 // scale = max(amax, 1e-10) / 448 and q = e4m3(clamp(x / scale, -448, 448)),
-// with IEEE fp32 division.
+// with IEEE fp32 division.  The division by 448 is Markstein's division by
+// a constant: q0 = m * RN(1/448), the exact residual m - 448 q0, one
+// correction; three instructions instead of the general division sequence.
+// m = +inf gives +inf, as the IEEE division does.
+// d3_check_epilogue_arithmetic compares it with the IEEE form for every
+// non-negative fp32 amax (+inf included).
 __device__ __forceinline__ float group_scale(float amax) {
-  return fmaxf(amax, 1e-10f) / 448.0f;
+  constexpr float kInv448 = 1.0f / 448.0f;
+  const float m = fmaxf(amax, 1e-10f);
+  const float q0 = m * kInv448;
+  const float r = fmaf(-q0, 448.0f, m);
+  const float q = fmaf(r, kInv448, q0);
+  return m == __builtin_huge_valf() ? m : q;
+}
+
+// 1.0f / scale for a group scale: every finite group scale lies in
+// [RN(1e-10 / 448), FLT_MAX / 448], inside recip_rn's range; +inf gives 0.
+__device__ __forceinline__ float scale_reciprocal(float scale) {
+  return scale == __builtin_huge_valf() ? 0.0f : recip_rn(scale);
 }
 
 __device__ __forceinline__ uint32_t quantize_one(float x, float scale) {
@@ -112,15 +139,16 @@ __device__ __forceinline__ float div_rn(float x, float s, float inv) {
   return copysignf(fmaf(r, inv, q0), x);
 }
 
-// quantize_one of four values, packed little-endian (v[0] in the low byte).
-// The division is div_rn (one reciprocal per call: callers that quantise
-// several words with one scale share it after inlining).  The conversion is
+// quantize_one of four values, packed little-endian (v[0] in the low byte),
+// for a scale from group_scale.  The division is div_rn with the reciprocal
+// from scale_reciprocal (one per call: callers that quantise several words
+// with one scale share it after inlining).  The conversion is
 // v_cvt_pk_fp8_f32 (round to nearest even into OCP e4m3), which gives
 // f32_to_e4m3's byte for every input in [-448, 448] in every byte position:
 // d3_check_e4m3_conversion (selftest.hip) compares the two over all 2^32
 // fp32 bit patterns after the clamp.
 __device__ __forceinline__ uint32_t quantize_four(const float* v, float scale) {
-  const float inv = 1.0f / scale;
+  const float inv = scale_reciprocal(scale);
   float c[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) c[i] = fminf(fmaxf(div_rn(v[i], scale, inv), -448.0f), 448.0f);

@@ -121,17 +121,6 @@ __device__ __forceinline__ floatx4 mfma_block_bf16(int32x8 a, const bf16x8 b[4])
   return acc;
 }
 
-// 1 / d rounded to nearest even for d in [1, 2^126): the hardware
-// reciprocal (v_rcp_f32, within one ulp) and one Newton-Raphson correction
-// with the exact residual 1 - d * y (Markstein's reciprocal step).
-// d3_check_epilogue_arithmetic (selftest.hip) compares it with the IEEE
-// division 1.0f / d for every fp32 d in that range on the device.
-__device__ __forceinline__ float recip_rn(float d) {
-  const float y = __builtin_amdgcn_rcpf(d);
-  const float e = fmaf(-d, y, 1.0f);
-  return fmaf(e, y, y);
-}
-
 // SwiGLU of bf16-rounded gate / up pairs in fp32: a = (g * sigmoid(g)) * u
 // with sigmoid(g) = 1 / (1 + exp(-g)) in IEEE fp32 (the library expf, within
 // one ulp, and a correctly rounded reciprocal, recip_rn), the arithmetic of the

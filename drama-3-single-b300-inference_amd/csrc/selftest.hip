@@ -8,10 +8,13 @@
 // every clamped fp32 input and in every byte position of the packed word.
 // This kernel compares the two over a range of fp32 bit patterns.
 //
-// The SwiGLU requantisation also takes three shortcuts that must give the
-// IEEE results: pack_bf16x2 (hardware bf16 rounding), recip_rn (hardware
-// reciprocal + one Newton-Raphson step) inside sigmoid_rn, and div_rn
-// (reciprocal of the scale + one residual correction) inside quantize_four.
+// The quantisers and the SwiGLU requantisation also take shortcuts that
+// must give the IEEE results: pack_bf16x2 (hardware bf16 rounding),
+// recip_rn (hardware reciprocal + one Newton-Raphson step) inside
+// sigmoid_rn and for the reciprocal of every group scale, div_rn
+// (reciprocal of the scale + one residual correction) inside quantize_four,
+// and group_scale's division by 448 (a constant reciprocal + one residual
+// correction).
 // check_arithmetic_kernel compares each with its IEEE / software form over a
 // range of fp32 bit patterns.
 #include "common.h"
@@ -94,12 +97,14 @@ __global__ __launch_bounds__(kCheckThreads) void check_e4m3_kernel(uint64_t firs
 // kind 0: pack_bf16x2 against f32_to_bf16 (NaN patterns skipped), pattern
 //   p in the low half next to p ^ 0x80000000 in the high half and the
 //   other way round;
-// kind 1: recip_rn(d) against 1.0f / d, d = pattern (inside [1, 2^126));
+// kind 1: recip_rn(d) against 1.0f / d, d = pattern (inside [2^-43, 2^126));
 // kind 2: the code and the quotient of div_rn(v, s, 1.0f / s) against
 //   v / s for v = +-pattern, s = scale (quotients from 2^-12 up compared
 //   bit for bit, smaller ones by their e4m3 code after the clamp);
 // kind 3: sigmoid_rn(g) against 1.0f / (1.0f + expf(-g)), g = pattern
-//   (NaN patterns skipped).
+//   (NaN patterns skipped);
+// kind 4: group_scale(m) against fmaxf(m, 1e-10f) / 448.0f, m = pattern
+//   (non-negative patterns up to +inf).
 __global__ __launch_bounds__(kCheckThreads) void check_arithmetic_kernel(int kind, uint64_t first, uint64_t count,
                                                                          float scale, uint32_t* __restrict__ result) {
   uint32_t mismatches = 0;
@@ -128,9 +133,11 @@ __global__ __launch_bounds__(kCheckThreads) void check_arithmetic_kernel(int kin
         if (fabsf(want) >= 0x1p-12f) bad |= __float_as_uint(got) != __float_as_uint(want);
         bad |= f32_to_e4m3(cw) != f32_to_e4m3(cg);
       }
-    } else {
+    } else if (kind == 3) {
       if ((p & 0x7fffffffu) <= 0x7f800000u)
         bad = __float_as_uint(sigmoid_rn(x)) != __float_as_uint(1.0f / (1.0f + expf(-x)));
+    } else {
+      if (p <= 0x7f800000u) bad = __float_as_uint(group_scale(x)) != __float_as_uint(fmaxf(x, 1e-10f) / 448.0f);
     }
     if (bad) {
       ++mismatches;
@@ -164,10 +171,10 @@ extern "C" int d3_check_e4m3_conversion(uint64_t first, uint64_t count, uint32_t
 extern "C" int d3_check_epilogue_arithmetic(int32_t kind, uint64_t first, uint64_t count, float scale,
                                             uint32_t* result, void* stream) {
   D3_REQUIRE(result != nullptr, "check_epilogue_arithmetic: null result");
-  D3_REQUIRE(kind >= 0 && kind <= 3, "check_epilogue_arithmetic: kind must be 0-3");
+  D3_REQUIRE(kind >= 0 && kind <= 4, "check_epilogue_arithmetic: kind must be 0-4");
   D3_REQUIRE(first + count <= (uint64_t{1} << 32), "check_epilogue_arithmetic: range beyond 2^32");
-  D3_REQUIRE(kind != 1 || (first >= 0x3f800000u && first + count <= 0x7e800000u),
-             "check_epilogue_arithmetic: reciprocal inputs must lie in [1, 2^126)");
+  D3_REQUIRE(kind != 1 || (first >= 0x2a000000u && first + count <= 0x7e800000u),
+             "check_epilogue_arithmetic: reciprocal inputs must lie in [2^-43, 2^126)");
   D3_REQUIRE(kind != 2 || (scale > 0.0f && first + count <= 0x7f800000u),
              "check_epilogue_arithmetic: division needs a positive scale and finite patterns");
   if (count == 0) {

@@ -62,20 +62,24 @@ extern "C" {
 int d3_check_e4m3_conversion(uint64_t first, uint64_t count, uint32_t *result, void *stream);
 
 /*
- * Device self-check of the arithmetic shortcuts of the SwiGLU requantisation
- * (no counterpart in the reference: it shows that the shortcuts give the
+ * Device self-check of the arithmetic shortcuts of the quantisers and the
+ * SwiGLU requantisation (no counterpart in the reference: it shows that the
+ * shortcuts give the
  * IEEE results the reference's rule moe_input.py:24-27 and silu
  * (kernels.py:392-394) ask for).  Over the fp32 bit patterns
  * [first, first + count):
  *   kind 0: hardware bf16 rounding (v_cvt_pk_bf16_f32) against the software
  *           round-to-nearest-even (NaN patterns skipped);
  *   kind 1: hardware reciprocal + one Newton-Raphson step against 1.0f / d
- *           (patterns inside [1, 2^126));
+ *           (patterns inside [2^-43, 2^126));
  *   kind 2: division by `scale` through its reciprocal + one residual
  *           correction against v / scale, for +v and -v (finite patterns):
  *           quotients from 2^-12 up bit for bit, all by e4m3 code;
  *   kind 3: the sigmoid 1 / (1 + expf(-g)) of the requantisation against
- *           its IEEE form (NaN patterns skipped).
+ *           its IEEE form (NaN patterns skipped);
+ *   kind 4: the group scale max(m, 1e-10) / 448 through a constant
+ *           reciprocal + one residual correction against the IEEE division
+ *           (non-negative patterns up to +inf).
  * result[0] += mismatches, result[1] = min(result[1], first bad pattern);
  * the caller initialises result to {0, 0xffffffff}.
  */

@@ -1,7 +1,9 @@
-"""The arithmetic shortcuts of the SwiGLU requantisation against their IEEE
-forms on the device (d3_check_epilogue_arithmetic): hardware bf16 rounding
-over every non-NaN fp32 pattern, the Newton-corrected hardware reciprocal
-over every d in [1, 2^126), the sigmoid over every non-NaN g, and the
+"""The arithmetic shortcuts of the quantisers and the SwiGLU requantisation
+against their IEEE forms on the device (d3_check_epilogue_arithmetic):
+hardware bf16 rounding over every non-NaN fp32 pattern, the Newton-corrected
+hardware reciprocal over every d in [2^-43, 2^126), the division by 448 of
+the group scale over every non-negative amax, the sigmoid over every
+non-NaN g, and the
 residual-corrected division over every |v| up to the group maximum for
 group scales max(amax, 1e-10) / 448 across the exponent range (the
 all-ones significand, the 1e-10 floor and scale 1 included)."""
@@ -33,8 +35,18 @@ def test_hardware_bf16_rounding_every_pattern(device):
 
 
 def test_newton_reciprocal_every_input(device):
-    count, first_bad = _run(device, 1, 0x3F800000, 0x7E800000)
+    """[2^-43, 2^126): the sigmoid's denominators 1 + exp(-g) from 1 on, and
+    every finite group scale, from RN(1e-10 / 448) (about 2^-42) up to
+    FLT_MAX / 448 (about 2^119)."""
+    count, first_bad = _run(device, 1, 0x2A000000, 0x7E800000)
     assert count == 0, f"{count} mismatches, first at d = {first_bad:#010x}"
+
+
+def test_group_scale_every_amax(device):
+    """group_scale(m) = max(m, 1e-10) / 448 through a constant reciprocal and
+    one residual correction, for every non-negative fp32 m up to +inf."""
+    count, first_bad = _run(device, 4, 0, 0x7F800001)
+    assert count == 0, f"{count} mismatches, first at m = {first_bad:#010x}"
 
 
 def test_sigmoid_every_input(device):
