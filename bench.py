@@ -68,6 +68,8 @@ def parse():
     p.add_argument("--mixed-steps", type=int, default=50)
     p.add_argument("--decode-config-only", type=int, choices=(1, 2, 3), default=None,
                    help="measure only this decode configuration's step (one JSON line)")
+    p.add_argument("--reference-shape-only", action="store_true",
+                   help="measure only the decode step at the reference model's shape (one JSON line)")
     p.add_argument("--layer-only", action="store_true",
                    help="measure only the whole MoE layer lines (64 and 4096 rows; one JSON line)")
     return p.parse_args()
@@ -615,6 +617,9 @@ def main():
     if args.decode_config_only is not None:
         print(json.dumps({"decode_config": bench_decode_config(torch, args.decode_config_only,
                                                                args.replays)}), flush=True)
+        return
+    if args.reference_shape_only:
+        print(json.dumps({"reference_shape": bench_reference_shape(torch)}), flush=True)
         return
     if args.layer_only:
         layer = bench_moe_layer(torch)

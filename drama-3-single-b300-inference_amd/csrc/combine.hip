@@ -113,7 +113,9 @@ struct RouteRows {
 // kMode 0: add_norm(x, residual); 1: combine_experts_add_norm(_inverse);
 // 2: mode 1 with each routed row reduced here from the per-route rows: the
 //    rank-order fp32 sum of d3_weighted_combine, rounded to bf16 as it does,
-//    so the bytes equal d3_weighted_combine followed by mode 1.
+//    so the bytes equal d3_weighted_combine followed by mode 1;
+// 3: mode 2 without the residual and the norm: out = the combined row, the
+//    bytes of d3_weighted_combine followed by d3_combine_experts.
 template <int kMode>
 __global__ __launch_bounds__(kThreads) void add_norm_kernel(
     const uint16_t* __restrict__ routed, const uint16_t* __restrict__ shared,
@@ -121,6 +123,8 @@ __global__ __launch_bounds__(kThreads) void add_norm_kernel(
     uint16_t* __restrict__ residual, const uint16_t* __restrict__ weight, float eps, int width,
     uint16_t* __restrict__ out, RouteRows routes) {
   __shared__ float scratch[kThreads / kWave];
+  constexpr bool kNorm = kMode != 3;
+  constexpr bool kRoutes = kMode >= 2;
   const int row = blockIdx.x;
   const int source = inverse != nullptr ? static_cast<int>(inverse[row]) : row;
   const int64_t src = static_cast<int64_t>(source) * width;
@@ -136,15 +140,17 @@ __global__ __launch_bounds__(kThreads) void add_norm_kernel(
   for (int column = threadIdx.x * 4; column < width; column += kThreads * 4, count += 4) {
     float r[4], res[4], v[4], s[4];
     uint16_t gate_bits = 0;
-    load4(weight + column, &norm[count]);
-    load4(residual + dst + column, res);
+    if constexpr (kNorm) {
+      load4(weight + column, &norm[count]);
+      load4(residual + dst + column, res);
+    }
     if constexpr (kMode != 0) {
       load4(shared + src + column, s);
       const uint16_t* gate_row = gate;
       asm volatile("" : "+s"(gate_row));  // loaded here, not hoisted out of the loop and waited for
       gate_bits = gate_row[static_cast<int64_t>(source) * gate_stride];
     }
-    if constexpr (kMode == 2) {
+    if constexpr (kRoutes) {
       const float4 sum = routes.top_k == 8
                              ? combine4_fixed<8>(routes.down, routes.weights, routes.weights_f32,
                                                  source, width, column)
@@ -157,7 +163,13 @@ __global__ __launch_bounds__(kThreads) void add_norm_kernel(
     } else {
       load4(routed + src + column, r);
     }
-    if constexpr (kMode != 0) {
+    if constexpr (!kNorm) {
+      const float g = gate_sigmoid_bf16(gate_bits);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = fma_bf16(s[i], g, r[i]);
+      store4(out + dst + column, v);
+      continue;
+    } else if constexpr (kMode != 0) {
       const float g = gate_sigmoid_bf16(gate_bits);
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = round_bf16(fma_bf16(s[i], g, r[i]) + res[i]);
@@ -172,6 +184,7 @@ __global__ __launch_bounds__(kThreads) void add_norm_kernel(
       squares += v[i] * v[i];
     }
   }
+  if constexpr (!kNorm) return;
   const float total = block_sum(squares, scratch);
   const float inv = 1.0f / sqrtf(total / static_cast<float>(width) + eps);
   count = 0;
@@ -413,24 +426,29 @@ extern "C" int d3_combine_routes_add_norm(const float* down, const void* route_w
                                           uint16_t* residual, const uint16_t* weight, float eps,
                                           int32_t rows, int32_t width, uint16_t* out,
                                           void* stream) {
-  D3_REQUIRE(down && route_weights && shared && gate && residual && weight && out,
+  D3_REQUIRE(down && route_weights && shared && gate && out && (residual == nullptr || weight),
              "combine_routes_add_norm: null pointer");
   D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
              "combine_routes_add_norm: weights must be bf16 or f32");
   D3_REQUIRE(top_k >= 1 && top_k <= 16, "combine_routes_add_norm: bad top_k %d", top_k);
   D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0 && width <= kThreads * kMaxPerThread,
              "combine_routes_add_norm: width %d must be a multiple of 4 and <= 8192", width);
-  D3_REQUIRE((reinterpret_cast<uintptr_t>(down) & 15u) == 0 && aligned8(shared) &&
-                 aligned8(residual) && aligned8(out) && aligned8(weight),
+  D3_REQUIRE((reinterpret_cast<uintptr_t>(down) & 15u) == 0 && aligned8(shared) && aligned8(out) &&
+                 (residual == nullptr || (aligned8(residual) && aligned8(weight))),
              "combine_routes_add_norm: alignment");
   if (rows == 0) {
     clear_error();
     return D3_OK;
   }
   const RouteRows routes{down, route_weights, weights_dtype == D3_DTYPE_F32 ? 1 : 0, top_k};
-  hipLaunchKernelGGL(add_norm_kernel<2>, dim3(rows), dim3(kThreads), 0, as_stream(stream),
-                     nullptr, shared, gate, gate_stride, inverse, residual, weight, eps, width,
-                     out, routes);
+  if (residual == nullptr)  // combine_experts of the routed combine, no norm
+    hipLaunchKernelGGL(add_norm_kernel<3>, dim3(rows), dim3(kThreads), 0, as_stream(stream),
+                       nullptr, shared, gate, gate_stride, inverse, nullptr, nullptr, eps, width,
+                       out, routes);
+  else
+    hipLaunchKernelGGL(add_norm_kernel<2>, dim3(rows), dim3(kThreads), 0, as_stream(stream),
+                       nullptr, shared, gate, gate_stride, inverse, residual, weight, eps, width,
+                       out, routes);
   D3_LAUNCHED("combine_routes_add_norm");
 }
 

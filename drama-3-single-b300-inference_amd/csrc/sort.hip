@@ -4,6 +4,7 @@
 // prefill-sized batches, which spreads the stable ranking over many
 // workgroups (one 1024-thread workgroup walks a 29k-pair batch in 29
 // dependent chunks: 56 us on MI355X).
+#include "expert_tile.h"
 #include "route_sort.h"
 #include "status.h"
 
@@ -40,15 +41,15 @@ __global__ __launch_bounds__(kSortThreads) void sort_routes_kernel(
 //      LDS, a running per-expert base across sub-chunks), and writes the
 //      chunk's expert histogram;
 //   2. wide_scan_kernel: one workgroup turns the chunk histograms into
-//      per-chunk expert offsets (exclusive scan over chunks), then the
-//      padded expert scan, work items, expert ids and sentinel padding;
+//      per-chunk expert offsets (exclusive scan over chunks, 1024 / E
+//      threads per expert), then the padded expert scan, work items, expert
+//      ids and sentinel padding;
 //   3. wide_scatter_kernel: sorted_ids[starts[e] + chunk offset + rank] = p.
 // Scratch: chunk histograms [chunks][E] and ranks [pairs] (int32).
 // ---------------------------------------------------------------------------
 constexpr int kWideThreads = 256;
 constexpr int kWideChunk = 512;
-constexpr int kWideScanLds = 12288;  // chunk histogram cells staged in LDS (48 KiB)
-static_assert(kWideScanLds % kSortThreads == 0, "whole staging rounds per thread");
+constexpr int kScanRegs = 16;  // chunk counts a scan thread holds in registers
 
 template <bool kI64>
 __global__ __launch_bounds__(kWideThreads) void wide_rank_kernel(
@@ -113,67 +114,65 @@ __global__ __launch_bounds__(kWideThreads) void wide_rank_kernel(
 __global__ __launch_bounds__(kSortThreads) void wide_scan_kernel(
     int rows, const int32_t* __restrict__ row_count, int top_k, int num_experts, int tile,
     int item_rows, int chunks, int32_t* __restrict__ chunk_counts, SortOutputs out) {
-  extern __shared__ int smem[];
-  int* wave_totals = smem;                      // [kSortThreads / 64]
-  int* staged = smem + kSortThreads / kWave;    // [chunks][E] when it fits
+  __shared__ int wave_totals[kSortThreads / kWave];
+  __shared__ int partial[kSortThreads];               // [E][share] chunk-range sums
+  __shared__ int expert_info[3 * kMaxSortExperts];    // count, start, first item per expert
   const int pairs = live_rows(row_count, rows) * top_k;
   const int tid = threadIdx.x;
-  const int cells = chunks * num_experts;
-  const bool in_lds = cells <= kWideScanLds;
-  if (in_lds) {
-    // Every load issued before the first LDS store: one memory round trip
-    // (a loop that stores as it loads waits for each load in turn).
-    constexpr int kPerThread = kWideScanLds / kSortThreads;
-    int v[kPerThread];
+  // Expert e is handled by `share` threads (e, j), thread j owning the
+  // contiguous chunk range [c0, c1); E <= 512 gives share >= 2.
+  const int share = kSortThreads / num_experts;
+  const int e = tid / share;
+  const int j = tid - e * share;
+  const bool owner = e < num_experts;
+  const int per = (chunks + share - 1) / share;
+  const int c0 = j * per;
+  const int c1 = min(chunks, c0 + per);
+  const uint32_t cells = static_cast<uint32_t>(chunks) * num_experts;
+  const BufferView count_view(chunk_counts, cells * 4);
+  auto cell = [&](int c) { return owner && c < c1 ? static_cast<uint32_t>(c * num_experts + e) * 4 : kNoRow; };
+  // Per expert: exclusive scan of its chunk counts over the chunks (written
+  // back in place as the chunk offsets) and its count.  A thread's range is
+  // read in batches of kScanRegs cells, every load of a batch issued before
+  // the first use (branch-free: cells outside the range read zero through
+  // the buffer bounds); ranges of at most kScanRegs chunks (up to 64k pairs
+  // at E = 128, 32k at E = 256) stay in registers between the sum and the
+  // write-back, longer ones are read twice.
+  int v[kScanRegs];
+  int sum = 0;
+  for (int b = c0; b < c1; b += kScanRegs) {
 #pragma unroll
-    for (int b = 0; b < kPerThread; ++b) {
-      const int i = b * kSortThreads + tid;
-      v[b] = i < cells ? chunk_counts[i] : 0;
-    }
+    for (int q = 0; q < kScanRegs; ++q) v[q] = static_cast<int>(count_view.load4(cell(b + q)));
 #pragma unroll
-    for (int b = 0; b < kPerThread; ++b) {
-      const int i = b * kSortThreads + tid;
-      if (i < cells) staged[i] = v[b];
-    }
-    __syncthreads();
+    for (int q = 0; q < kScanRegs; ++q) sum += v[q];
   }
-  // Per expert: exclusive scan of its chunk counts (offsets written back in
-  // place) -> count.  Staged in LDS, each expert's chunks are split over
-  // `share` threads (contiguous chunk ranges, their partial sums scanned in
-  // LDS), so the serial chain is chunks / share long.
-  int count = 0;
-  if (in_lds) {
-    int* partial = staged + cells;  // [E][share]
-    const int share = kSortThreads / num_experts;
-    const int e = tid / share;
-    const int j = tid % share;
-    const int per = (chunks + share - 1) / share;
-    const int c0 = j * per;
-    const int c1 = min(chunks, c0 + per);
-    int sum = 0;
-    if (e < num_experts)
-      for (int c = c0; c < c1; ++c) sum += staged[c * num_experts + e];
-    if (e < num_experts) partial[e * share + j] = sum;
-    __syncthreads();
-    if (e < num_experts) {
-      int base = 0;
-      for (int q = 0; q < j; ++q) base += partial[e * share + q];
-      for (int c = c0; c < c1; ++c) {
-        const int v = staged[c * num_experts + e];
-        chunk_counts[static_cast<size_t>(c) * num_experts + e] = base;
-        base += v;
+  partial[tid] = sum;
+  __syncthreads();
+  int base = 0;
+  for (int q = 0; q < j; ++q) base += partial[e * share + q];
+  if (owner) {
+    if (per <= kScanRegs) {
+#pragma unroll
+      for (int q = 0; q < kScanRegs; ++q) {
+        if (c0 + q < c1) chunk_counts[static_cast<size_t>(c0 + q) * num_experts + e] = base;
+        base += v[q];
+      }
+    } else {
+      for (int b = c0; b < c1; b += kScanRegs) {
+#pragma unroll
+        for (int q = 0; q < kScanRegs; ++q) v[q] = static_cast<int>(count_view.load4(cell(b + q)));
+#pragma unroll
+        for (int q = 0; q < kScanRegs; ++q) {
+          if (b + q < c1) chunk_counts[static_cast<size_t>(b + q) * num_experts + e] = base;
+          base += v[q];
+        }
       }
     }
-    if (tid < num_experts)
-      for (int q = 0; q < share; ++q) count += partial[tid * share + q];
-  } else if (tid < num_experts) {
-    for (int c = 0; c < chunks; ++c) {
-      int32_t* slot = chunk_counts + static_cast<size_t>(c) * num_experts + tid;
-      const int v = *slot;
-      *slot = count;
-      count += v;
-    }
   }
+  int count = 0;
+  if (tid < num_experts)
+    for (int q = 0; q < share; ++q) count += partial[tid * share + q];
+  // Padded expert scan and work items (thread e < E holds expert e).
   const int padded = (count + tile - 1) / tile * tile;
   int total = 0;
   const int start = block_inclusive_scan<kSortThreads>(padded, wave_totals, &total) - padded;
@@ -182,17 +181,28 @@ __global__ __launch_bounds__(kSortThreads) void wide_scan_kernel(
   const int item_base =
       block_inclusive_scan<kSortThreads>(my_items, wave_totals, &total_items) - my_items;
   if (tid < num_experts) {
-    const int e = tid;
-    for (int i = count; i < padded; ++i) out.sorted_ids[start + i] = pairs;
+    expert_info[3 * tid] = count;
+    expert_info[3 * tid + 1] = start;
+    expert_info[3 * tid + 2] = item_base;
+    if (out.counts != nullptr) out.counts[tid] = count;
+    out.starts[tid] = start;
+  }
+  __syncthreads();
+  // Each expert's sentinel padding, expert ids and work items, spread over
+  // its `share` threads.
+  if (owner) {
+    const int e_count = expert_info[3 * e], e_start = expert_info[3 * e + 1];
+    const int e_padded = (e_count + tile - 1) / tile * tile;
+    for (int i = e_count + j; i < e_padded; i += share) out.sorted_ids[e_start + i] = pairs;
     if (out.expert_ids != nullptr)
-      for (int b = 0; b < padded / tile; ++b) out.expert_ids[start / tile + b] = e;
-    if (out.counts != nullptr) out.counts[e] = count;
-    out.starts[e] = start;
-    if (out.items != nullptr)
-      for (int j = 0; j < my_items; ++j) {
-        const int routes = count - j * item_rows < item_rows ? count - j * item_rows : item_rows;
-        out.items[item_base + j] = make_int4(e, start + j * item_rows, routes, 0);
+      for (int t = j; t < e_padded / tile; t += share) out.expert_ids[e_start / tile + t] = e;
+    if (out.items != nullptr) {
+      const int e_items = (e_count + item_rows - 1) / item_rows, e_item_base = expert_info[3 * e + 2];
+      for (int it = j; it < e_items; it += share) {
+        const int routes = min(item_rows, e_count - it * item_rows);
+        out.items[e_item_base + it] = make_int4(e, e_start + it * item_rows, routes, 0);
       }
+    }
   }
   for (int i = total + tid; i < out.max_rows; i += kSortThreads) out.sorted_ids[i] = pairs;
   if (out.expert_ids != nullptr)
@@ -345,10 +355,6 @@ extern "C" int d3_sort_routes_wide(const void* ids, int32_t ids_dtype, int32_t r
                         reinterpret_cast<int4*>(items), max_items, num_items, pairs_out};
   hipStream_t s = as_stream(stream);
   const size_t rank_shared = sizeof(int) * static_cast<size_t>(num_experts) * (1 + kWideThreads / kWave);
-  const int cells = chunks * num_experts;
-  // wave totals + staged chunk counts + per-thread partial sums
-  const size_t scan_shared =
-      sizeof(int) * (kSortThreads / kWave + (cells <= kWideScanLds ? cells + kSortThreads : 0));
   const int scatter_blocks = static_cast<int>((pairs + kWideThreads - 1) / kWideThreads);
   if (chunks > 0) {
     if (ids_dtype == D3_DTYPE_I64)
@@ -358,7 +364,7 @@ extern "C" int d3_sort_routes_wide(const void* ids, int32_t ids_dtype, int32_t r
       hipLaunchKernelGGL(wide_rank_kernel<false>, dim3(chunks), dim3(kWideThreads), rank_shared, s, ids,
                          rows, row_count, top_k, num_experts, chunk_counts, ranks);
   }
-  hipLaunchKernelGGL(wide_scan_kernel, dim3(1), dim3(kSortThreads), scan_shared, s, rows, row_count,
+  hipLaunchKernelGGL(wide_scan_kernel, dim3(1), dim3(kSortThreads), 0, s, rows, row_count,
                      top_k, num_experts, tile, item_rows, chunks, chunk_counts, out);
   if (scatter_blocks > 0) {
     if (ids_dtype == D3_DTYPE_I64)

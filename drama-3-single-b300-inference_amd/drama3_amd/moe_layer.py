@@ -17,7 +17,9 @@ rows the routed experts are the decode step, whose combine is folded into
 the layer's (``d3_combine_route_logits``: routing weights, rank-order
 routed sum, gated shared add and optionally the residual + RMSNorm of
 ``combine_experts_add_norm``, one launch); larger batches run the prefill
-path.  ``overlap`` puts the shared expert on a default-priority side stream
+path, whose routed combine is folded into the layer's the same way
+(``d3_combine_routes_add_norm`` over the fp32 per-route rows).  ``overlap``
+puts the shared expert on a default-priority side stream
 forked after the projection and joined before the combine.
 """
 
@@ -163,9 +165,12 @@ class MoELayer:
                 and step.uses_frontless(self.all_rows, x, router) and self.hidden <= 2048
                 and self.num_experts <= 256)
 
-    def _routed_and_shared(self, x, projection, down_proj, experts, fuse: bool):
-        """Projection, routed experts (without their combine when ``fuse``)
-        and shared expert; returns the router logits view."""
+    def _routed_and_shared(self, x, projection, down_proj, experts, fuse: bool,
+                           routes: bool = False):
+        """Projection, routed experts (without their combine when ``fuse``,
+        the decode step's; or when ``routes``, the prefill path's: the fp32
+        per-route rows only) and shared expert; returns the router logits
+        view."""
         self._check(x, projection, down_proj)
         main = torch.cuda.current_stream(self.device)
         self._project(x, projection)
@@ -183,6 +188,10 @@ class MoELayer:
             ws.decode_fc2(experts, self.step.count, stream)
         elif self.decode:
             self.routed = self.step(self.all_rows, x, router, experts)
+        elif routes:
+            stream = _lib.stream(self.device)
+            self.workspace.front(x, router, stream=stream)
+            self.workspace.routes_down(experts, stream=stream)
         else:
             self.workspace.forward(x, router, experts, out=self.routed)
         if self.side is None:
@@ -202,10 +211,19 @@ class MoELayer:
     def _combine(self, x, projection, down_proj, experts, residual=None, norm_weight=None,
                  eps=0.0, out=None) -> torch.Tensor:
         fuse = self._fused(experts, x, self._views()[1])
-        router = self._routed_and_shared(x, projection, down_proj, experts, fuse)
+        # prefill-sized batches: the routed combine folds into the gated
+        # shared add (and the norm), one launch over the per-route rows
+        routes = not self.decode
+        router = self._routed_and_shared(x, projection, down_proj, experts, fuse, routes)
         _, _, gate = self._views()
         stream = _lib.stream(self.device)
-        if fuse:
+        if routes:
+            ws = self.workspace
+            call("d3_combine_routes_add_norm", ptr(ws.down), ptr(ws.weights),
+                 dtype_code(ws.weights.dtype), ws.shape.top_k, ptr(self.shared), ptr(gate),
+                 gate.stride(0), None, ptr(residual), ptr(norm_weight), float(eps), self.rows,
+                 self.hidden, ptr(out), stream)
+        elif fuse:
             ws = self.step.workspace
             call("d3_combine_route_logits", ptr(ws.down), ptr(router), DTYPE_BF16, router.stride(0),
                  self.num_experts, ws.shape.top_k, ptr(ws.weights), dtype_code(ws.weights.dtype),

@@ -578,7 +578,9 @@ int d3_combine_experts_add_norm(const uint16_t *routed, const uint16_t *shared,
  * d3_combine_experts_add_norm rule.  down f32 [MoE rows * top_k, width]
  * (16-byte aligned); w bf16 or f32 [MoE rows, top_k]; shared bf16
  * [MoE rows, width]; gate bf16 (row stride gate_stride); residual bf16
- * [rows, width] updated in place; out bf16 [rows, width].  width <= 8192.
+ * [rows, width] updated in place; out bf16 [rows, width].  With residual ==
+ * NULL (weight and eps unused) out[r] = the combined row: the bytes of
+ * d3_weighted_combine followed by d3_combine_experts.  width <= 8192.
  */
 int d3_combine_routes_add_norm(const float *down, const void *route_weights,
                                int32_t weights_dtype, int32_t top_k, const uint16_t *shared,
