@@ -33,8 +33,8 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 # this script (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors read off
 # the 1 GiB device copy in the same runs); profiles/expert_gemm_c2_hbm_traffic.md.
 # Re-measure whenever the FC1 kernel or its tiling changes.
-FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,1,6,1,true>", "bytes": 401743160,
-                     "measured_on": "4d5527a (profiles/expert_gemm_c2_hbm_traffic.md)"}
+FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,1,6,1,true>", "bytes": 401749606,
+                     "measured_on": "bb4fea4 (profiles/expert_gemm_c2_hbm_traffic.md)"}
 
 
 def parse():
