@@ -17,7 +17,11 @@
 //     two-slot LDS ring (128 routes x 144-byte rows; the 16-byte pad keeps
 //     the 16 rows of each ds_read_b128 on distinct banks); their loads are
 //     issued before the weights', so waiting for them never waits for the
-//     weights.  One barrier per K block.
+//     weights.  The next block's loads are issued in units spread over the
+//     current block's route tiles (one activation copy or one weight tile
+//     per route tile): issued in one block at its top they held the wave's
+//     MFMAs back while the memory pipeline drained (3 % slower per GEMM).
+//     One barrier per K block.
 //   * Measured per workgroup (per-workgroup timestamps, config-4 FC1): the
 //     prologue (item, route ids, scales, first blocks) and the epilogue
 //     cost a third of a workgroup's time; two resident workgroups per CU
@@ -336,12 +340,33 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
     for (int rt = 0; rt < kRT; ++rt) acc[t][rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // The next K block's loads in issue units (activation staging copies
+  // first, so that waiting for them never waits for the weights; then one
+  // weight tile, two loads, per unit), spread over the route tiles of the
+  // current block so the MFMAs keep issuing while the loads go out.
+  constexpr int kUnits = kStaged + kGgWaveTiles;
+  auto issue_unit = [&](int kb, int u) {
+    if (u < kStaged) {
+      staged[u] = view.load16(src[u] + kb * kGroup);
+    } else {
+      const int t = u - kStaged;
+      const uint32_t base = static_cast<uint32_t>(tile_row(t)) * K;
+      int32x4 lo, hi;
+      if constexpr (kPacked) {
+        lo = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, base + kb * 2048, kNonTemporal);
+        hi = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, base + kb * 2048 + 1024, kNonTemporal);
+      } else {
+        lo = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, base + kb * kGroup, 0);
+        hi = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, base + kb * kGroup + 64, 0);
+      }
+      int32x8 v;
+      v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
+      v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
+      wf[kb & 1][t] = v;
+    }
+  };
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
-    if (kb + 1 < KB) {
-      stage_load(kb + 1);  // before the weights: waiting for it never waits for them
-      load_weights(kb + 1);
-    }
     // Keep each K block's loads in its own iteration (the unrolled loop would
     // otherwise let the scheduler hoist later blocks' loads).
     __builtin_amdgcn_sched_barrier(0);
@@ -356,6 +381,11 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
     float as_prev = 0.0f;
 #pragma unroll
     for (int rt = 0; rt <= kRT; ++rt) {
+      if (kb + 1 < KB) {  // units rt (and, on the last route tile, the rest)
+#pragma unroll
+        for (int u = 0; u < kUnits; ++u)
+          if (u == rt || (rt == kRT - 1 && u >= kRT)) issue_unit(kb + 1, u);
+      }
       float as = 0.0f;
       if (rt < kRT) {
         const int route = 16 * rt + row16;
