@@ -385,7 +385,7 @@ using namespace d3;
 extern "C" int d3_combine_experts(const uint16_t* routed, const uint16_t* shared,
                                   const uint16_t* gate, int64_t gate_stride, int32_t rows,
                                   int32_t width, uint16_t* out, void* stream) {
-  D3_REQUIRE(routed && shared && gate && out, "combine_experts: null pointer");
+  D3_REQUIRE(rows == 0 || (routed && shared && gate && out), "combine_experts: null pointer");
   D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0, "combine_experts: width %% 4 != 0");
   D3_REQUIRE(aligned8(routed) && aligned8(shared) && aligned8(out), "combine_experts: alignment");
   if (rows == 0) {
@@ -402,7 +402,7 @@ extern "C" int d3_combine_experts_add_norm(const uint16_t* routed, const uint16_
                                            const int64_t* inverse, uint16_t* residual,
                                            const uint16_t* weight, float eps, int32_t rows,
                                            int32_t width, uint16_t* out, void* stream) {
-  D3_REQUIRE(routed && shared && gate && residual && weight && out,
+  D3_REQUIRE(rows == 0 || (routed && shared && gate && residual && weight && out),
              "combine_experts_add_norm: null pointer");
   D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0 && width <= kThreads * kMaxPerThread,
              "combine_experts_add_norm: width %d must be a multiple of 4 and <= 8192", width);
@@ -426,7 +426,7 @@ extern "C" int d3_combine_routes_add_norm(const float* down, const void* route_w
                                           uint16_t* residual, const uint16_t* weight, float eps,
                                           int32_t rows, int32_t width, uint16_t* out,
                                           void* stream) {
-  D3_REQUIRE(down && route_weights && shared && gate && out && (residual == nullptr || weight),
+  D3_REQUIRE(rows == 0 || (down && route_weights && shared && gate && out && (residual == nullptr || weight)),
              "combine_routes_add_norm: null pointer");
   D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
              "combine_routes_add_norm: weights must be bf16 or f32");
@@ -454,7 +454,7 @@ extern "C" int d3_combine_routes_add_norm(const float* down, const void* route_w
 
 extern "C" int d3_add_norm(const uint16_t* x, uint16_t* residual, const uint16_t* weight, float eps,
                            int32_t rows, int32_t width, uint16_t* out, void* stream) {
-  D3_REQUIRE(x && residual && weight && out, "add_norm: null pointer");
+  D3_REQUIRE(rows == 0 || (x && residual && weight && out), "add_norm: null pointer");
   D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0 && width <= kThreads * kMaxPerThread,
              "add_norm: width %d must be a multiple of 4 and <= 8192", width);
   D3_REQUIRE(aligned8(x) && aligned8(residual) && aligned8(out) && aligned8(weight),
@@ -470,7 +470,7 @@ extern "C" int d3_add_norm(const uint16_t* x, uint16_t* residual, const uint16_t
 
 extern "C" int d3_silu_mul(const uint16_t* projected, int64_t row_stride, int32_t rows,
                            int32_t width, uint16_t* out, void* stream) {
-  D3_REQUIRE(projected && out, "silu_mul: null pointer");
+  D3_REQUIRE(rows == 0 || (projected && out), "silu_mul: null pointer");
   D3_REQUIRE(rows >= 0 && width > 0 && width % 4 == 0 && row_stride >= 2 * width &&
                  row_stride % 4 == 0,
              "silu_mul: bad shape");
@@ -491,7 +491,7 @@ extern "C" int d3_combine_route_logits(const float* down, const void* logits, in
                                        int64_t gate_stride, uint16_t* residual,
                                        const uint16_t* weight, float eps, int32_t rows,
                                        int32_t width, uint16_t* out, void* stream) {
-  D3_REQUIRE(down && logits && shared && gate && out && (residual == nullptr || weight != nullptr),
+  D3_REQUIRE(rows == 0 || (down && logits && shared && gate && out && (residual == nullptr || weight != nullptr)),
              "combine_route_logits: null pointer");
   D3_REQUIRE(logits_dtype == D3_DTYPE_BF16 || logits_dtype == D3_DTYPE_F32,
              "combine_route_logits: logits must be bf16 or f32");

@@ -438,7 +438,7 @@ using namespace d3;
 extern "C" int d3_dense_bf16(const uint16_t* x, int64_t x_stride, int32_t rows, const uint16_t* w,
                              int32_t n, int32_t k, int32_t pair_rows, uint16_t* out,
                              int64_t out_stride, uint16_t* act, int64_t act_stride, void* stream) {
-  D3_REQUIRE(x && w && out, "dense_bf16: null pointer");
+  D3_REQUIRE(rows == 0 || (x && w && out), "dense_bf16: null pointer");
   D3_REQUIRE(rows >= 0 && n > 0 && k > 0 && pair_rows >= 0 && 2 * pair_rows <= n,
              "dense_bf16: rows %d, N %d, K %d, pair_rows %d", rows, n, k, pair_rows);
   D3_SUPPORTED(n % 16 == 0 && pair_rows % 16 == 0, "dense_bf16: N=%d and pair_rows %d must be multiples of 16",

@@ -254,8 +254,8 @@ extern "C" int d3_route(const void* logits, int32_t logits_dtype, int64_t logits
                         int32_t rows, int32_t num_experts, int32_t top_k,
                         const int32_t* row_index, const int32_t* row_count, int32_t* ids32,
                         int64_t* ids64, void* weights, int32_t weights_dtype, void* stream) {
-  D3_REQUIRE(logits && weights, "route: null logits or weights");
-  D3_REQUIRE(ids32 || ids64, "route: need ids32 or ids64");
+  D3_REQUIRE(rows == 0 || (logits && weights), "route: null logits or weights");
+  D3_REQUIRE(rows == 0 || ids32 || ids64, "route: need ids32 or ids64");
   D3_REQUIRE(logits_dtype == D3_DTYPE_BF16 || logits_dtype == D3_DTYPE_F32,
              "route: logits must be bf16 or f32");
   D3_REQUIRE(weights_dtype == D3_DTYPE_BF16 || weights_dtype == D3_DTYPE_F32,
@@ -299,7 +299,7 @@ extern "C" int d3_quantize_rows(const uint16_t* x, int64_t x_row_stride, int32_t
                                 int32_t width, const int32_t* row_index,
                                 const int32_t* row_count, uint8_t* q, float* scales,
                                 int32_t scales_transposed, void* stream) {
-  D3_REQUIRE(x && q && scales, "quantize_rows: null pointer");
+  D3_REQUIRE(rows == 0 || (x && q && scales), "quantize_rows: null pointer");
   D3_REQUIRE(rows >= 0 && width > 0 && width % kGroup == 0,
              "quantize_rows: width %d must be a positive multiple of 128", width);
   D3_SUPPORTED(width <= kMaxRowChunks * 8 * kWave, "quantize_rows: width %d > 4096", width);
@@ -323,7 +323,7 @@ extern "C" int d3_prepare_moe_input(const uint16_t* x, int64_t x_row_stride, con
                                     const void* row_slots, int32_t row_slots_dtype,
                                     int64_t padding_start, uint8_t* q, float* scales,
                                     float* logits, void* stream) {
-  D3_REQUIRE(x && router && q && scales && logits, "prepare_moe_input: null pointer");
+  D3_REQUIRE(rows == 0 || (x && router && q && scales && logits), "prepare_moe_input: null pointer");
   D3_REQUIRE(rows >= 0 && hidden > 0 && hidden % kGroup == 0,
              "prepare_moe_input: hidden %d must be a positive multiple of 128", hidden);
   D3_SUPPORTED(hidden <= kMaxRowChunks * 8 * kWave, "prepare_moe_input: hidden %d > 4096", hidden);

@@ -21,6 +21,10 @@
  * Device row counts: wherever `row_count` appears, a non-NULL pointer names an
  * int32 on the device holding the live number of rows (<= the host `rows`
  * capacity); rows at or beyond it are left untouched.  NULL means all `rows`.
+ * Empty batches: the elementwise and dense entry points (route, quantize_rows,
+ * prepare_moe_input, combine_*, add_norm, silu_mul, dense_bf16) accept
+ * rows = 0 with NULL buffers, launch nothing and return D3_OK; their shape
+ * arguments are still checked.
  *
  * Return value: D3_OK or a D3_ERR_* code; d3_last_error() describes the
  * failure of the last call made on the calling thread.

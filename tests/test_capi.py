@@ -213,6 +213,32 @@ def test_route_fc1_and_combine_contract(lib):
         _lib.call("d3_decode_route_combine", *bad)
 
 
+def test_empty_batches_accept_null_buffers(lib):
+    """Zero rows: NULL row buffers are accepted and nothing is launched (the
+    calls below return before any HIP call); one row with the same NULLs is
+    still a contract violation, and shape checks still apply at zero rows."""
+    from drama3_amd import _lib
+
+    bf16 = _lib.DTYPE_BF16
+    for rows, ok in ((0, True), (1, False)):
+        calls = [
+            ("d3_route", (None, bf16, 16, rows, 16, 8, None, None, None, None, None, bf16, None)),
+            ("d3_quantize_rows", (None, 1024, rows, 1024, None, None, None, None, 0, None)),
+            ("d3_combine_experts", (None, None, None, 1, rows, 1024, None, None)),
+            ("d3_add_norm", (None, None, None, 1e-6, rows, 1024, None, None)),
+            ("d3_silu_mul", (None, 2048, rows, 1024, None, None)),
+            ("d3_dense_bf16", (None, 1024, rows, None, 256, 1024, 0, None, 256, None, 0, None)),
+        ]
+        for name, args in calls:
+            if ok:
+                _lib.call(name, *args)
+            else:
+                with pytest.raises(ValueError, match="null"):
+                    _lib.call(name, *args)
+    with pytest.raises(ValueError, match="width"):
+        _lib.call("d3_add_norm", None, None, None, 1e-6, 0, 1022, None, None)
+
+
 def test_product_code_does_not_import_the_oracle():
     package = ROOT / "drama-3-single-b300-inference_amd"
     for path in package.rglob("*.py"):

@@ -343,7 +343,8 @@ def test_fc2_swiglu_prologue_matches_separate_stages(device, hidden, inter, expe
                                                        (1, torch.float32, True)])
 def test_combine_routes_add_norm_equals_two_launches(device, top_k, wdtype, with_inverse):
     """d3_combine_routes_add_norm = d3_weighted_combine followed by
-    d3_combine_experts_add_norm, byte for byte (routed, residual and out)."""
+    d3_combine_experts_add_norm, byte for byte (routed, residual and out);
+    without a residual, d3_weighted_combine followed by d3_combine_experts."""
     from drama3_amd import _lib
     from drama3_amd._lib import call, ptr
 
@@ -369,9 +370,19 @@ def test_combine_routes_add_norm_equals_two_launches(device, top_k, wdtype, with
     res_b, out_b = res0.clone(), torch.empty_like(res0)
     call("d3_combine_routes_add_norm", ptr(down), ptr(w), wcode, top_k, ptr(shared), ptr(gate), 1,
          ptr(inverse), ptr(res_b), ptr(norm), 1e-6, n, width, ptr(out_b), stream)
+    # residual == NULL: the combined row only, the bytes of d3_weighted_combine
+    # followed by d3_combine_experts (gathered through inverse)
+    combined = torch.empty((moe_rows, width), dtype=torch.bfloat16, device=device)
+    call("d3_combine_experts", ptr(routed), ptr(shared), ptr(gate), 1, moe_rows, width,
+         ptr(combined), stream)
+    out_c = torch.full_like(res0, 5.0)
+    call("d3_combine_routes_add_norm", ptr(down), ptr(w), wcode, top_k, ptr(shared), ptr(gate), 1,
+         ptr(inverse), None, None, 0.0, n, width, ptr(out_c), stream)
     torch.cuda.synchronize()
     assert torch.equal(res_a.view(torch.int16), res_b.view(torch.int16))
     assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16))
+    want_c = combined[inverse] if inverse is not None else combined
+    assert torch.equal(out_c.view(torch.int16), want_c.view(torch.int16))
 
 
 # --------------------------------------------------------------------------- A12
@@ -490,3 +501,30 @@ def test_device_requests_known_answer(device):
     state.save(slots[:1], fresh)
     assert torch.equal(state.codes[5, 0], fresh[0, 1:])
     assert state.metadata[5].tolist() == [51, 1, 1, 1]
+
+
+# --------------------------------------------------------------------------- empty batches
+def test_empty_batches_launch_nothing_and_return_empty(device):
+    """Zero rows through every reference-named operator and the layer's
+    GEMM: empty outputs, no error (the reference's operators accept T = 0)."""
+    from drama3_amd import workloads
+    from drama3_amd.kernels import (add_norm, combine_experts, combine_experts_add_norm,
+                                    native_moe, route, routed_moe, small_batch_moe)
+    from drama3_amd.moe_layer import dense_bf16
+
+    experts = workloads.config1().experts.to(device)
+    x = torch.empty((0, 1024), dtype=torch.bfloat16, device=device)
+    logits = torch.empty((0, 16), dtype=torch.bfloat16, device=device)
+    weights, ids = route(logits)
+    assert weights.shape == (0, 8) and ids.shape == (0, 8)
+    for out in (routed_moe(x, logits, experts), small_batch_moe(x, ids, weights, experts),
+                native_moe(x, ids, weights, experts)):
+        assert out.shape == (0, 1024) and out.dtype == torch.bfloat16
+    gate = torch.empty((0,), dtype=torch.bfloat16, device=device)
+    norm = torch.zeros(1024, dtype=torch.bfloat16, device=device)
+    assert combine_experts(x, x, gate).shape == (0, 1024)
+    assert combine_experts_add_norm(x, x, gate, x.clone(), norm, 1e-6).shape == (0, 1024)
+    assert add_norm(x, x.clone(), norm, 1e-6).shape == (0, 1024)
+    w = torch.zeros((256, 1024), dtype=torch.bfloat16, device=device)
+    assert dense_bf16(x, w, torch.empty((0, 256), dtype=torch.bfloat16, device=device)).shape == (0, 256)
+    torch.cuda.synchronize()
