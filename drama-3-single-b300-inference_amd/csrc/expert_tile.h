@@ -121,41 +121,59 @@ __device__ __forceinline__ floatx4 mfma_block_bf16(int32x8 a, const bf16x8 b[4])
   return acc;
 }
 
-// SwiGLU of bf16-rounded gate / up pairs in fp32: a = (g * sigmoid(g)) * u
-// with sigmoid(g) = 1 / (1 + exp(-g)) in IEEE fp32 (the library expf, within
-// one ulp, and a correctly rounded reciprocal, recip_rn), the arithmetic of the
-// reference's in-repo SwiGLU (kernels.py:392-394) without its bf16 rounding
-// of silu(g).  Every kernel of this build that requantises FC1 outputs uses
-// these functions, so they agree bit for bit.
-//
-// N values at once: d >= 2^126 (g < -87.3, the reciprocal subnormal or
-// zero) takes the IEEE division, behind one wave-uniform branch for all N
-// values that real data never takes, so the common path is straight-line
-// code whose N exponentials and reciprocals the compiler can interleave.
+// exp(-g) as 2^(-g log2 e) on the hardware exponential, with log2 e split
+// into fp32 high and low parts (Cody and Waite's argument splitting): the
+// product -g * hi is formed with its exact rounding error (one fma), the low
+// part's contribution added to that error, and 2^(t + t_lo) taken as
+// 2^t * (1 + t_lo ln 2).  Six instructions against the library expf's
+// range reduction; measured on the device against the float64 sigmoid it
+// gives the same error distribution as expf over every bf16 input (at most
+// two ulps of the sigmoid, d3_check_epilogue_arithmetic kind 5).  -g is
+// clamped to [-88, 88], so every step stays finite (no inf * 0 in the
+// correction) and the result lies in [2^-127, 2^127]: exp(-g) itself
+// would overflow from -g > 88.7 on, and 1 + exp(-g) rounds to 1 from
+// -g < -16.7 on.
+__device__ __forceinline__ float exp_neg(float g) {
+  constexpr float kLog2eHi = 1.44269502162933349609375f;  // RN(log2 e)
+  constexpr float kLog2eLo = 1.925963033500011e-08f;      // RN(log2 e - kLog2eHi)
+  constexpr float kLn2 = 0.693147180559945309f;
+  const float x = __builtin_amdgcn_fmed3f(-g, -88.0f, 88.0f);
+  const float t = x * kLog2eHi;
+  const float t_lo = fmaf(x, kLog2eLo, fmaf(x, kLog2eHi, -t));
+  const float e = __builtin_amdgcn_exp2f(t);
+  return fmaf(e, t_lo * kLn2, e);
+}
+
+// sigmoid(g) = 1 / (1 + exp(-g)) in fp32: exp_neg and a correctly rounded
+// reciprocal (recip_rn), branch-free.  Where the true sigmoid is below
+// 2^-126 (g < -87.3, d = 1 + exp(-g) >= 2^126) the result is 0 or a
+// subnormal below 2^-125; no fp32 form keeps it exact there (1 + expf(-g)
+// overflows from g < -88.7 on, and the reference's own silu gives 0 from
+// there).  The SwiGLU requantisations quantise g * sigmoid(g) * u
+// (|g * sigmoid(g)| < 2^-118 there) against a group scale of at least
+// 1e-10 / 448, so they give the float64 oracle's code, a zero of the same
+// sign, unless |u| exceeds 2^67.  (A wave-uniform branch to the IEEE form
+// for such values cost the prefill FC1 launch 10 % even untaken: it keeps
+// the N values of a call from being interleaved with the code after it.)
 template <int N>
-__device__ __forceinline__ void sigmoid_rn_n(const float* g, float* sig) {
-  float d[N];
-  bool tiny = false;
+__device__ __forceinline__ void sigmoid_n(const float* g, float* sig) {
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    d[i] = 1.0f + expf(-g[i]);
-    sig[i] = recip_rn(d[i]);
-    tiny |= !(d[i] < 0x1p126f);
-  }
-  if (__builtin_amdgcn_ballot_w64(tiny)) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) sig[i] = d[i] < 0x1p126f ? sig[i] : 1.0f / d[i];
-  }
+  for (int i = 0; i < N; ++i) sig[i] = recip_rn(1.0f + exp_neg(g[i]));
 }
 __device__ __forceinline__ float sigmoid_rn(float g) {
   float sig;
-  sigmoid_rn_n<1>(&g, &sig);
+  sigmoid_n<1>(&g, &sig);
   return sig;
 }
+
+// SwiGLU of bf16-rounded gate / up pairs in fp32: a = (g * sigmoid(g)) * u,
+// the arithmetic of the reference's in-repo SwiGLU (kernels.py:392-394)
+// without its bf16 rounding of silu(g).  Every kernel of this build that
+// requantises FC1 outputs uses these functions, so they agree bit for bit.
 template <int N>
 __device__ __forceinline__ void swiglu_values(const float* g, const float* u, float* a) {
   float sig[N];
-  sigmoid_rn_n<N>(g, sig);
+  sigmoid_n<N>(g, sig);
 #pragma unroll
   for (int i = 0; i < N; ++i) a[i] = (g[i] * sig[i]) * u[i];
 }
@@ -167,7 +185,7 @@ __device__ __forceinline__ float swiglu_value(float g, float u) { return (g * si
 template <int N>
 __device__ __forceinline__ void silu_mul_values(const float* g, const float* u, float* a) {
   float sig[N];
-  sigmoid_rn_n<N>(g, sig);
+  sigmoid_n<N>(g, sig);
 #pragma unroll
   for (int i = 0; i < N; ++i) a[i] = bf16_to_f32(f32_to_bf16(g[i] * sig[i])) * u[i];
 }

@@ -11,12 +11,14 @@
 // The quantisers and the SwiGLU requantisation also take shortcuts that
 // must give the IEEE results: pack_bf16x2 (hardware bf16 rounding),
 // recip_rn (hardware reciprocal + one Newton-Raphson step) inside
-// sigmoid_rn and for the reciprocal of every group scale, div_rn
+// sigmoid_rn and for the reciprocal of every group scale, exp_neg (the
+// hardware exponential of a split product) inside sigmoid_rn, div_rn
 // (reciprocal of the scale + one residual correction) inside quantize_four,
 // and group_scale's division by 448 (a constant reciprocal + one residual
 // correction).
 // check_arithmetic_kernel compares each with its IEEE / software form over a
-// range of fp32 bit patterns.
+// range of fp32 bit patterns; the sigmoid, which is not correctly rounded,
+// with the float64 sigmoid rounded to fp32, within a stated number of ulps.
 #include "common.h"
 #include "expert_tile.h"
 #include "status.h"
@@ -101,18 +103,22 @@ __global__ __launch_bounds__(kCheckThreads) void check_e4m3_kernel(uint64_t firs
 // kind 2: the code and the quotient of div_rn(v, s, 1.0f / s) against
 //   v / s for v = +-pattern, s = scale (quotients from 2^-12 up compared
 //   bit for bit, smaller ones by their e4m3 code after the clamp);
-// kind 3: sigmoid_rn(g) against 1.0f / (1.0f + expf(-g)), g = pattern
-//   (NaN patterns skipped);
+// kind 3: sigmoid_rn(g) against RN(1 / (1 + exp(-g))) evaluated in float64,
+//   g = pattern (NaN patterns skipped): more than `scale` ulps apart where
+//   the reference is a normal number, or not below 2^-125 where it is not;
 // kind 4: group_scale(m) against fmaxf(m, 1e-10f) / 448.0f, m = pattern
-//   (non-negative patterns up to +inf).
+//   (non-negative patterns up to +inf);
+// kind 5: kind 3 for the bf16 inputs only, g = pattern << 16 (patterns
+//   below 2^16), the values every SwiGLU of this library feeds it.
 __global__ __launch_bounds__(kCheckThreads) void check_arithmetic_kernel(int kind, uint64_t first, uint64_t count,
                                                                          float scale, uint32_t* __restrict__ result) {
   uint32_t mismatches = 0;
   uint32_t first_bad = 0xffffffffu;
   const float inv = 1.0f / scale;
+  const uint32_t shift = kind == 5 ? 16 : 0;
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kCheckThreads;
   for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kCheckThreads + threadIdx.x; i < count; i += stride) {
-    const uint32_t p = static_cast<uint32_t>(first + i);
+    const uint32_t p = static_cast<uint32_t>(first + i) << shift;
     const float x = __uint_as_float(p);
     bool bad = false;
     if (kind == 0) {
@@ -133,9 +139,14 @@ __global__ __launch_bounds__(kCheckThreads) void check_arithmetic_kernel(int kin
         if (fabsf(want) >= 0x1p-12f) bad |= __float_as_uint(got) != __float_as_uint(want);
         bad |= f32_to_e4m3(cw) != f32_to_e4m3(cg);
       }
-    } else if (kind == 3) {
-      if ((p & 0x7fffffffu) <= 0x7f800000u)
-        bad = __float_as_uint(sigmoid_rn(x)) != __float_as_uint(1.0f / (1.0f + expf(-x)));
+    } else if (kind == 3 || kind == 5) {
+      if ((p & 0x7fffffffu) <= 0x7f800000u) {
+        const float want = static_cast<float>(1.0 / (1.0 + exp(-static_cast<double>(x))));
+        const float got = sigmoid_rn(x);
+        // both lie in [0, 1]: the bit patterns order the values
+        const uint32_t a = __float_as_uint(got), b = __float_as_uint(want);
+        bad = want >= 0x1p-126f ? static_cast<float>(a > b ? a - b : b - a) > scale : !(got < 0x1p-125f);
+      }
     } else {
       if (p <= 0x7f800000u) bad = __float_as_uint(group_scale(x)) != __float_as_uint(fmaxf(x, 1e-10f) / 448.0f);
     }
@@ -171,12 +182,16 @@ extern "C" int d3_check_e4m3_conversion(uint64_t first, uint64_t count, uint32_t
 extern "C" int d3_check_epilogue_arithmetic(int32_t kind, uint64_t first, uint64_t count, float scale,
                                             uint32_t* result, void* stream) {
   D3_REQUIRE(result != nullptr, "check_epilogue_arithmetic: null result");
-  D3_REQUIRE(kind >= 0 && kind <= 4, "check_epilogue_arithmetic: kind must be 0-4");
+  D3_REQUIRE(kind >= 0 && kind <= 5, "check_epilogue_arithmetic: kind must be 0-5");
   D3_REQUIRE(first + count <= (uint64_t{1} << 32), "check_epilogue_arithmetic: range beyond 2^32");
   D3_REQUIRE(kind != 1 || (first >= 0x2a000000u && first + count <= 0x7e800000u),
              "check_epilogue_arithmetic: reciprocal inputs must lie in [2^-43, 2^126)");
   D3_REQUIRE(kind != 2 || (scale > 0.0f && first + count <= 0x7f800000u),
              "check_epilogue_arithmetic: division needs a positive scale and finite patterns");
+  D3_REQUIRE(kind != 5 || first + count <= (uint64_t{1} << 16),
+             "check_epilogue_arithmetic: bf16 sigmoid inputs are patterns below 2^16");
+  D3_REQUIRE((kind != 3 && kind != 5) || scale >= 0.0f,
+             "check_epilogue_arithmetic: the sigmoid's ulp bound must be non-negative");
   if (count == 0) {
     clear_error();
     return D3_OK;

@@ -68,9 +68,9 @@ int d3_check_e4m3_conversion(uint64_t first, uint64_t count, uint32_t *result, v
 /*
  * Device self-check of the arithmetic shortcuts of the quantisers and the
  * SwiGLU requantisation (no counterpart in the reference: it shows that the
- * shortcuts give the
- * IEEE results the reference's rule moe_input.py:24-27 and silu
- * (kernels.py:392-394) ask for).  Over the fp32 bit patterns
+ * shortcuts give the IEEE results the reference's rule moe_input.py:24-27
+ * asks for, and bounds the sigmoid of its silu (kernels.py:392-394) against
+ * the float64 sigmoid).  Over the fp32 bit patterns
  * [first, first + count):
  *   kind 0: hardware bf16 rounding (v_cvt_pk_bf16_f32) against the software
  *           round-to-nearest-even (NaN patterns skipped);
@@ -79,11 +79,16 @@ int d3_check_e4m3_conversion(uint64_t first, uint64_t count, uint32_t *result, v
  *   kind 2: division by `scale` through its reciprocal + one residual
  *           correction against v / scale, for +v and -v (finite patterns):
  *           quotients from 2^-12 up bit for bit, all by e4m3 code;
- *   kind 3: the sigmoid 1 / (1 + expf(-g)) of the requantisation against
- *           its IEEE form (NaN patterns skipped);
+ *   kind 3: the sigmoid 1 / (1 + exp(-g)) of the SwiGLU (hardware
+ *           exponential of a split product, Newton-corrected reciprocal)
+ *           against the float64 sigmoid rounded to fp32: a mismatch is more
+ *           than `scale` ulps apart where the reference is normal, or a
+ *           result not below 2^-125 where it is not (NaN patterns skipped);
  *   kind 4: the group scale max(m, 1e-10) / 448 through a constant
  *           reciprocal + one residual correction against the IEEE division
- *           (non-negative patterns up to +inf).
+ *           (non-negative patterns up to +inf);
+ *   kind 5: kind 3 over the bf16 inputs: g = pattern << 16 for the patterns
+ *           [first, first + count) inside [0, 2^16).
  * result[0] += mismatches, result[1] = min(result[1], first bad pattern);
  * the caller initialises result to {0, 0xffffffff}.
  */

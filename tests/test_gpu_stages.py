@@ -528,3 +528,41 @@ def test_empty_batches_launch_nothing_and_return_empty(device):
     w = torch.zeros((256, 1024), dtype=torch.bfloat16, device=device)
     assert dense_bf16(x, w, torch.empty((0, 256), dtype=torch.bfloat16, device=device)).shape == (0, 256)
     torch.cuda.synchronize()
+
+
+def test_swiglu_sigmoid_tail(device):
+    """Gates from -104 to -80 (the true sigmoid below 2^-126 from -87.3
+    down, where the fp32 sigmoid returns 0 or a subnormal below 2^-125).
+    The FP8 requantisation gives the float64 oracle's codes and scales byte
+    for byte there: zeros of the right sign, next to groups whose other
+    gates (20 to 30: sigmoid exactly 1) set normal scales.  The bf16
+    silu_mul equals the oracle's bytes outside the tail and stays below
+    2^-118 |u| inside it (where the oracle's value is a subnormal or a
+    tiny normal)."""
+    from drama3_amd import _lib
+    from drama3_amd._lib import call, ptr
+    from drama3_amd.kernels import silu_mul
+
+    rng = np.random.default_rng(17)
+    rows, width = 64, 256
+    gate = np.linspace(-104.0, -80.0, rows * width).astype(np.float32).reshape(rows, width)
+    up = (rng.standard_normal((rows, width)) * np.exp(rng.uniform(-4, 4, (rows, width)))).astype(np.float32)
+    gate[::2, ::3] = rng.uniform(20.0, 30.0, gate[::2, ::3].shape).astype(np.float32)
+    projected = np.concatenate([f32_to_bf16(gate), f32_to_bf16(up)], axis=1)
+    x = torch.from_numpy(projected.view(np.int16)).view(torch.bfloat16).to(device)
+
+    act = torch.empty((rows, width), dtype=torch.uint8, device=device)
+    scales = torch.empty((rows, width // 128), dtype=torch.float32, device=device)
+    call("d3_silu_mul_quant", ptr(x), rows, width, None, None, None, 0, ptr(act), ptr(scales),
+         _lib.stream(device))
+    got_bf16 = np_bf16(silu_mul(x))
+    torch.cuda.synchronize()
+    want_q, want_s = om.silu_mul_quant(projected)
+    assert np.array_equal(np_u8(act), want_q)
+    assert np.array_equal(np_f32(scales), want_s)
+
+    g, u = bf16_to_f32(projected[:, :width]), bf16_to_f32(projected[:, width:])
+    want = om.silu_mul(projected)
+    tail = g < -87.3
+    assert np.array_equal(got_bf16[~tail], want[~tail])
+    assert np.all(np.abs(bf16_to_f32(got_bf16[tail])) <= 2.0**-118 * np.abs(u[tail]))
