@@ -34,22 +34,27 @@ __global__ __launch_bounds__(kSortThreads) void sort_routes_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Wide sort (three launches), the same results as sort_routes_block:
+// Wide sort (two launches), the same results as sort_routes_block:
 //   1. wide_rank_kernel: one workgroup per chunk of kWideChunk pairs ranks
 //      every pair among the chunk's pairs of its expert, in pair order
 //      (per-wave ballot matching on the expert-id bits, per-wave counts in
 //      LDS, a running per-expert base across sub-chunks), and writes the
 //      chunk's expert histogram;
-//   2. wide_scan_kernel: one workgroup turns the chunk histograms into
-//      per-chunk expert offsets (exclusive scan over chunks, 1024 / E
-//      threads per expert), then the padded expert scan, work items, expert
-//      ids and sentinel padding;
-//   3. wide_scatter_kernel: sorted_ids[starts[e] + chunk offset + rank] = p.
+//   2. wide_place_kernel: one workgroup per chunk again, a thread per pair
+//      and per expert.  Every workgroup reads all chunk histograms (thread e
+//      sums its expert's column, and the part of it above its own chunk), so
+//      each holds the padded expert scan and its chunk's offsets itself:
+//      sorted_ids[start[e] + chunk offset + rank] = p.  The last workgroup
+//      also writes the sentinel padding, expert ids, work items and totals.
+//      (A single workgroup scanning the histograms between two launches, as
+//      before, took 8 us of a 13 us pair at config 4.)
 // Scratch: chunk histograms [chunks][E] and ranks [pairs] (int32).
 // ---------------------------------------------------------------------------
 constexpr int kWideThreads = 256;
 constexpr int kWideChunk = 512;
-constexpr int kScanRegs = 16;  // chunk counts a scan thread holds in registers
+constexpr int kPlaceThreads = kWideChunk;  // one pair and at most one expert per thread
+static_assert(kPlaceThreads >= kMaxSortExperts, "a placement thread per expert");
+constexpr int kPlaceBatch = 64;  // chunk counts a placement thread holds in registers
 
 template <bool kI64>
 __global__ __launch_bounds__(kWideThreads) void wide_rank_kernel(
@@ -111,129 +116,62 @@ __global__ __launch_bounds__(kWideThreads) void wide_rank_kernel(
     chunk_counts[static_cast<size_t>(blockIdx.x) * num_experts + e] = running[e];
 }
 
-__global__ __launch_bounds__(kSortThreads) void wide_scan_kernel(
-    int rows, const int32_t* __restrict__ row_count, int top_k, int num_experts, int tile,
-    int item_rows, int chunks, int32_t* __restrict__ chunk_counts, SortOutputs out) {
-  __shared__ int wave_totals[kSortThreads / kWave];
-  __shared__ int partial[kSortThreads];               // [E][share] chunk-range sums
-  __shared__ int expert_info[3 * kMaxSortExperts];    // count, start, first item per expert
+template <bool kI64>
+__global__ __launch_bounds__(kPlaceThreads) void wide_place_kernel(
+    const void* __restrict__ ids, int rows, const int32_t* __restrict__ row_count, int top_k,
+    int num_experts, int tile, int item_rows, int chunks, const int32_t* __restrict__ chunk_counts,
+    const int32_t* __restrict__ ranks, SortOutputs out) {
+  __shared__ int wave_totals[kPlaceThreads / kWave];
+  __shared__ int counts[kMaxSortExperts];
+  __shared__ int starts[kMaxSortExperts];
+  __shared__ int first_item[kMaxSortExperts];
+  __shared__ int base[kMaxSortExperts];  // start + this chunk's offset, per expert
   const int pairs = live_rows(row_count, rows) * top_k;
   const int tid = threadIdx.x;
-  // Expert e is handled by `share` threads (e, j), thread j owning the
-  // contiguous chunk range [c0, c1); E <= 512 gives share >= 2.
-  const int share = kSortThreads / num_experts;
-  const int e = tid / share;
-  const int j = tid - e * share;
-  const bool owner = e < num_experts;
-  const int per = (chunks + share - 1) / share;
-  const int c0 = j * per;
-  const int c1 = min(chunks, c0 + per);
+  const int mine = blockIdx.x;
+  // This thread's pair: its expert and rank, issued first (they do not
+  // depend on the histograms).
+  const int p = mine * kWideChunk + tid;
+  const int e_p = p < pairs ? load_route_id<kI64>(ids, p) : -1;
+  const int rank = p < pairs ? ranks[p] : -1;
+  // Expert e = tid: its column of the chunk histograms, in batches read
+  // branch-free (cells past the last chunk or expert read zero).
   const uint32_t cells = static_cast<uint32_t>(chunks) * num_experts;
   const BufferView count_view(chunk_counts, cells * 4);
-  auto cell = [&](int c) { return owner && c < c1 ? static_cast<uint32_t>(c * num_experts + e) * 4 : kNoRow; };
-  // Per expert: exclusive scan of its chunk counts over the chunks (written
-  // back in place as the chunk offsets) and its count.  A thread's range is
-  // read in batches of kScanRegs cells, every load of a batch issued before
-  // the first use (branch-free: cells outside the range read zero through
-  // the buffer bounds); ranges of at most kScanRegs chunks (up to 64k pairs
-  // at E = 128, 32k at E = 256) stay in registers between the sum and the
-  // write-back, longer ones are read twice.
-  int v[kScanRegs];
-  int sum = 0;
-  for (int b = c0; b < c1; b += kScanRegs) {
+  int total_e = 0, below = 0;
+  for (int b = 0; b < chunks; b += kPlaceBatch) {
+    int v[kPlaceBatch];
 #pragma unroll
-    for (int q = 0; q < kScanRegs; ++q) v[q] = static_cast<int>(count_view.load4(cell(b + q)));
+    for (int q = 0; q < kPlaceBatch; ++q) {
+      const int c = b + q;
+      v[q] = static_cast<int>(count_view.load4(
+          c < chunks && tid < num_experts ? static_cast<uint32_t>(c * num_experts + tid) * 4 : kNoRow));
+    }
 #pragma unroll
-    for (int q = 0; q < kScanRegs; ++q) sum += v[q];
+    for (int q = 0; q < kPlaceBatch; ++q) {
+      total_e += v[q];
+      below += b + q < mine ? v[q] : 0;
+    }
   }
-  partial[tid] = sum;
+  if (tid < num_experts) counts[tid] = total_e;
   __syncthreads();
-  int base = 0;
-  for (int q = 0; q < j; ++q) base += partial[e * share + q];
-  if (owner) {
-    if (per <= kScanRegs) {
-#pragma unroll
-      for (int q = 0; q < kScanRegs; ++q) {
-        if (c0 + q < c1) chunk_counts[static_cast<size_t>(c0 + q) * num_experts + e] = base;
-        base += v[q];
-      }
+  int total = 0, total_items = 0;
+  expert_offsets<kPlaceThreads>(counts, num_experts, tile, item_rows, starts, first_item, wave_totals,
+                                &total, &total_items);
+  if (tid < num_experts) base[tid] = starts[tid] + below;
+  __syncthreads();
+  if (p < pairs) {
+    if (e_p < 0 || e_p >= num_experts || rank < 0) {
+      if (out.inverse != nullptr) out.inverse[p] = -1;
     } else {
-      for (int b = c0; b < c1; b += kScanRegs) {
-#pragma unroll
-        for (int q = 0; q < kScanRegs; ++q) v[q] = static_cast<int>(count_view.load4(cell(b + q)));
-#pragma unroll
-        for (int q = 0; q < kScanRegs; ++q) {
-          if (b + q < c1) chunk_counts[static_cast<size_t>(b + q) * num_experts + e] = base;
-          base += v[q];
-        }
-      }
+      const int position = base[e_p] + rank;
+      out.sorted_ids[position] = p;
+      if (out.inverse != nullptr) out.inverse[p] = position;
     }
   }
-  int count = 0;
-  if (tid < num_experts)
-    for (int q = 0; q < share; ++q) count += partial[tid * share + q];
-  // Padded expert scan and work items (thread e < E holds expert e).
-  const int padded = (count + tile - 1) / tile * tile;
-  int total = 0;
-  const int start = block_inclusive_scan<kSortThreads>(padded, wave_totals, &total) - padded;
-  const int my_items = (count + item_rows - 1) / item_rows;
-  int total_items = 0;
-  const int item_base =
-      block_inclusive_scan<kSortThreads>(my_items, wave_totals, &total_items) - my_items;
-  if (tid < num_experts) {
-    expert_info[3 * tid] = count;
-    expert_info[3 * tid + 1] = start;
-    expert_info[3 * tid + 2] = item_base;
-    if (out.counts != nullptr) out.counts[tid] = count;
-    out.starts[tid] = start;
-  }
-  __syncthreads();
-  // Each expert's sentinel padding, expert ids and work items, spread over
-  // its `share` threads.
-  if (owner) {
-    const int e_count = expert_info[3 * e], e_start = expert_info[3 * e + 1];
-    const int e_padded = (e_count + tile - 1) / tile * tile;
-    for (int i = e_count + j; i < e_padded; i += share) out.sorted_ids[e_start + i] = pairs;
-    if (out.expert_ids != nullptr)
-      for (int t = j; t < e_padded / tile; t += share) out.expert_ids[e_start / tile + t] = e;
-    if (out.items != nullptr) {
-      const int e_items = (e_count + item_rows - 1) / item_rows, e_item_base = expert_info[3 * e + 2];
-      for (int it = j; it < e_items; it += share) {
-        const int routes = min(item_rows, e_count - it * item_rows);
-        out.items[e_item_base + it] = make_int4(e, e_start + it * item_rows, routes, 0);
-      }
-    }
-  }
-  for (int i = total + tid; i < out.max_rows; i += kSortThreads) out.sorted_ids[i] = pairs;
-  if (out.expert_ids != nullptr)
-    for (int i = total / tile + tid; i < out.max_rows / tile; i += kSortThreads) out.expert_ids[i] = -1;
-  if (out.items != nullptr)
-    for (int i = total_items + tid; i < out.max_items; i += kSortThreads)
-      out.items[i] = make_int4(-1, 0, 0, 0);
-  if (tid == 0) {
-    if (out.total != nullptr) *out.total = total;
-    if (out.num_items != nullptr) *out.num_items = total_items;
-    if (out.pairs_out != nullptr) *out.pairs_out = pairs;
-  }
-}
-
-template <bool kI64>
-__global__ __launch_bounds__(kWideThreads) void wide_scatter_kernel(
-    const void* __restrict__ ids, int rows, const int32_t* __restrict__ row_count, int top_k,
-    int num_experts, const int32_t* __restrict__ chunk_counts, const int32_t* __restrict__ ranks,
-    const int32_t* __restrict__ starts, int32_t* __restrict__ sorted_ids, int32_t* __restrict__ inverse) {
-  const int pairs = live_rows(row_count, rows) * top_k;
-  const int p = blockIdx.x * kWideThreads + threadIdx.x;
-  if (p >= pairs) return;
-  const int e = load_route_id<kI64>(ids, p);
-  const int rank = ranks[p];
-  if (e < 0 || e >= num_experts || rank < 0) {
-    if (inverse != nullptr) inverse[p] = -1;
-    return;
-  }
-  const int position = starts[e] + chunk_counts[static_cast<size_t>(p / kWideChunk) * num_experts + e] + rank;
-  sorted_ids[position] = p;
-  if (inverse != nullptr) inverse[p] = position;
+  if (mine == static_cast<int>(gridDim.x) - 1)
+    write_sort_tail<kPlaceThreads, false>(counts, starts, first_item, num_experts, tile, item_rows, total,
+                                          total_items, pairs, out);
 }
 
 }  // namespace
@@ -355,7 +293,6 @@ extern "C" int d3_sort_routes_wide(const void* ids, int32_t ids_dtype, int32_t r
                         reinterpret_cast<int4*>(items), max_items, num_items, pairs_out};
   hipStream_t s = as_stream(stream);
   const size_t rank_shared = sizeof(int) * static_cast<size_t>(num_experts) * (1 + kWideThreads / kWave);
-  const int scatter_blocks = static_cast<int>((pairs + kWideThreads - 1) / kWideThreads);
   if (chunks > 0) {
     if (ids_dtype == D3_DTYPE_I64)
       hipLaunchKernelGGL(wide_rank_kernel<true>, dim3(chunks), dim3(kWideThreads), rank_shared, s, ids,
@@ -364,17 +301,13 @@ extern "C" int d3_sort_routes_wide(const void* ids, int32_t ids_dtype, int32_t r
       hipLaunchKernelGGL(wide_rank_kernel<false>, dim3(chunks), dim3(kWideThreads), rank_shared, s, ids,
                          rows, row_count, top_k, num_experts, chunk_counts, ranks);
   }
-  hipLaunchKernelGGL(wide_scan_kernel, dim3(1), dim3(kSortThreads), 0, s, rows, row_count,
-                     top_k, num_experts, tile, item_rows, chunks, chunk_counts, out);
-  if (scatter_blocks > 0) {
-    if (ids_dtype == D3_DTYPE_I64)
-      hipLaunchKernelGGL(wide_scatter_kernel<true>, dim3(scatter_blocks), dim3(kWideThreads), 0, s, ids,
-                         rows, row_count, top_k, num_experts, chunk_counts, ranks, starts, sorted_ids,
-                         inverse);
-    else
-      hipLaunchKernelGGL(wide_scatter_kernel<false>, dim3(scatter_blocks), dim3(kWideThreads), 0, s, ids,
-                         rows, row_count, top_k, num_experts, chunk_counts, ranks, starts, sorted_ids,
-                         inverse);
-  }
+  // At least one placement workgroup, for the outputs of an empty batch.
+  const dim3 place_grid(chunks > 0 ? chunks : 1);
+  if (ids_dtype == D3_DTYPE_I64)
+    hipLaunchKernelGGL(wide_place_kernel<true>, place_grid, dim3(kPlaceThreads), 0, s, ids, rows, row_count,
+                       top_k, num_experts, tile, item_rows, chunks, chunk_counts, ranks, out);
+  else
+    hipLaunchKernelGGL(wide_place_kernel<false>, place_grid, dim3(kPlaceThreads), 0, s, ids, rows, row_count,
+                       top_k, num_experts, tile, item_rows, chunks, chunk_counts, ranks, out);
   D3_LAUNCHED("sort_routes_wide");
 }
