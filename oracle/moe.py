@@ -84,7 +84,10 @@ def route(logits: np.ndarray, top_k: int = 8, out_dtype: str = "bf16"):
     keys = route_keys(logits)
     ids = np.argsort(-keys.astype(np.int64), axis=-1, kind="stable")[:, :top_k]
     row_max = logits.max(axis=-1, keepdims=True)
-    shifted = (logits - row_max).astype(np.float32)  # fp32 subtraction, as the kernel
+    # fp32 subtraction, as the kernel; a row holding +inf gives inf - inf =
+    # NaN there too (its weights are NaN; its ids still follow the keys)
+    with np.errstate(invalid="ignore"):
+        shifted = (logits - row_max).astype(np.float32)
     exps = np.exp(shifted.astype(np.float64))
     denominator = exps.sum(axis=-1, keepdims=True)
     selected = np.take_along_axis(exps, ids, axis=-1) / denominator
