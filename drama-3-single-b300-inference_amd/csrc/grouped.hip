@@ -56,6 +56,7 @@ constexpr int kGgWaveTiles = 4;                    // 16-row weight tiles per wa
 constexpr int kGgRows = kGgWaves * kGgWaveTiles * 16;  // 256 weight rows per workgroup
 constexpr int kGgStride = kGroup + 16;             // LDS bytes per staged route row
 constexpr int kGgXcds = 8;
+constexpr int kStreamOutRoutes = 16384;  // FC2 launches up to this many item routes stream their rows
 // Routes found by the workgroups themselves (by-pair launches): at most this
 // many (row, rank) pairs, read in chunks of one id per thread.
 constexpr int kGgMaxPairChunks = 32;
@@ -83,7 +84,8 @@ struct SharedItems {
 // routes), its pairs at list_ids[128 i ..] in ascending order - and FC1
 // writes act rows at those positions, so the sorted FC2 launch reads them
 // as it reads a route sort's.
-template <int KB, int MODE, bool kPacked, bool kByPair>
+// kStreamOut (FC2): the fp32 rows go out with non-temporal stores.
+template <int KB, int MODE, bool kPacked, bool kByPair, bool kStreamOut = false>
 __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2))) void grouped_gemm_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int n_rows, int out_cols,
     const uint8_t* __restrict__ act, uint32_t act_bytes, const float* __restrict__ act_scales,
@@ -419,7 +421,10 @@ __global__ __launch_bounds__(kGgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
       for (int t = 0; t < kGgWaveTiles; ++t) {
         float* dst = out_f32 + static_cast<size_t>(pair) * n_rows + tile_row(t) + 4 * group;
-        *reinterpret_cast<float4*>(dst) = make_float4(acc[t][rt][0], acc[t][rt][1], acc[t][rt][2], acc[t][rt][3]);
+        if constexpr (kStreamOut)
+          __builtin_nontemporal_store(acc[t][rt], reinterpret_cast<floatx4*>(dst));
+        else
+          *reinterpret_cast<float4*>(dst) = make_float4(acc[t][rt][0], acc[t][rt][1], acc[t][rt][2], acc[t][rt][3]);
       }
     }
   } else {
@@ -513,6 +518,18 @@ void launch_grouped(const GroupedLaunch& g, hipStream_t s) {
         hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true, true>), D3_GG_ARGS);
       else
         hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, false, true>), D3_GG_ARGS);
+      return;
+    }
+  }
+  if constexpr (MODE == 1) {
+    // Small batches (the mixed step's few thousand routes) write FC2's fp32
+    // rows non-temporally: measured 1.4 us less per mixed step, while the
+    // prefill batch (29k routes, 240 MB of rows) is 10 us slower that way.
+    if ((static_cast<int64_t>(g.max_items) + shared_items) * kGgRoutes <= kStreamOutRoutes) {
+      if (g.layout == D3_LAYOUT_FRAGMENT)
+        hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, true, false, true>), D3_GG_ARGS);
+      else
+        hipLaunchKernelGGL((grouped_gemm_kernel<KB, MODE, false, false, true>), D3_GG_ARGS);
       return;
     }
   }
