@@ -119,8 +119,8 @@ __global__ __launch_bounds__(kWideThreads) void wide_rank_kernel(
 template <bool kI64>
 __global__ __launch_bounds__(kPlaceThreads) void wide_place_kernel(
     const void* __restrict__ ids, int rows, const int32_t* __restrict__ row_count, int top_k,
-    int num_experts, int tile, int item_rows, int chunks, const int32_t* __restrict__ chunk_counts,
-    const int32_t* __restrict__ ranks, SortOutputs out) {
+    int num_experts, int tile, int item_rows, int align_items, int chunks,
+    const int32_t* __restrict__ chunk_counts, const int32_t* __restrict__ ranks, SortOutputs out) {
   __shared__ int wave_totals[kPlaceThreads / kWave];
   __shared__ int counts[kMaxSortExperts];
   __shared__ int starts[kMaxSortExperts];
@@ -158,6 +158,19 @@ __global__ __launch_bounds__(kPlaceThreads) void wide_place_kernel(
   int total = 0, total_items = 0;
   expert_offsets<kPlaceThreads>(counts, num_experts, tile, item_rows, starts, first_item, wave_totals,
                                 &total, &total_items);
+  const int count_e = tid < num_experts ? counts[tid] : 0;
+  const int items_e = (count_e + item_rows - 1) / item_rows;
+  if (align_items) {
+    // Every expert's items start on an even item (an odd count is followed
+    // by one empty item), so the grouped GEMMs' XCD runs of two consecutive
+    // items hold one expert's items and share its weights in that L2.
+    const int padded_items = (items_e + 1) & ~1;
+    const int first_aligned =
+        block_inclusive_scan<kPlaceThreads>(padded_items, wave_totals, &total_items) - padded_items;
+    if (tid < num_experts) first_item[tid] = first_aligned;
+    if (mine == static_cast<int>(gridDim.x) - 1 && tid < num_experts && padded_items > items_e)
+      out.items[first_aligned + items_e] = make_int4(tid, starts[tid], 0, 0);
+  }
   if (tid < num_experts) base[tid] = starts[tid] + below;
   __syncthreads();
   if (p < pairs) {
@@ -190,6 +203,12 @@ extern "C" int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item
   if (pairs < 0 || num_experts <= 0 || item_rows <= 0) return -1;
   const int64_t used = pairs < num_experts ? pairs : num_experts;
   return static_cast<int32_t>((static_cast<int64_t>(pairs) + used * (item_rows - 1)) / item_rows);
+}
+
+extern "C" int32_t d3_max_items_aligned(int32_t pairs, int32_t num_experts, int32_t item_rows) {
+  const int32_t plain = d3_max_items(pairs, num_experts, item_rows);
+  if (plain < 0) return -1;
+  return plain + (pairs < num_experts ? pairs : num_experts);  // one empty item per used expert at most
 }
 
 extern "C" int d3_sort_routes(const void* ids, int32_t ids_dtype, int32_t rows,
@@ -286,6 +305,8 @@ extern "C" int d3_sort_routes_wide(const void* ids, int32_t ids_dtype, int32_t r
   } else {
     item_rows = tile;
   }
+  const int align_items =
+      items != nullptr && max_items >= d3_max_items_aligned(static_cast<int32_t>(pairs), num_experts, item_rows);
   const int chunks = static_cast<int>((pairs + kWideChunk - 1) / kWideChunk);
   int32_t* chunk_counts = scratch;
   int32_t* ranks = scratch + static_cast<int64_t>(chunks) * num_experts;
@@ -305,9 +326,11 @@ extern "C" int d3_sort_routes_wide(const void* ids, int32_t ids_dtype, int32_t r
   const dim3 place_grid(chunks > 0 ? chunks : 1);
   if (ids_dtype == D3_DTYPE_I64)
     hipLaunchKernelGGL(wide_place_kernel<true>, place_grid, dim3(kPlaceThreads), 0, s, ids, rows, row_count,
-                       top_k, num_experts, tile, item_rows, chunks, chunk_counts, ranks, out);
+                       top_k, num_experts, tile, item_rows, align_items, chunks, chunk_counts, ranks,
+                       out);
   else
     hipLaunchKernelGGL(wide_place_kernel<false>, place_grid, dim3(kPlaceThreads), 0, s, ids, rows, row_count,
-                       top_k, num_experts, tile, item_rows, chunks, chunk_counts, ranks, out);
+                       top_k, num_experts, tile, item_rows, align_items, chunks, chunk_counts, ranks,
+                       out);
   D3_LAUNCHED("sort_routes_wide");
 }

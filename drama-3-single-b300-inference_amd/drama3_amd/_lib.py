@@ -58,6 +58,7 @@ SIGNATURES = {
     "d3_gather_rows": (_i32, [_p, _i64, _i64, _p, _p, _i32, _p, _p]),
     "d3_max_sorted_rows": (_i32, [_i32, _i32, _i32]),
     "d3_max_items": (_i32, [_i32, _i32, _i32]),
+    "d3_max_items_aligned": (_i32, [_i32, _i32, _i32]),
     "d3_expert_gemm": (
         _i32, [_i32, _p, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32,
                _p, _p, _p]),

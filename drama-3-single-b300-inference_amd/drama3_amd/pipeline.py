@@ -144,7 +144,15 @@ class MoEWorkspace:
             raise ValueError("item_rows must be a multiple of the sort tile")
         pairs = shape.pairs
         self.max_rows = lib.d3_max_sorted_rows(pairs, shape.num_experts, tile)
-        self.max_items = lib.d3_max_items(pairs, shape.num_experts, self.item_rows)
+        self.wide_sort = pairs > WIDE_SORT_PAIRS
+        # The wide sort pads each expert's items to an even count when the
+        # items array holds the padding: the tiled grouped GEMMs, which give
+        # each XCD runs of two consecutive items, then never split a pair of
+        # one expert's items over two XCDs' L2s.  Other consumers keep the
+        # unpadded list.
+        self.aligned_items = bool(self.wide_sort and grouped and not sortless)
+        self.max_items = (lib.d3_max_items_aligned if self.aligned_items else lib.d3_max_items)(
+            pairs, shape.num_experts, self.item_rows)
         dev = self.device
         i32 = dict(dtype=torch.int32, device=dev)
         h, e, i, t = shape.hidden, shape.num_experts, shape.intermediate, shape.rows
@@ -211,7 +219,6 @@ class MoEWorkspace:
                                               device=dev)
         self.rows_dev = torch.full((1,), t, **i32)  # the live row count when none is given
         # Scratch of the wide route sort (prefill-sized batches).
-        self.wide_sort = pairs > WIDE_SORT_PAIRS
         self.sort_scratch = torch.empty(
             lib.d3_sort_wide_scratch_ints(t, shape.top_k, e) if self.wide_sort else 1, **i32)
 

@@ -210,10 +210,15 @@ int d3_moe_front(const uint8_t *occupancy, int32_t num_slots, int32_t *active_sl
 /*
  * A5-A7  The same histogram / offsets / stable sort as d3_sort_routes, for
  * prefill-sized batches: the ranking is spread over one workgroup per 512
- * pairs (three launches) instead of one workgroup walking every pair.
+ * pairs (two launches) instead of one workgroup walking every pair.
  * Same arguments and outputs as d3_sort_routes (starts is required), plus a
  * caller-owned int32 scratch of d3_sort_wide_scratch_ints(rows, top_k, E)
- * ints.  Replaces expert_counts_kernel / expert_offsets_kernel /
+ * ints.  With max_items >= d3_max_items_aligned(pairs, E, item_rows) the
+ * items are aligned: every expert's items start at an even item index, and
+ * an expert with an odd number of items is followed by one empty item
+ * {expert, start, 0, 0} (counted in *num_items), so two consecutive items
+ * never mix experts' weights; the grouped GEMMs skip empty items (their XCD
+ * runs of two consecutive items then share one expert's weights in L2).  Replaces expert_counts_kernel / expert_offsets_kernel /
  * expert_scatter_kernel (src/drama3/kernels.py:658-699) as native_moe runs
  * them for prefill (kernels.py:710-731).
  */
@@ -258,6 +263,9 @@ int d3_gather_rows(const void *src, int64_t row_bytes, int64_t src_rows, const i
 
 int32_t d3_max_sorted_rows(int32_t pairs, int32_t num_experts, int32_t tile);
 int32_t d3_max_items(int32_t pairs, int32_t num_experts, int32_t item_rows);
+/* Items capacity for d3_sort_routes_wide's aligned items: d3_max_items plus
+ * one empty item per used expert (no counterpart in the reference). */
+int32_t d3_max_items_aligned(int32_t pairs, int32_t num_experts, int32_t item_rows);
 
 /*
  * A8-A11  Grouped FP8 expert GEMM over sorted routes (FC1 or FC2).

@@ -82,7 +82,7 @@ def test_capacity_helpers(lib):
     for pairs, experts, tile in ((32, 16, 16), (384, 128, 16), (33280, 128, 64), (0, 8, 16)):
         assert lib.d3_max_sorted_rows(pairs, experts, tile) == om.max_sorted_rows(pairs, experts, tile)
     assert lib.d3_max_items(384, 128, 64) == (384 + 128 * 63) // 64
-    assert lib.d3_abi_version() == 10
+    assert lib.d3_abi_version() == 11
     # wide sort scratch: chunk histograms [ceil(pairs / 512)][E] + ranks [pairs]
     assert lib.d3_sort_wide_scratch_ints(3668, 8, 128) == (-(-3668 * 8 // 512)) * 128 + 3668 * 8
     assert lib.d3_sort_wide_scratch_ints(-1, 8, 128) == -1

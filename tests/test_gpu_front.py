@@ -76,7 +76,7 @@ def test_fused_front_matches_standalone_kernels(device, hidden, experts, p):
 
 @pytest.mark.parametrize("rows,experts,live", [
     (560, 16, None),    # 4480 pairs: fused row-mask sort
-    (1100, 16, None),   # 8800 pairs: the standalone sort kernel
+    (1100, 16, None),   # 8800 pairs: the wide sort (aligned items)
     (1024, 128, None),  # 8192 pairs, 128 x 16 mask words: the row-mask sort at its limits
     (600, 256, None),   # 256 x 10 mask words: the fused ballot sort
     (1000, 128, 301),   # device row count below capacity
@@ -87,8 +87,8 @@ def test_fused_front_row_mode_with_index(device, rows, experts, live, fused):
     """Row mode (mixed batches): row_index gathers rows; the sort is fused
     (opt-in) while pairs <= 8192 (row masks while E x ceil(rows / 64) <= 2048,
     else the chunked ballot sort) and otherwise the sort kernel's (row masks
-    while they fit, else the ballot sort); every variant gives the oracle's
-    sort, inverse map and work items."""
+    while they fit, else the ballot sort; the wide sort above 8192 pairs);
+    every variant gives the oracle's sort, inverse map and work items."""
     from drama3_amd.pipeline import MoEWorkspace, Shape
 
     x, logits, xd, ld = _inputs(device, rows + 7, 1024, experts, rows + experts)
@@ -112,9 +112,14 @@ def test_fused_front_row_mode_with_index(device, rows, experts, live, fused):
         assert np.all(sorted_ids[o.total:] == n * 8)
         assert np.array_equal(ws.expert_ids.cpu().numpy()[:o.total // ws.tile], o.expert_ids)
         assert np.array_equal(ws.inverse.cpu().numpy()[:n * 8], o.inverse)
-        # work items: each expert's routes in chunks of item_rows, in expert order
-        want = [(e, int(o.starts[e]) + j, min(ws.item_rows, int(o.counts[e]) - j), 0)
-                for e in range(experts) for j in range(0, int(o.counts[e]), ws.item_rows)]
+        # work items: each expert's routes in chunks of item_rows, in expert
+        # order; a workspace for the grouped GEMMs over the wide sort pads
+        # each expert's run to an even count with one empty item
+        want = []
+        for e in range(experts):
+            run = [(e, int(o.starts[e]) + j, min(ws.item_rows, int(o.counts[e]) - j), 0)
+                   for j in range(0, int(o.counts[e]), ws.item_rows)]
+            want += run + ([(e, int(o.starts[e]), 0, 0)] if ws.aligned_items and len(run) % 2 else [])
         num_items = int(ws.num_items.item())
         assert num_items == len(want)
         assert np.array_equal(ws.items.cpu().numpy().reshape(-1, 4)[:num_items], np.array(want))

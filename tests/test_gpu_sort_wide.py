@@ -2,7 +2,9 @@
 against the CPU oracle, bit for bit: histogram, padded offsets, stable
 sorted pair list with sentinel padding, expert ids, inverse map and work
 items, at prefill sizes, under skew, for int64 ids, with a device row count
-below the capacity, and at the 512-expert limit.  The reference-named
+below the capacity, and at the 512-expert limit.  With an items array of
+d3_max_items_aligned's capacity each expert's items are padded to an even
+count by one empty item (rows 0).  The reference-named
 sort_routes() takes this path above 8192 pairs."""
 
 import numpy as np
@@ -14,7 +16,8 @@ from oracle import moe as om
 pytestmark = pytest.mark.gpu
 
 
-def run_wide(device, ids_np, experts, tile, item_rows, live_rows=None, dtype=torch.int32):
+def run_wide(device, ids_np, experts, tile, item_rows, live_rows=None, dtype=torch.int32,
+             aligned=False):
     from drama3_amd import _lib
     from drama3_amd._lib import call, ptr
     from drama3_amd.pipeline import dtype_code
@@ -24,7 +27,7 @@ def run_wide(device, ids_np, experts, tile, item_rows, live_rows=None, dtype=tor
     pairs = rows * top_k
     i32 = dict(dtype=torch.int32, device=device)
     max_rows = lib.d3_max_sorted_rows(pairs, experts, tile)
-    max_items = lib.d3_max_items(pairs, experts, item_rows)
+    max_items = (lib.d3_max_items_aligned if aligned else lib.d3_max_items)(pairs, experts, item_rows)
     out = dict(counts=torch.empty(experts, **i32), starts=torch.empty(experts, **i32),
                total=torch.empty(1, **i32), sorted_ids=torch.empty(max_rows, **i32),
                expert_ids=torch.empty(max_rows // tile, **i32), inverse=torch.empty(pairs, **i32),
@@ -42,7 +45,7 @@ def run_wide(device, ids_np, experts, tile, item_rows, live_rows=None, dtype=tor
     return {k: v.cpu().numpy() for k, v in out.items()}
 
 
-def check(got, ids_np, experts, tile, item_rows):
+def check(got, ids_np, experts, tile, item_rows, aligned=False):
     o = om.sort_routes(ids_np, experts, tile)
     pairs = ids_np.size
     assert np.array_equal(got["counts"], o.counts)
@@ -53,8 +56,13 @@ def check(got, ids_np, experts, tile, item_rows):
     assert np.array_equal(got["expert_ids"][:o.total // tile], o.expert_ids)
     assert np.all(got["expert_ids"][o.total // tile:] == -1)
     assert np.array_equal(got["inverse"][:pairs], o.inverse)
-    items = [(e, int(o.starts[e]) + j * item_rows, min(item_rows, int(o.counts[e]) - j * item_rows), 0)
-             for e in range(experts) for j in range(-(-int(o.counts[e]) // item_rows))]
+    items = []
+    for e in range(experts):
+        n_e = -(-int(o.counts[e]) // item_rows)
+        items += [(e, int(o.starts[e]) + j * item_rows,
+                   min(item_rows, int(o.counts[e]) - j * item_rows), 0) for j in range(n_e)]
+        if aligned and n_e % 2:
+            items.append((e, int(o.starts[e]), 0, 0))
     n = int(got["num_items"][0])
     assert n == len(items)
     assert np.array_equal(got["items"][:n], np.array(items, np.int32).reshape(-1, 4))
@@ -80,6 +88,19 @@ def test_wide_sort_skewed_and_live_rows(device):
     ids[:, [0, 3]] = ids[:, [3, 0]]  # the hot expert at rank 3
     got = run_wide(device, ids, experts, 16, 128, live_rows=live)
     check({k: v for k, v in got.items()}, ids[:live], experts, 16, 128)
+
+
+@pytest.mark.parametrize("rows,experts,item_rows", [(4096, 256, 128), (3001, 64, 256), (1100, 512, 16)])
+def test_wide_sort_aligned_items(device, rows, experts, item_rows):
+    """Aligned capacity: every expert's first item sits at an even index
+    and the list is the plain one with one empty item after each odd run."""
+    rng = np.random.default_rng(rows * 3 + experts)
+    ids = np.stack([rng.permutation(experts)[:8] for _ in range(rows)]).astype(np.int64)
+    got = run_wide(device, ids, experts, 16, item_rows, aligned=True)
+    check(got, ids, experts, 16, item_rows, aligned=True)
+    items = got["items"][:int(got["num_items"][0])]
+    first = np.flatnonzero(np.r_[True, items[1:, 0] != items[:-1, 0]])
+    assert np.all(first % 2 == 0)
 
 
 def test_reference_sort_routes_takes_wide_path(device):
