@@ -709,7 +709,7 @@ def main():
     if frontless:  # the step's own expert kernels: FC1 from the slots, sortless FC2
         fc1_graph = kernel_graph(lambda c: ws.decode_route_fc1(c, occ, x_slots, logits_slots,
                                                                ds.active, ds.count))
-        fc2_graph = kernel_graph(lambda c: ws.decode_fc2(c, ds.count))
+        fc2_graph = kernel_graph(lambda c: ws.decode_fc2(c, ds.count, row_slots=ds.active))
     elif ws.sortless:  # sortless decode GEMMs after the front
         fc1_graph = kernel_graph(lambda c: ws.decode_fc1(c, ds.count))
         fc2_graph = kernel_graph(lambda c: ws.decode_fc2(c, ds.count))

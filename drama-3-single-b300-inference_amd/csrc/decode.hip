@@ -70,6 +70,9 @@ struct DecodeArgs {
   int32_t* active_out;
   uint16_t* out_bf16;  // MODE 0 / 1: gate|up [pairs, n_rows]
   float* out_f32;      // MODE 2: down [pairs, n_rows]
+  // MODE 2: the slot of every row (FC1's slot list); down rows are then
+  // indexed by slot pair, row_slots[row] * top_k + rank (nullptr: by pair)
+  const int32_t* row_slots;
   // Route slices per (expert, weight-tile group), set at launch: slice j of
   // an expert takes its route tiles j, j + slices, ... (1: every tile).
   int slices;
@@ -384,6 +387,7 @@ __device__ __forceinline__ void decode_gemm_body(const DecodeArgs& a, DecodeLds<
   int4 b_stage[MODE == 0 ? kChunks : 1];
   float b_stage_scale = 0.0f;
   int stage_pair = -1;
+  uint32_t stage_slot = 0;  // MODE 2 with row_slots: the slot of the route's row
   // MODE 1: live (route column, 128-group) units packed densely as in MODE
   // 2; a unit's 16 threads hold 8 bf16 each (the front's quantisation
   // layout), so only live units are quantised.
@@ -471,6 +475,10 @@ __device__ __forceinline__ void decode_gemm_body(const DecodeArgs& a, DecodeLds<
       b_stage_scale = __uint_as_float(scale_view.load4(
           stage_pair >= 0 && stage_part < KB ? static_cast<uint32_t>(token * KB + stage_part) * 4 : kNoRow));
     } else {
+      // The route's slot first (read only with row_slots: an empty view
+      // otherwise), so that waiting for the gate|up rows covers it.
+      const BufferView slot_view(a.row_slots, a.row_slots != nullptr ? static_cast<uint32_t>(capacity) * 4 : 0u);
+      stage_slot = slot_view.load4(stage_pair >= 0 ? static_cast<uint32_t>(stage_pair / top_k) * 4 : kNoRow);
       const BufferView gu_view(act, static_cast<uint32_t>(capacity * top_k) * 2 * K * 2);
       live_units = min(16, routes - m0) * KB;
 #pragma unroll
@@ -513,7 +521,12 @@ __device__ __forceinline__ void decode_gemm_body(const DecodeArgs& a, DecodeLds<
         *reinterpret_cast<int4*>(b_tile + stage_col * kStride + j * 256 + stage_part * 16) = b_stage[j];
       if (stage_part < KB) b_scales[stage_col * KB + stage_part] = b_stage_scale;
     }
-    if (stage_part == 0) b_target[stage_col] = stage_pair;
+    int target = stage_pair;
+    if constexpr (MODE == 2) {
+      if (a.row_slots != nullptr && stage_pair >= 0)
+        target = static_cast<int>(stage_slot) * top_k + (stage_pair - (stage_pair / top_k) * top_k);
+    }
+    if (stage_part == 0) b_target[stage_col] = target;
   };
 
   // K blocks [kb0, kb1) of one weight tile against the route tile in LDS.
@@ -756,7 +769,8 @@ void launch_decode(int num_experts, hipStream_t s, const DecodeArgs& a) {
 // ---------------------------------------------------------------------------
 // Weighted combine of the step whose FC1 routed the slots itself: one
 // workgroup per (slot, 512-column slice).  The down rows of the slot's
-// routes are loaded first; meanwhile wave 0 recomputes the slot's top-k
+// routes (indexed by slot pair: FC2 wrote them there from the slot list)
+// are loaded first, with the logits, in one memory round trip; meanwhile wave 0 recomputes the slot's top-k
 // weights from its logits with the front's function (route_top_k) and
 // rounds them to the stored dtype, so the sum is the chain combine's
 // (one fused multiply-add per rank, in rank order).  Slice 0 also stores
@@ -787,12 +801,25 @@ __global__ __launch_bounds__(kRoutedCombineThreads) void routed_combine_kernel(R
   const int slice = blockIdx.x % slices;
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) / kWave;
-  // The slot's logits (indexed by slot, so issued before its row is known;
-  // every wave loads them, so no branch makes the first wait come early).
+  // The slot's logits and down rows (both indexed by slot, so issued before
+  // its row is known; every wave loads the logits, so no branch makes the
+  // first wait come early).  A free slot's rows are read and dropped.
   RouteLogits<NPL> logits;
   load_route_logits<NPL, kF32>(static_cast<const char*>(a.logits) +
                                      static_cast<int64_t>(slot) * a.logits_stride * (kF32 ? 4 : 2),
                                  a.num_experts, logits);
+  const int column = slice * kRoutedCombineColumns + static_cast<int>(threadIdx.x) * 4;
+  const bool inside = column < a.hidden;
+  const BufferView down_view(a.down, static_cast<uint32_t>(a.capacity * a.top_k * a.hidden) * 4);
+  float4 y[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int4 v = down_view.load16(
+        inside && r < a.top_k
+            ? static_cast<uint32_t>(((slot * a.top_k + r) * a.hidden + column) * 4)
+            : kNoRow);
+    y[r] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
+  }
   // The slot's row: occupied slots below it (every wave counts them).
   int row = 0;
   bool on = false;
@@ -808,15 +835,6 @@ __global__ __launch_bounds__(kRoutedCombineThreads) void routed_combine_kernel(R
     }
   }
   if (!on) return;  // uniform over the workgroup
-  const int column = slice * kRoutedCombineColumns + static_cast<int>(threadIdx.x) * 4;
-  const bool inside = column < a.hidden;
-  float4 y[8];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    y[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (inside && r < a.top_k)
-      y[r] = *reinterpret_cast<const float4*>(a.down + (static_cast<size_t>(row) * a.top_k + r) * a.hidden + column);
-  }
   if (wave == 0) {
     const RouteChoice choice = route_top_k<NPL>(logits, a.num_experts, a.top_k);
     if (lane < a.top_k) {
@@ -859,9 +877,11 @@ struct GemmLaunch {
 
 int check_expert_gemm(int32_t mode, const uint8_t* w, const float* ws, int32_t num_experts,
                       int32_t n, int32_t k, const int32_t* ids, const int32_t* row_count,
-                      int32_t capacity, int32_t top_k, const void* a, const float* a_scales,
-                      int32_t exact_routes, uint16_t* out_bf16, float* out_f32, GemmLaunch* launch) {
+                      const int32_t* row_slots, int32_t capacity, int32_t top_k, const void* a,
+                      const float* a_scales, int32_t exact_routes, uint16_t* out_bf16,
+                      float* out_f32, GemmLaunch* launch) {
   D3_REQUIRE(mode == 0 || mode == 2, "decode_expert_gemm: mode must be 0 (FC1) or 2 (FC2 + SwiGLU)");
+  D3_REQUIRE(row_slots == nullptr || mode == 2, "decode_expert_gemm: row_slots is for mode 2 (FC2)");
   D3_REQUIRE(w && ws && ids && a && (mode == 2 || a_scales), "decode_expert_gemm: null pointer");
   D3_REQUIRE(mode == 0 ? out_bf16 != nullptr : out_f32 != nullptr, "decode_expert_gemm: null output");
   D3_REQUIRE(num_experts >= 1 && n > 0 && k > 0 && n % kGroup == 0 && k % 256 == 0,
@@ -891,6 +911,7 @@ int check_expert_gemm(int32_t mode, const uint8_t* w, const float* ws, int32_t n
   args.act_scales = a_scales;
   args.out_bf16 = out_bf16;
   args.out_f32 = out_f32;
+  args.row_slots = row_slots;
   *launch = GemmLaunch{mode, kb, num_experts, args};
   return D3_OK;
 }
@@ -983,6 +1004,8 @@ int check_route_combine(const uint8_t* occupancy, int32_t capacity, const void* 
                "decode_route_combine: capacity %d (<= %d), top_k %d (<= 8), E %d (<= 256)",
                capacity, kMaxSlots, top_k, num_experts);
   D3_REQUIRE(aligned(down, 16) && aligned(out, 8), "decode_route_combine: alignment");
+  D3_SUPPORTED(static_cast<int64_t>(capacity) * top_k * hidden * 4 < (int64_t{1} << 31),
+               "decode_route_combine: down rows above 2 GiB");
   *launch = CombineLaunch{logits_dtype == D3_DTYPE_F32,
                           RoutedCombineArgs{occupancy, capacity, logits, logits_stride, num_experts,
                                             top_k, hidden, down, weights,
@@ -1026,8 +1049,8 @@ int decode_step(const uint8_t* w13, const float* s13, const uint8_t* w2, const f
                                x, x_stride, logits, logits_dtype, logits_stride, top_k,
                                exact_routes, ids, count, active, gate_up, &fc1);
   if (status != D3_OK) return status;
-  status = check_expert_gemm(2, w2, s2, num_experts, hidden, intermediate, ids, count, capacity,
-                             top_k, gate_up, nullptr, exact_routes, nullptr, down, &fc2);
+  status = check_expert_gemm(2, w2, s2, num_experts, hidden, intermediate, ids, count, active,
+                             capacity, top_k, gate_up, nullptr, exact_routes, nullptr, down, &fc2);
   if (status != D3_OK) return status;
   status = check_route_combine(occupancy, capacity, logits, logits_dtype, logits_stride, num_experts,
                                top_k, hidden, down, weights, weights_dtype, out, &combine);
@@ -1106,12 +1129,13 @@ using namespace d3;
 extern "C" int d3_decode_expert_gemm(int32_t mode, const uint8_t* w, const float* ws,
                                      int32_t num_experts, int32_t n, int32_t k,
                                      const int32_t* ids, const int32_t* row_count,
-                                     int32_t capacity, int32_t top_k, const void* a,
-                                     const float* a_scales, int32_t exact_routes,
+                                     const int32_t* row_slots, int32_t capacity, int32_t top_k,
+                                     const void* a, const float* a_scales, int32_t exact_routes,
                                      uint16_t* out_bf16, float* out_f32, void* stream) {
   GemmLaunch launch{};
-  const int status = check_expert_gemm(mode, w, ws, num_experts, n, k, ids, row_count, capacity,
-                                       top_k, a, a_scales, exact_routes, out_bf16, out_f32, &launch);
+  const int status = check_expert_gemm(mode, w, ws, num_experts, n, k, ids, row_count, row_slots,
+                                       capacity, top_k, a, a_scales, exact_routes, out_bf16, out_f32,
+                                       &launch);
   if (status != D3_OK) return status;
   launch_expert_gemm(launch, as_stream(stream));
   D3_LAUNCHED("decode_expert_gemm");

@@ -21,6 +21,6 @@ void clear_error() { g_message[0] = '\0'; }
 
 }  // namespace d3
 
-extern "C" int d3_abi_version(void) { return 11; }
+extern "C" int d3_abi_version(void) { return 12; }
 
 extern "C" const char* d3_last_error(void) { return d3::g_message; }

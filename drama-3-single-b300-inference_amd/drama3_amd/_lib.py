@@ -76,7 +76,7 @@ SIGNATURES = {
     "d3_expert_fc2_swiglu": (
         _i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _p, _p]),
     "d3_decode_expert_gemm": (
-        _i32, [_i32, _p, _p, _i32, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _i32, _p, _p, _p]),
+        _i32, [_i32, _p, _p, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _p, _p, _i32, _p, _p, _p]),
     "d3_decode_route_fc1": (
         _i32, [_p, _p, _i32, _i32, _i32, _p, _i32, _p, _i64, _p, _i32, _i64, _i32, _i32, _p, _p,
                _p, _p, _p]),

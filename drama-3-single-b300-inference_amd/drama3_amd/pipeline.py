@@ -415,18 +415,21 @@ class MoEWorkspace:
         if layout != LAYOUT_FRAGMENT:
             raise ValueError("sortless decode needs fragment-major weights (prepare_experts)")
         call("d3_decode_expert_gemm", 0, ptr(w), ptr(ws), s.num_experts, 2 * s.intermediate,
-             s.hidden, ptr(self.ids), ptr(row_count), s.rows, s.top_k, ptr(self.q),
+             s.hidden, ptr(self.ids), ptr(row_count), None, s.rows, s.top_k, ptr(self.q),
              ptr(self.x_scales), self.exact_routes, ptr(self.gate_up), None, stream)
 
-    def decode_fc2(self, experts, row_count=None, stream=None) -> None:
-        """Sortless FC2 with the SwiGLU requant in its prologue: down[pair]."""
+    def decode_fc2(self, experts, row_count=None, stream=None, row_slots=None) -> None:
+        """Sortless FC2 with the SwiGLU requant in its prologue: down[pair],
+        or down[slot pair] with ``row_slots`` (decode_route_fc1's
+        ``active``), the layout decode_route_combine reads."""
         s, stream = self.shape, self._stream(stream)
         w, ws, layout = fc2_operands(experts)
         if layout != LAYOUT_FRAGMENT:
             raise ValueError("sortless decode needs fragment-major weights (prepare_experts)")
+        require_cuda(row_slots)
         call("d3_decode_expert_gemm", 2, ptr(w), ptr(ws), s.num_experts, s.hidden,
-             s.intermediate, ptr(self.ids), ptr(row_count), s.rows, s.top_k, ptr(self.gate_up),
-             None, self.exact_routes, None, ptr(self.down), stream)
+             s.intermediate, ptr(self.ids), ptr(row_count), ptr(row_slots), s.rows, s.top_k,
+             ptr(self.gate_up), None, self.exact_routes, None, ptr(self.down), stream)
 
     def decode_route_fc1(self, experts, occupancy, x, logits, active, count,
                          stream=None) -> None:

@@ -431,7 +431,11 @@ int d3_expert_fc2_swiglu(const uint8_t *w2, const float *s2, int32_t weight_layo
  *   mode 2 (FC2): a = gate_up bf16 [capacity * top_k, 2k]; the SwiGLU
  *                 requant of each route is computed in the prologue exactly
  *                 as d3_silu_mul_quant -> out_f32 down [capacity * top_k, n],
- *                 n = H, k = I.
+ *                 n = H, k = I.  With row_slots int32 [capacity] (the slot
+ *                 of each row: d3_decode_route_fc1's active) down rows are
+ *                 indexed by slot pair, row_slots[row] * top_k + rank, the
+ *                 layout d3_decode_route_combine reads; NULL: by pair.
+ *                 Mode 0 takes row_slots = NULL.
  * Values equal d3_expert_gemm's for the same pair.  Weights must be
  * fragment-major (d3_pack_expert_weights).  A workgroup of an expert with no
  * route reads half a weight tile before it knows, so this suits batches
@@ -440,8 +444,9 @@ int d3_expert_fc2_swiglu(const uint8_t *w2, const float *s2, int32_t weight_layo
  */
 int d3_decode_expert_gemm(int32_t mode, const uint8_t *w, const float *ws, int32_t num_experts,
                           int32_t n, int32_t k, const int32_t *ids, const int32_t *row_count,
-                          int32_t capacity, int32_t top_k, const void *a, const float *a_scales,
-                          int32_t exact_routes, uint16_t *out_bf16, float *out_f32, void *stream);
+                          const int32_t *row_slots, int32_t capacity, int32_t top_k,
+                          const void *a, const float *a_scales, int32_t exact_routes,
+                          uint16_t *out_bf16, float *out_f32, void *stream);
 
 /*
  * A1-A3, A5, A8  Decode FC1 straight from the slots (no front launch).
@@ -473,12 +478,15 @@ int d3_decode_route_fc1(const uint8_t *w, const float *ws, int32_t num_experts, 
  * A4, A12  Weighted combine of the step started by d3_decode_route_fc1.
  * Replaces route_kernel's weights (src/drama3/kernels.py:360-383) and the
  * combine (kernels.py:319-322) for the decode step.  One workgroup per
- * (slot, 512 columns): an occupied slot's row r gets
- * out[r] = bf16(sum_rank w[rank] * down[r * top_k + rank]) in rank order,
- * w being the front's routing weights of the slot's logits rounded to
- * weights_dtype (bf16 or f32), which are also stored in weights
- * [capacity, top_k] by row.  Same bytes as d3_moe_front's weights +
- * d3_weighted_combine.  capacity <= 256, top_k <= 8, E <= 256.
+ * (slot, 512 columns): occupied slot s, row r, gets
+ * out[r] = bf16(sum_rank w[rank] * down[s * top_k + rank]) in rank order
+ * (down f32 [capacity * top_k, hidden] by slot pair, as d3_decode_expert_gemm
+ * mode 2 writes it with row_slots; the slot indexing lets the down rows load
+ * with the logits, before the row is known), w being the front's routing
+ * weights of the slot's logits rounded to weights_dtype (bf16 or f32),
+ * which are also stored in weights [capacity, top_k] by row.  Same bytes
+ * as d3_moe_front's weights + d3_weighted_combine.  capacity <= 256,
+ * top_k <= 8, E <= 256.
  */
 int d3_decode_route_combine(const uint8_t *occupancy, int32_t capacity, const void *logits,
                             int32_t logits_dtype, int64_t logits_stride, int32_t num_experts,
@@ -493,8 +501,9 @@ int d3_decode_route_combine(const uint8_t *occupancy, int32_t capacity, const vo
  * expert_down_kernel and the combine kernels.py:290-322, 344) for one
  * step: d3_decode_route_fc1 (ids int32 [capacity, top_k], *count, active
  * int32 [capacity], gate_up bf16 [capacity * top_k, 2I] by pair), then
- * d3_decode_expert_gemm mode 2 (down f32 [capacity * top_k, hidden] by pair)
- * with row_count = count, then d3_decode_route_combine (weights [capacity,
+ * d3_decode_expert_gemm mode 2 with row_count = count and row_slots = active
+ * (down f32 [capacity * top_k, hidden] by slot pair), then
+ * d3_decode_route_combine (weights [capacity,
  * top_k] in weights_dtype, out bf16 [capacity, hidden]: row r < *count
  * belongs to slot active[r]).  Every stage's arguments are checked before
  * the first launch; the limits are those of the three entry points

@@ -82,7 +82,7 @@ def test_capacity_helpers(lib):
     for pairs, experts, tile in ((32, 16, 16), (384, 128, 16), (33280, 128, 64), (0, 8, 16)):
         assert lib.d3_max_sorted_rows(pairs, experts, tile) == om.max_sorted_rows(pairs, experts, tile)
     assert lib.d3_max_items(384, 128, 64) == (384 + 128 * 63) // 64
-    assert lib.d3_abi_version() == 11
+    assert lib.d3_abi_version() == 12
     # wide sort scratch: chunk histograms [ceil(pairs / 512)][E] + ranks [pairs]
     assert lib.d3_sort_wide_scratch_ints(3668, 8, 128) == (-(-3668 * 8 // 512)) * 128 + 3668 * 8
     assert lib.d3_sort_wide_scratch_ints(-1, 8, 128) == -1
@@ -171,14 +171,17 @@ def test_decode_gemm_contract(lib):
     from drama3_amd import _lib
 
     with pytest.raises(ValueError, match="mode"):
-        _lib.call("d3_decode_expert_gemm", 1, 16, 16, 4, 512, 1024, 16, None, 64, 8, 16, 16, 64,
-                  16, None, None)
+        _lib.call("d3_decode_expert_gemm", 1, 16, 16, 4, 512, 1024, 16, None, None, 64, 8, 16, 16,
+                  64, 16, None, None)
     with pytest.raises(ValueError, match="capacity"):
-        _lib.call("d3_decode_expert_gemm", 0, 16, 16, 4, 512, 1024, 16, None, 300, 8, 16, 16, 64,
-                  16, None, None)
+        _lib.call("d3_decode_expert_gemm", 0, 16, 16, 4, 512, 1024, 16, None, None, 300, 8, 16, 16,
+                  64, 16, None, None)
     with pytest.raises(ValueError, match="K=768"):
-        _lib.call("d3_decode_expert_gemm", 0, 16, 16, 4, 512, 768, 16, None, 64, 8, 16, 16, 64,
-                  16, None, None)
+        _lib.call("d3_decode_expert_gemm", 0, 16, 16, 4, 512, 768, 16, None, None, 64, 8, 16, 16,
+                  64, 16, None, None)
+    with pytest.raises(ValueError, match="row_slots"):  # the slot layout is FC2's only
+        _lib.call("d3_decode_expert_gemm", 0, 16, 16, 4, 512, 1024, 16, None, 16, 64, 8, 16, 16,
+                  64, 16, None, None)
 
 
 def test_route_fc1_and_combine_contract(lib):

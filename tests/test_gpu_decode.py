@@ -1,10 +1,11 @@
 """Sortless decode expert GEMMs (d3_decode_expert_gemm) and the three-launch
 step that starts from the slots (d3_decode_route_fc1 + FC2 +
 d3_decode_route_combine).  Every expert-GEMM workgroup finds its expert's
-routes itself and rows are indexed by pair.  All results are bit-identical
-to the sorted chain's for the same pairs: ids, routing weights, the slot
-list, gate_up (mapped through the sorted layout), down and the combined
-output."""
+routes itself and rows are indexed by pair (the three-launch step's down
+rows by slot pair, slot * top_k + rank).  All results are bit-identical to
+the sorted chain's for the same pairs: ids, routing weights, the slot list,
+gate_up (mapped through the sorted layout), down (mapped through the slot
+list) and the combined output."""
 
 import numpy as np
 import pytest
@@ -29,7 +30,15 @@ def steps_for(w, device, experts, slots=64):
     return frontless, front, sorted_chain
 
 
-def compare(sortless, chain):
+def pair_rows(down, active, n, top_k):
+    """Down rows stored by slot pair (the three-launch step), in pair order:
+    row r's rank-k route is slot active[r]'s."""
+    slots = active[:n].long()
+    index = (slots[:, None] * top_k + torch.arange(top_k, device=down.device)).reshape(-1)
+    return down[index]
+
+
+def compare(sortless, chain, by_slot=False):
     n = int(chain.count.item())
     assert int(sortless.count.item()) == n
     assert torch.equal(sortless.active, chain.active)
@@ -38,7 +47,8 @@ def compare(sortless, chain):
     assert torch.equal(a.ids[:n], b.ids[:n])
     assert torch.equal(a.weights[:n].view(torch.int16 if a.weights.dtype == torch.bfloat16 else torch.int32),
                        b.weights[:n].view(torch.int16 if b.weights.dtype == torch.bfloat16 else torch.int32))
-    assert torch.equal(a.down[:pairs].view(torch.int32), b.down[:pairs].view(torch.int32))
+    down = pair_rows(a.down, sortless.active, n, a.shape.top_k) if by_slot else a.down[:pairs]
+    assert torch.equal(down.view(torch.int32), b.down[:pairs].view(torch.int32))
     # chain gate_up row at sorted position p holds pair sorted_ids[p]
     total = int(b.total.item())
     order = b.sorted_ids[:total].cpu().numpy()
@@ -56,7 +66,7 @@ def run_all(steps, occ, xs, ls, experts):
     torch.cuda.synchronize()
     frontless, front, chain = steps
     assert frontless.uses_frontless(occ, xs, ls) and not front.uses_frontless(occ, xs, ls)
-    n = compare(frontless, chain)
+    n = compare(frontless, chain, by_slot=True)
     assert compare(front, chain) == n
     return n
 
@@ -263,10 +273,11 @@ def test_route_slices_of_hot_experts(device, slots, live):
     a, b = frontless.workspace, front.workspace
     assert int(frontless.count.item()) == n and torch.equal(frontless.active, chain.active)
     assert torch.equal(a.ids[:n], b.ids[:n]) and torch.equal(a.ids[:n], chain.workspace.ids[:n])
-    assert torch.equal(a.down[:8 * n].view(torch.int32), b.down[:8 * n].view(torch.int32))
+    assert torch.equal(pair_rows(a.down, frontless.active, n, 8).view(torch.int32),
+                       b.down[:8 * n].view(torch.int32))
     assert torch.equal(a.out[:n].view(torch.int16), b.out[:n].view(torch.int16))
     if counts.max() <= 64:
-        assert compare(frontless, chain) == n
+        assert compare(frontless, chain, by_slot=True) == n
     expected = om.expert_ffn(np_bf16(xs)[active], ids, weights, oracle_weights(experts_cpu))
     tolerance = EXACT if counts.max() <= 64 else CONTRACTION
     stats = assert_bf16_close(np_bf16(a.out)[:n], expected, **tolerance)
