@@ -273,6 +273,14 @@ __device__ __forceinline__ uint32_t collect_u32(const void* p) {
 // Every store of the calling thread has completed (reached the coherent
 // level for published stores) before it proceeds.
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+// Workgroup barrier ordering LDS only: global loads and stores issued before
+// it stay in flight (__syncthreads also waits for every outstanding global
+// access).  For kernels whose threads exchange data through LDS alone.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 __device__ __forceinline__ int take_ticket(int32_t* ticket) {
   return __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

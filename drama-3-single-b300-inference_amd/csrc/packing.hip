@@ -103,21 +103,24 @@ constexpr int kMixedMaxRows = 8192;   // row space with prefix reuse (LDS owner 
 constexpr int kMixedMaxPrompts = 16;  // prompts compared for prefix reuse
 constexpr int kMixedMaxBounds = 1025; // boundaries staged in LDS (1024 sequences)
 constexpr int kMixedMaxCodes = 16;    // frame codes compared from registers
+constexpr int kMixedCodeParts = 4;    // threads per (pair, row) comparison, each a quarter of the codes
+constexpr int kMixedPartCodes = kMixedMaxCodes / kMixedCodeParts;
 constexpr int kMixedMaxPairs = kMixedMaxPrompts * (kMixedMaxPrompts - 1) / 2;  // 120
 
 // Exclusive rank of `flag` among the workgroup's threads (thread order) and
-// the workgroup's total.  Two barriers; `wave_counts` is free again on return.
+// the workgroup's total.  Two LDS barriers; `wave_counts` is free again on
+// return.
 __device__ __forceinline__ int block_rank(bool flag, int* wave_counts, int* total) {
   const int wave = threadIdx.x / kWave;
   const uint64_t mask = __ballot(flag);
   if (lane_id() == 0) wave_counts[wave] = __popcll(mask);
-  __syncthreads();
+  lds_barrier();
   int before = 0, all = 0;
   for (int w = 0; w < kMixedWaves; ++w) {
     before += w < wave ? wave_counts[w] : 0;
     all += wave_counts[w];
   }
-  __syncthreads();
+  lds_barrier();
   *total = all;
   return before + __popcll(mask & lanemask_lt());
 }
@@ -171,6 +174,83 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
   if (tid < nbounds) bounds[tid] = bound0;
   if (tid + kMixedThreads < nbounds) bounds[tid + kMixedThreads] = bound1;
   if (positions != nullptr && tid < sequences) sequence_slot[tid] = slot_of;
+  // Threads exchange data through LDS only (inputs are read, outputs
+  // written once), so every barrier here is an LDS barrier: global loads
+  // stay in flight across them.
+  lds_barrier();  // bounds written
+
+  // b[prompts] after clamping: the largest clamped boundary.
+  int live_prefill = 0;
+  for (int i = 0; i <= prompts; ++i) {
+    const int b = bounds[i];
+    const int clamped = b > capacity ? capacity : b;
+    live_prefill = clamped > live_prefill ? clamped : live_prefill;
+  }
+
+  // 2a. Prefix reuse set-up from the boundaries alone: clamped, non-
+  //     decreasing starts; for every pair (i, j), j < i, its comparable
+  //     length common[i][j] (the shorter prompt's) and its first flat
+  //     comparison index first[q].  Each thread then issues the frame loads
+  //     of its first comparison unit, which stay in flight through the slot
+  //     compaction below.
+  const int pairs = reuse ? prompts * (prompts - 1) / 2 : 0;
+  if (reuse) {
+    if (tid == 0) {
+      int previous = 0;
+      for (int i = 0; i <= prompts; ++i) {
+        int b = bounds[i];
+        b = b < previous ? previous : (b > capacity ? capacity : b);
+        starts[i] = b;
+        previous = b;
+      }
+      int sum = 0;
+      for (int q = 0, i = 1, base = 0; q < pairs; ++q) {
+        if (q - base == i) base += i++;  // pair q = (i, q - base)
+        const int j = q - base;
+        const int li = starts[i + 1] - starts[i], lj = starts[j + 1] - starts[j];
+        const int n = li < lj ? li : lj;
+        common[i * kMixedMaxPrompts + j] = n;
+        first[q] = sum;
+        sum += n;
+      }
+      first[pairs] = sum;
+    }
+    lds_barrier();
+  }
+  const int compares = reuse ? first[pairs] : 0;
+  // The pair (i, j) and row p of flat comparison f.
+  auto comparison = [&](int f, int& i, int& j, int& p) {
+    int q = 0;  // the pair holding f: last q with first[q] <= f
+    for (int step = 64; step >= 1; step >>= 1)  // pairs <= 120 < 128
+      if (q + step < pairs && first[q + step] <= f) q += step;
+    int base = 0;
+    i = 1;
+    while (base + i <= q) base += i++;
+    j = q - base;
+    p = f - first[q];
+  };
+  // Comparison unit u = kMixedCodeParts f + part: codes part, part + 4, ...
+  // of comparison f.  A thread's first unit (u = tid) is loaded here.
+  const int units = compares * kMixedCodeParts;
+  // (uniform; with at least one comparison, frame row 0 exists)
+  const bool registered = reuse && codes <= kMixedMaxCodes && compares > 0;
+  int64_t va[kMixedPartCodes], vb[kMixedPartCodes];
+  int fi = 0, fj = 0, fp = 0;
+  const bool preloaded = registered && tid < units;
+  if (registered) {
+    // Branch-free loads (a thread without a unit, or a code past `codes`,
+    // reads frame row 0 / code 0 and ignores it): all of them are in
+    // flight before the compaction's first barrier.
+    if (preloaded) comparison(tid / kMixedCodeParts, fi, fj, fp);
+    const int64_t* a = frames + (preloaded ? static_cast<int64_t>(starts[fi] + fp) * codes : 0);
+    const int64_t* b = frames + (preloaded ? static_cast<int64_t>(starts[fj] + fp) * codes : 0);
+#pragma unroll
+    for (int m = 0; m < kMixedPartCodes; ++m) {
+      const int c = tid % kMixedCodeParts + m * kMixedCodeParts;
+      va[m] = a[c < codes ? c : 0];
+      vb[m] = b[c < codes ? c : 0];
+    }
+  }
 
   // 1. slot compaction and decode row slots
   int occupied = 0;
@@ -190,84 +270,57 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
   for (int j = used + tid; j < decode_rows; j += kMixedThreads) decode_slots[j] = padding_start + j;
   if (tid == 0) *count = occupied;
 
-  // 2. clamped boundaries and prefix ownership
-  // b[prompts] after clamping: the largest clamped boundary.
-  int live_prefill = 0;
-  __syncthreads();  // bounds written
-  for (int i = 0; i <= prompts; ++i) {
-    const int b = bounds[i];
-    const int clamped = b > capacity ? capacity : b;
-    live_prefill = clamped > live_prefill ? clamped : live_prefill;
-  }
+  // 2b. prefix ownership: prompt i (suffix rows [b[i], b[i+1])) aliases its
+  //     first L rows to the earliest earlier prompt with the longest
+  //     agreeing leading run L.  Every (pair, row) comparison of all pairs
+  //     at once, a quarter of its codes per thread, so the frames cost one
+  //     memory round trip per 256 rows rather than one per 64 rows of each
+  //     pair (and the first of them overlaps the compaction).
   if (reuse) {
-    if (tid == 0) {
-      int previous = 0;
-      for (int i = 0; i <= prompts; ++i) {
-        int b = bounds[i];
-        b = b < previous ? previous : (b > capacity ? capacity : b);
-        starts[i] = b;
-        previous = b;
-      }
-    }
     for (int r = tid; r < full; r += kMixedThreads) owner_of[r] = r;
-    __syncthreads();
-    // common[i][j], j < i: first differing row of prompts i and j (or the
-    // shorter length).
-    const int pairs = prompts * (prompts - 1) / 2;
-    if (tid < pairs) {
-      int i = 1, base = 0;
-      while (base + i <= tid) base += i++;
-      const int j = tid - base;
-      const int li = starts[i + 1] - starts[i], lj = starts[j + 1] - starts[j];
-      common[i * kMixedMaxPrompts + j] = li < lj ? li : lj;
-    }
-    // Every (pair, row) comparison of all pairs at once, one per thread
-    // (flat index f = first[q] + p, first[] the pairs' running row counts),
-    // so the frames cost one memory round trip per 1024 rows rather than
-    // one per 64 rows of each pair.
-    __syncthreads();
-    if (tid == 0) {
-      int sum = 0;
-      for (int q = 0; q < pairs; ++q) {
-        int i = 1, base = 0;
-        while (base + i <= q) base += i++;
-        first[q] = sum;
-        sum += common[i * kMixedMaxPrompts + (q - base)];
-      }
-      first[pairs] = sum;
-    }
-    __syncthreads();
-    const int compares = first[pairs];
-    for (int f = tid; f < compares; f += kMixedThreads) {
-      int q = 0;  // the pair holding f: last q with first[q] <= f
-      for (int step = 64; step >= 1; step >>= 1)  // pairs <= 120 < 128
-        if (q + step < pairs && first[q + step] <= f) q += step;
-      int i = 1, base = 0;
-      while (base + i <= q) base += i++;
-      const int j = q - base;
-      const int p = f - first[q];
-      const int64_t* a = frames + static_cast<int64_t>(starts[i] + p) * codes;
-      const int64_t* b = frames + static_cast<int64_t>(starts[j] + p) * codes;
-      bool differ = false;
-      if (codes <= kMixedMaxCodes) {
-        // Issue every load of both rows before the first compare (a loop
-        // that compares as it loads waits a round trip per code).
-        int64_t va[kMixedMaxCodes], vb[kMixedMaxCodes];
+    if (registered) {
+      for (int u = tid; u < units; u += kMixedThreads) {
+        const int part = u % kMixedCodeParts;
+        int i, j, p;
+        bool differ = false;
+        if (u == tid) {
+          i = fi;
+          j = fj;
+          p = fp;
 #pragma unroll
-        for (int c = 0; c < kMixedMaxCodes; ++c)
-          if (c < codes) {
-            va[c] = a[c];
-            vb[c] = b[c];
+          for (int m = 0; m < kMixedPartCodes; ++m) {
+            // compared here, after the compaction (not where they were loaded)
+            asm volatile("" : "+v"(va[m]), "+v"(vb[m]));
+            differ |= part + m * kMixedCodeParts < codes && va[m] != vb[m];
+          }
+        } else {
+          comparison(u / kMixedCodeParts, i, j, p);
+          const int64_t* a = frames + static_cast<int64_t>(starts[i] + p) * codes;
+          const int64_t* b = frames + static_cast<int64_t>(starts[j] + p) * codes;
+          int64_t xa[kMixedPartCodes], xb[kMixedPartCodes];
+#pragma unroll
+          for (int m = 0; m < kMixedPartCodes; ++m) {
+            const int c = part + m * kMixedCodeParts;
+            xa[m] = a[c < codes ? c : 0];
+            xb[m] = b[c < codes ? c : 0];
           }
 #pragma unroll
-        for (int c = 0; c < kMixedMaxCodes; ++c)
-          if (c < codes) differ |= va[c] != vb[c];
-      } else {
-        for (int c = 0; c < codes; ++c) differ |= a[c] != b[c];
+          for (int m = 0; m < kMixedPartCodes; ++m) differ |= part + m * kMixedCodeParts < codes && xa[m] != xb[m];
+        }
+        if (differ) atomicMin(&common[i * kMixedMaxPrompts + j], p);
       }
-      if (differ) atomicMin(&common[i * kMixedMaxPrompts + j], p);
+    } else {
+      for (int f = tid; f < compares; f += kMixedThreads) {
+        int i, j, p;
+        comparison(f, i, j, p);
+        const int64_t* a = frames + static_cast<int64_t>(starts[i] + p) * codes;
+        const int64_t* b = frames + static_cast<int64_t>(starts[j] + p) * codes;
+        bool differ = false;
+        for (int c = 0; c < codes; ++c) differ |= a[c] != b[c];
+        if (differ) atomicMin(&common[i * kMixedMaxPrompts + j], p);
+      }
     }
-    __syncthreads();
+    lds_barrier();
     for (int i = 1; i < prompts; ++i) {
       int longest = 0, source = 0;
       for (int j = 0; j < i; ++j) {
@@ -279,7 +332,7 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
       }
       for (int p = tid; p < longest; p += kMixedThreads)
         owner_of[decode_rows + starts[i] + p] = owner_of[decode_rows + starts[source] + p];
-      __syncthreads();
+      lds_barrier();
     }
   }
 
@@ -308,7 +361,7 @@ __global__ __launch_bounds__(kMixedThreads) void mixed_rows_kernel(
       keep[at] = r;
       if (reuse) owner_of[r] = -(at + 1);
     }
-    if (reuse) __syncthreads();
+    if (reuse) lds_barrier();
     if (in) {
       int64_t back = 0;
       if (live) {
