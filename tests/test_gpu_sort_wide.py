@@ -113,3 +113,22 @@ def test_reference_sort_routes_takes_wide_path(device):
     o = om.sort_routes(ids, 128, 16)
     assert np.array_equal(sorted_ids.cpu().numpy()[:o.total], o.sorted_ids)
     assert np.array_equal(inverse.cpu().numpy(), o.inverse)
+
+
+def test_workspace_pads_items_only_for_busy_experts(device):
+    """MoEWorkspace asks the wide sort for padded items (aligned capacity)
+    when its experts average at least 1.5 items of routes at full capacity
+    (config 4: 229 routes per expert), not at about one item per expert
+    (4,096 rows x E256: 128 routes each), nor below the wide sort."""
+    from drama3_amd import _lib
+    from drama3_amd.pipeline import MoEWorkspace, Shape
+
+    lib = _lib.load()
+    cases = [((3668, 128, 2048, 768), True), ((4096, 256, 2048, 512), False),
+             ((1000, 128, 1024, 256), False)]
+    for dims, aligned in cases:
+        ws = MoEWorkspace(Shape(*dims), device)
+        assert ws.aligned_items == aligned
+        want = (lib.d3_max_items_aligned if aligned else lib.d3_max_items)(
+            ws.shape.pairs, ws.shape.num_experts, ws.item_rows)
+        assert ws.max_items == want
