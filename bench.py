@@ -34,7 +34,7 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 # the 1 GiB device copy in the same runs); profiles/expert_gemm_c2_hbm_traffic.md.
 # Re-measure whenever the FC1 kernel or its tiling changes.
 FC1_TRAFFIC_BYTES = {"kernel": "decode_gemm_kernel<16,1,1,6,1,true>", "bytes": 401749606,
-                     "measured_on": "bb4fea4, again on 294a999 (profiles/expert_gemm_c2_hbm_traffic.md)"}
+                     "measured_on": "bb4fea4, again on 294a999 and 218139f (profiles/expert_gemm_c2_hbm_traffic.md)"}
 
 
 def parse():
