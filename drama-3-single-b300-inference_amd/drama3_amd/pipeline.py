@@ -22,8 +22,10 @@ Step (one kernel each, all on the current stream):
 Decode step (``DecodeStep``, fragment-major weights, >= 1 route per expert): no
 route sort and no front launch.  ``decode_route_fc1`` routes (expert ranks
 from the logits), quantises and runs FC1 from the slots; ``decode_fc2``
-finds each expert's routes from the ids FC1 wrote; ``decode_route_combine``
-recomputes the routing weights and combines.
+finds each expert's routes from the ids FC1 wrote and stores its down rows
+by slot pair (slot * top_k + rank); ``decode_route_combine`` recomputes the
+routing weights and combines, loading each slot's down rows with its
+logits.
 """
 
 from __future__ import annotations
