@@ -282,3 +282,39 @@ def test_route_slices_of_hot_experts(device, slots, live):
     tolerance = EXACT if counts.max() <= 64 else CONTRACTION
     stats = assert_bf16_close(np_bf16(a.out)[:n], expected, **tolerance)
     print(f"slots {slots} live {n}: routes per expert {counts.tolist()} {stats}", flush=True)
+
+
+def test_standalone_entries_match_the_step(device):
+    """d3_decode_route_fc1, d3_decode_expert_gemm mode 2 and
+    d3_decode_route_combine called one by one: with row_slots = the slot
+    list, FC2's down rows (by slot pair) and the combined rows equal
+    d3_decode_step's byte for byte; without it, FC2 stores the same rows by
+    pair (row * top_k + rank).  Config 2 with a quarter of the slots free."""
+    from drama3_amd import workloads
+    from drama3_amd.expert_weights import prepare_experts
+    from drama3_amd.pipeline import DecodeStep
+
+    w = workloads.config2()
+    step = w.steps[0]
+    experts = prepare_experts(w.experts.to(device))
+    occ = step.occupancy.to(device)
+    xs, ls = step.x_slots.to(device), step.logits_slots.to(device)
+    whole = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device)
+    parts = DecodeStep(64, w.num_experts, w.hidden, w.intermediate, device=device)
+    assert whole.uses_frontless(occ, xs, ls)
+    out_whole = whole(occ, xs, ls, experts).clone()
+    ws = parts.workspace
+    ws.decode_route_fc1(experts, occ, xs, ls, parts.active, parts.count)
+    ws.decode_fc2(experts, parts.count, row_slots=parts.active)
+    out_parts = ws.decode_route_combine(occ, ls).clone()
+    torch.cuda.synchronize()
+    n = int(whole.count.item())
+    assert int(parts.count.item()) == n and torch.equal(parts.active, whole.active)
+    slots = whole.active[:n].long()
+    by_slot = (slots[:, None] * 8 + torch.arange(8, device=device)).reshape(-1)
+    assert torch.equal(ws.down[by_slot].view(torch.int32), whole.workspace.down[by_slot].view(torch.int32))
+    assert torch.equal(out_parts[:n].view(torch.int16), out_whole[:n].view(torch.int16))
+    # the same FC2 without the slot list: rows by pair
+    ws.decode_fc2(experts, parts.count)
+    torch.cuda.synchronize()
+    assert torch.equal(ws.down[:8 * n].view(torch.int32), whole.workspace.down[by_slot].view(torch.int32))
