@@ -21,29 +21,29 @@ pytestmark = pytest.mark.gpu
 CODES = 11
 
 
-def prompts_with_prefixes(rng, lengths, share):
+def prompts_with_prefixes(rng, lengths, share, codes=CODES):
     """Prompt frames where prompt i copies a leading run of an earlier prompt
     with probability ``share`` (then diverges at one random code)."""
     prompts = []
     for n in lengths:
-        p = rng.integers(0, 4, (n, CODES)).astype(np.int64)
+        p = rng.integers(0, 4, (n, codes)).astype(np.int64)
         if prompts and rng.random() < share:
             src = prompts[int(rng.integers(0, len(prompts)))]
             run = int(rng.integers(0, min(n, len(src)) + 1))
             p[:run] = src[:run]
             if run < min(n, len(src)):
                 p[run] = src[run]
-                p[run, int(rng.integers(0, CODES))] += 1 + int(rng.integers(0, 3))
+                p[run, int(rng.integers(0, codes))] += 1 + int(rng.integers(0, 3))
         prompts.append(p)
     return prompts
 
 
-def layout_inputs(rng, slots, live, lengths, capacity, share=0.8):
+def layout_inputs(rng, slots, live, lengths, capacity, share=0.8, codes=CODES):
     occupancy = np.zeros(slots, dtype=np.uint8)
     occupancy[rng.permutation(slots)[:live]] = 1
-    prompts = prompts_with_prefixes(rng, lengths, share)
+    prompts = prompts_with_prefixes(rng, lengths, share, codes)
     total = sum(lengths)
-    frames = rng.integers(0, 4, (capacity, CODES)).astype(np.int64)
+    frames = rng.integers(0, 4, (capacity, codes)).astype(np.int64)
     if total:
         frames[:total] = np.concatenate(prompts)
     boundaries = np.concatenate([[0], np.cumsum(lengths), [capacity]]).astype(np.int32)
@@ -102,6 +102,22 @@ def test_layout_matches_oracle(device, case):
     expected = om.mixed_layout(occupancy, d, slots // 2, boundaries, prompts, capacity,
                                frames if reuse and prompts >= 2 else None)
     assert_layout(rows, expected, d)
+
+
+@pytest.mark.parametrize("codes", [1, 3, 16, 20])
+def test_layout_frame_widths(device, codes):
+    """Frame rows of 1 and 3 codes (fewer than the four threads of a
+    comparison), 16 (the widest compared from registers) and 20 (compared
+    by a loop over the codes)."""
+    rng = np.random.default_rng(codes)
+    lengths = [120, 60, 120, 90]
+    occupancy, frames, boundaries = layout_inputs(rng, 64, 40, lengths, 400, share=1.0,
+                                                  codes=codes)
+    rows = run_layout(device, occupancy, 64, 32, boundaries, len(lengths), 400, frames)
+    expected = om.mixed_layout(occupancy, 64, 32, boundaries, len(lengths), 400, frames,
+                               codes=codes)
+    assert_layout(rows, expected, 64)
+    assert int(rows.keep_count.item()) < 40 + sum(lengths)  # some prefix was reused
 
 
 def test_layout_clamps_bad_boundaries(device):
