@@ -90,14 +90,16 @@ def test_wide_sort_skewed_and_live_rows(device):
     check({k: v for k, v in got.items()}, ids[:live], experts, 16, 128)
 
 
-@pytest.mark.parametrize("rows,experts,item_rows", [(4096, 256, 128), (3001, 64, 256), (1100, 512, 16)])
-def test_wide_sort_aligned_items(device, rows, experts, item_rows):
+@pytest.mark.parametrize("rows,experts,item_rows,live", [(4096, 256, 128, None), (3001, 64, 256, None),
+                                                       (1100, 512, 16, None), (3668, 128, 128, 2900)])
+def test_wide_sort_aligned_items(device, rows, experts, item_rows, live):
     """Aligned capacity: every expert's first item sits at an even index
-    and the list is the plain one with one empty item after each odd run."""
+    and the list is the plain one with one empty item after each odd run
+    (also with a device row count below the capacity)."""
     rng = np.random.default_rng(rows * 3 + experts)
     ids = np.stack([rng.permutation(experts)[:8] for _ in range(rows)]).astype(np.int64)
-    got = run_wide(device, ids, experts, 16, item_rows, aligned=True)
-    check(got, ids, experts, 16, item_rows, aligned=True)
+    got = run_wide(device, ids, experts, 16, item_rows, live_rows=live, aligned=True)
+    check(got, ids if live is None else ids[:live], experts, 16, item_rows, aligned=True)
     items = got["items"][:int(got["num_items"][0])]
     first = np.flatnonzero(np.r_[True, items[1:, 0] != items[:-1, 0]])
     assert np.all(first % 2 == 0)
