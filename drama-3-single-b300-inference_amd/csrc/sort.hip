@@ -160,7 +160,10 @@ __global__ __launch_bounds__(kPlaceThreads) void wide_place_kernel(
                                 &total, &total_items);
   const int count_e = tid < num_experts ? counts[tid] : 0;
   const int items_e = (count_e + item_rows - 1) / item_rows;
-  if (align_items) {
+  // Padding pays while the experts with routes average at least 1.5 items;
+  // at about one item each, most of them would take an empty item.
+  const int used = __syncthreads_count(count_e > 0);
+  if (align_items && 2 * total_items >= 3 * used) {  // uniform
     // Every expert's items start on an even item (an odd count is followed
     // by one empty item), so the grouped GEMMs' XCD runs of two consecutive
     // items hold one expert's items and share its weights in that L2.

@@ -150,13 +150,12 @@ class MoEWorkspace:
         # The wide sort pads each expert's items to an even count when the
         # items array holds the padding: the tiled grouped GEMMs, which give
         # each XCD runs of two consecutive items, then never split a pair of
-        # one expert's items over two XCDs' L2s.  Worth it when experts
-        # average at least 1.5 items (config 4, 229 routes per expert:
-        # -5 us per step); at about one item per expert most experts would
-        # take an empty item (4,096 rows x E256: +28 us per layer, measured).
-        # Other consumers keep the unpadded list.
-        self.aligned_items = bool(self.wide_sort and grouped and not sortless
-                                  and 2 * pairs >= 3 * self.item_rows * shape.num_experts)
+        # one expert's items over two XCDs' L2s.  The sort pads only while
+        # the experts with routes average at least 1.5 items (config 4, 229
+        # routes per expert: -5 us per step); at about one item per expert
+        # most experts would take an empty item (4,096 rows x E256: +28 us
+        # per layer when padded).  Other consumers keep the unpadded list.
+        self.aligned_items = bool(self.wide_sort and grouped and not sortless)
         self.max_items = (lib.d3_max_items_aligned if self.aligned_items else lib.d3_max_items)(
             pairs, shape.num_experts, self.item_rows)
         dev = self.device

@@ -213,12 +213,14 @@ int d3_moe_front(const uint8_t *occupancy, int32_t num_slots, int32_t *active_sl
  * pairs (two launches) instead of one workgroup walking every pair.
  * Same arguments and outputs as d3_sort_routes (starts is required), plus a
  * caller-owned int32 scratch of d3_sort_wide_scratch_ints(rows, top_k, E)
- * ints.  With max_items >= d3_max_items_aligned(pairs, E, item_rows) the
- * items are aligned: every expert's items start at an even item index, and
- * an expert with an odd number of items is followed by one empty item
- * {expert, start, 0, 0} (counted in *num_items), so two consecutive items
- * never mix experts' weights; the grouped GEMMs skip empty items (their XCD
- * runs of two consecutive items then share one expert's weights in L2).  Replaces expert_counts_kernel / expert_offsets_kernel /
+ * ints.  With max_items >= d3_max_items_aligned(pairs, E, item_rows), and
+ * when the experts with routes average at least 1.5 items (decided on the
+ * device from the live histogram), the items are aligned: every expert's
+ * items start at an even item index, and an expert with an odd number of
+ * items is followed by one empty item {expert, start, 0, 0} (counted in
+ * *num_items), so two consecutive items never mix experts' weights; the
+ * grouped GEMMs skip empty items (their XCD runs of two consecutive items
+ * then share one expert's weights in L2).  Replaces expert_counts_kernel / expert_offsets_kernel /
  * expert_scatter_kernel (src/drama3/kernels.py:658-699) as native_moe runs
  * them for prefill (kernels.py:710-731).
  */

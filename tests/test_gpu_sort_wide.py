@@ -3,8 +3,9 @@ against the CPU oracle, bit for bit: histogram, padded offsets, stable
 sorted pair list with sentinel padding, expert ids, inverse map and work
 items, at prefill sizes, under skew, for int64 ids, with a device row count
 below the capacity, and at the 512-expert limit.  With an items array of
-d3_max_items_aligned's capacity each expert's items are padded to an even
-count by one empty item (rows 0).  The reference-named
+d3_max_items_aligned's capacity, and experts with routes averaging at least
+1.5 items, each expert's items are padded to an even count by one empty
+item (rows 0).  The reference-named
 sort_routes() takes this path above 8192 pairs."""
 
 import numpy as np
@@ -45,8 +46,18 @@ def run_wide(device, ids_np, experts, tile, item_rows, live_rows=None, dtype=tor
     return {k: v.cpu().numpy() for k, v in out.items()}
 
 
+def padded_items(counts, item_rows) -> bool:
+    """The wide sort's rule: pad while the experts with routes average at
+    least 1.5 items."""
+    items = sum(-(-int(c) // item_rows) for c in counts)
+    used = int(np.count_nonzero(counts))
+    return 2 * items >= 3 * used
+
+
 def check(got, ids_np, experts, tile, item_rows, aligned=False):
+    """Returns whether the items were padded."""
     o = om.sort_routes(ids_np, experts, tile)
+    aligned = aligned and padded_items(o.counts, item_rows)
     pairs = ids_np.size
     assert np.array_equal(got["counts"], o.counts)
     assert np.array_equal(got["starts"], o.starts)
@@ -67,6 +78,7 @@ def check(got, ids_np, experts, tile, item_rows, aligned=False):
     assert n == len(items)
     assert np.array_equal(got["items"][:n], np.array(items, np.int32).reshape(-1, 4))
     assert np.all(got["items"][n:, 0] == -1)
+    return aligned
 
 
 @pytest.mark.parametrize("rows,experts,dtype", [(3668, 128, torch.int32), (4200, 16, torch.int64),
@@ -90,19 +102,22 @@ def test_wide_sort_skewed_and_live_rows(device):
     check({k: v for k, v in got.items()}, ids[:live], experts, 16, 128)
 
 
-@pytest.mark.parametrize("rows,experts,item_rows,live", [(4096, 256, 128, None), (3001, 64, 256, None),
-                                                       (1100, 512, 16, None), (3668, 128, 128, 2900)])
-def test_wide_sort_aligned_items(device, rows, experts, item_rows, live):
-    """Aligned capacity: every expert's first item sits at an even index
-    and the list is the plain one with one empty item after each odd run
-    (also with a device row count below the capacity)."""
+@pytest.mark.parametrize("rows,experts,item_rows,live,padded", [
+    (4096, 256, 128, None, False),  # 128 routes per expert: about one item each, no padding
+    (3001, 64, 256, None, True), (1100, 512, 16, None, True), (3668, 128, 128, 2900, True)])
+def test_wide_sort_aligned_items(device, rows, experts, item_rows, live, padded):
+    """Aligned capacity: when padded, every expert's first item sits at an
+    even index and the list is the plain one with one empty item after each
+    odd run (also with a device row count below the capacity)."""
     rng = np.random.default_rng(rows * 3 + experts)
     ids = np.stack([rng.permutation(experts)[:8] for _ in range(rows)]).astype(np.int64)
     got = run_wide(device, ids, experts, 16, item_rows, live_rows=live, aligned=True)
-    check(got, ids if live is None else ids[:live], experts, 16, item_rows, aligned=True)
-    items = got["items"][:int(got["num_items"][0])]
-    first = np.flatnonzero(np.r_[True, items[1:, 0] != items[:-1, 0]])
-    assert np.all(first % 2 == 0)
+    assert check(got, ids if live is None else ids[:live], experts, 16, item_rows,
+                 aligned=True) == padded
+    if padded:
+        items = got["items"][:int(got["num_items"][0])]
+        first = np.flatnonzero(np.r_[True, items[1:, 0] != items[:-1, 0]])
+        assert np.all(first % 2 == 0)
 
 
 def test_reference_sort_routes_takes_wide_path(device):
@@ -117,16 +132,15 @@ def test_reference_sort_routes_takes_wide_path(device):
     assert np.array_equal(inverse.cpu().numpy(), o.inverse)
 
 
-def test_workspace_pads_items_only_for_busy_experts(device):
-    """MoEWorkspace asks the wide sort for padded items (aligned capacity)
-    when its experts average at least 1.5 items of routes at full capacity
-    (config 4: 229 routes per expert), not at about one item per expert
-    (4,096 rows x E256: 128 routes each), nor below the wide sort."""
+def test_workspace_allows_padded_items_over_the_wide_sort(device):
+    """MoEWorkspace gives the wide sort the aligned capacity whenever it runs
+    the tiled grouped GEMMs over it (the sort then pads or not from the
+    live histogram), not below the wide sort."""
     from drama3_amd import _lib
     from drama3_amd.pipeline import MoEWorkspace, Shape
 
     lib = _lib.load()
-    cases = [((3668, 128, 2048, 768), True), ((4096, 256, 2048, 512), False),
+    cases = [((3668, 128, 2048, 768), True), ((4096, 256, 2048, 512), True),
              ((1000, 128, 1024, 256), False)]
     for dims, aligned in cases:
         ws = MoEWorkspace(Shape(*dims), device)
