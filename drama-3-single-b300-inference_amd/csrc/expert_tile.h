@@ -252,16 +252,20 @@ __device__ __forceinline__ float4 combine4(const float* down, const void* weight
 // before the first FMA; the same rank-order chain, so the same bits.  The
 // route rows are issued first and the weights' dtype is chosen once for all
 // ranks: a dtype branch per rank made each weight load wait before the next
-// rank's loads were issued (one memory round trip per rank).
+// rank's loads were issued (one memory round trip per rank).  The route
+// rows are read exactly once, with non-temporal loads, so they do not evict
+// from the caches what the next launches read again.
 template <int kTopK>
 __device__ __forceinline__ float4 combine4_fixed(const float* down, const void* weights,
                                                  int weights_f32, int token, int hidden,
                                                  int column) {
   float4 y[kTopK];
 #pragma unroll
-  for (int r = 0; r < kTopK; ++r)
-    y[r] = *reinterpret_cast<const float4*>(down + (static_cast<size_t>(token) * kTopK + r) * hidden +
-                                            column);
+  for (int r = 0; r < kTopK; ++r) {
+    const floatx4 v = __builtin_nontemporal_load(
+        reinterpret_cast<const floatx4*>(down + (static_cast<size_t>(token) * kTopK + r) * hidden + column));
+    y[r] = make_float4(v[0], v[1], v[2], v[3]);
+  }
   float w[kTopK];
   const size_t first = static_cast<size_t>(token) * kTopK;
   if (weights_f32) {
