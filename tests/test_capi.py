@@ -88,6 +88,37 @@ def test_capacity_helpers(lib):
     assert lib.d3_sort_wide_scratch_ints(-1, 8, 128) == -1
 
 
+def _histograms(pairs: int, experts: int):
+    """Every expert histogram of `pairs` routes over `experts` experts."""
+    if experts == 1:
+        yield (pairs,)
+        return
+    for first in range(pairs + 1):
+        for rest in _histograms(pairs - first, experts - 1):
+            yield (first,) + rest
+
+
+def test_capacities_bound_every_histogram(lib):
+    """The sorted-row and work-item capacities against brute force over
+    every histogram of small batches: d3_max_sorted_rows and d3_max_items
+    are the largest padded row count and item count any histogram needs
+    (tight), d3_max_items_aligned bounds the items with each odd run padded
+    by one empty item (the wide sort's aligned layout)."""
+    for experts in (1, 2, 3, 4):
+        for pairs in range(0, 11):
+            hists = list(_histograms(pairs, experts))
+            for tile in (1, 2, 3, 4, 16):
+                need = max(sum(-(-c // tile) * tile for c in h) for h in hists)
+                assert lib.d3_max_sorted_rows(pairs, experts, tile) >= need
+            for item_rows in (1, 2, 3, 4, 16):
+                items = [[-(-c // item_rows) for c in h] for h in hists]
+                plain = max(sum(n) for n in items)
+                aligned = max(sum(k + (k & 1) for k in n) for n in items)
+                assert lib.d3_max_items(pairs, experts, item_rows) == plain
+                assert lib.d3_max_items_aligned(pairs, experts, item_rows) >= aligned
+    assert lib.d3_max_items(-1, 4, 16) == -1 and lib.d3_max_items_aligned(4, 0, 16) == -1
+
+
 def test_contract_violations_raise_value_error(lib):
     from drama3_amd import _lib
 
